@@ -1,0 +1,452 @@
+// C ABI of fp8lin: argument validation (the reference's TORCH_CHECK
+// preconditions turned into status codes), kernel dispatch and the
+// Engine::linear decision table.  No allocation, no host synchronisation.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <mutex>
+#include <string>
+
+#include "../../include/fp8lin.h"
+#include "internal.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Failure {
+    int code;
+    std::string msg;
+};
+
+[[noreturn]] void fail(int code, const std::string& msg) { throw Failure{code, msg}; }
+
+void require(bool ok, int code, const char* msg) {
+    if (!ok) fail(code, msg);
+}
+
+void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) fail(FP8LIN_ERR_LAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <class F>
+int guarded(F&& body) {
+    try {
+        body();
+        g_last_error.clear();
+        return FP8LIN_OK;
+    } catch (const Failure& f) {
+        g_last_error = f.msg;
+        return f.code;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return FP8LIN_ERR_LAUNCH;
+    } catch (...) {
+        g_last_error = "unknown failure";
+        return FP8LIN_ERR_LAUNCH;
+    }
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_device_mutex;
+int g_device_state[kMaxDevices];  // 0 unknown, 1 gfx950, -1 other
+
+void ensure_device() {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) fail(FP8LIN_ERR_DEVICE, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    require(dev >= 0 && dev < kMaxDevices, FP8LIN_ERR_DEVICE, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_device_mutex);
+    if (g_device_state[dev] == 0) {
+        hipDeviceProp_t prop;
+        check_hip(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
+        g_device_state[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    }
+    require(g_device_state[dev] == 1, FP8LIN_ERR_DEVICE,
+            "fp8lin kernels are built for gfx950 (MI355X) only");
+}
+
+hipStream_t as_stream(fp8lin_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+constexpr int64_t kMaxDim = (int64_t)1 << 31;
+
+void check_dims(int64_t M, int64_t N, int64_t K) {
+    require(M > 0 && N > 0 && K > 0, FP8LIN_ERR_SHAPE, "Empty GEMM: M, N and K must be positive");
+    require(M < kMaxDim && N < kMaxDim && K < kMaxDim, FP8LIN_ERR_SHAPE,
+            "dimension exceeds 2^31-1");
+}
+
+// src/optimized.cu:64: scales are [N] or [N, ceil(K/128)].
+void check_scales(const float* scales, int64_t scale_cols, int64_t K) {
+    require(scales != nullptr, FP8LIN_ERR_ARGUMENT, "Invalid FP8 scales: null pointer");
+    require(scale_cols == 1 || scale_cols == ceil_div(K, 128), FP8LIN_ERR_ARGUMENT,
+            "Invalid FP8 scales: scale_cols must be 1 or ceil(K/128)");
+}
+
+void linear_impl(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S,
+                 uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+    if (M <= 8) {
+        const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
+        check_hip(fp8lin::launch_gemv(x, codes, true, scales, (int)S, y, ldy, (int)M, (int)N, (int)K,
+                                      wide, stream),
+                  "fp8 gemv launch");
+    } else {
+        check_hip(fp8lin::launch_gemm(x, codes, scales, (int)S, y, ldy, (int)M, (int)N, (int)K,
+                                      false, stream),
+                  "fp8 gemm launch");
+    }
+}
+
+void gemm_bf16_impl(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t ldy, int64_t M,
+                    int64_t N, int64_t K, hipStream_t stream) {
+    if (M <= 8) {
+        const bool wide = K % 16 == 0 && aligned16(x) && aligned16(w);
+        check_hip(fp8lin::launch_gemv(x, w, false, nullptr, 1, y, ldy, (int)M, (int)N, (int)K, wide,
+                                      stream),
+                  "bf16 gemv launch");
+    } else {
+        check_hip(fp8lin::launch_gemm(x, w, nullptr, 1, y, ldy, (int)M, (int)N, (int)K, false,
+                                      stream),
+                  "bf16 gemm launch");
+    }
+}
+
+size_t tensor_small_ws(int64_t M, int64_t N, int split) {
+    return split > 1 ? (size_t)split * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+void tensor_small_impl(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K, int split, void* ws,
+                       size_t ws_bytes, hipStream_t stream) {
+    // src/fp8_tensor.cu:54-59
+    require(x && codes && scales && y, FP8LIN_ERR_ARGUMENT, "Invalid FP8 W8A16 inputs: null pointer");
+    require(M >= 2 && M <= 8 && N > 0 && K > 0 && K % 128 == 0 && N < kMaxDim && K < kMaxDim,
+            FP8LIN_ERR_SHAPE, "Invalid FP8 W8A16 geometry: need 2 <= M <= 8, N > 0, K % 128 == 0");
+    require(split == 1 || split == 4, FP8LIN_ERR_ARGUMENT, "Invalid FP8 W8A16 split: must be 1 or 4");
+    require(aligned16(x) && aligned16(codes), FP8LIN_ERR_UNSUPPORTED,
+            "FP8 W8A16 matrix-core path needs 16-byte aligned x and codes");
+    const size_t need = tensor_small_ws(M, N, split);
+    require(need == 0 || (ws != nullptr && ws_bytes >= need && aligned16(ws)), FP8LIN_ERR_WORKSPACE,
+            "FP8 W8A16 split-K workspace missing, too small or unaligned");
+    ensure_device();
+    check_hip(fp8lin::launch_small_m(x, codes, scales, y, ldy, (int)M, (int)N, (int)K, split,
+                                     static_cast<float*>(ws), stream),
+              "fp8 small-M launch");
+}
+
+void shared_impl(const uint16_t* x, const void* weight, const float* scales, int64_t S, uint16_t* y,
+                 int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+    // src/deep_kernels.cu:135-146
+    require(x && weight && y, FP8LIN_ERR_ARGUMENT, "Invalid shared GEMV inputs: null pointer");
+    require(M >= 1 && M <= 8 && N > 0 && K > 0 && N < kMaxDim && K < kMaxDim, FP8LIN_ERR_SHAPE,
+            "Shared GEMV requires 1..8 rows and N, K > 0");
+    if (scales) check_scales(scales, S, K);
+    ensure_device();
+    const bool wide = K % 16 == 0 && aligned16(x) && aligned16(weight);
+    check_hip(fp8lin::launch_gemv(x, weight, scales != nullptr, scales, scales ? (int)S : 1, y, ldy,
+                                  (int)M, (int)N, (int)K, wide, stream),
+              "shared gemv launch");
+}
+
+constexpr int64_t kSlabRows = 2048;  // src/engine.cpp:229
+
+size_t dequant_gemm_ws(int64_t N, int64_t K) {
+    const int64_t rows = N < kSlabRows ? N : kSlabRows;
+    return (size_t)rows * (size_t)K * 2;
+}
+
+bool tensor_small_eligible(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t rows) {
+    return (o.fp8_tensor_small || o.tilelang_fp8) && rows >= 2 && rows <= 8 && w.scales &&
+           w.K % 128 == 0 && w.scale_cols == w.K / 128 && (!o.tilelang_fp8 || w.N % 16 == 0);
+}
+
+size_t engine_ws(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t rows) {
+    if (tensor_small_eligible(o, w, rows)) return tensor_small_ws(rows, w.N, o.fp8_tensor_split);
+    if (o.multi_token_gemv && rows > 1 && rows <= 8) return 0;
+    if (w.cached_bf16 && rows > 1) return 0;
+    if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) return 0;
+    if (w.scales) return dequant_gemm_ws(w.N, w.K);
+    return 0;
+}
+
+// The branch Engine::linear takes (src/engine.cpp:206-237), without running it.
+int engine_path(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t rows) {
+    if (tensor_small_eligible(o, w, rows)) return FP8LIN_PATH_TENSOR_SMALL;
+    if (o.multi_token_gemv && rows > 1 && rows <= 8) return FP8LIN_PATH_SHARED_GEMV;
+    if (w.cached_bf16 && rows > 1) return FP8LIN_PATH_CACHED_BF16;
+    if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8))
+        return rows <= 8 ? FP8LIN_PATH_FP8_GEMV : FP8LIN_PATH_FP8_GEMM;
+    if (w.scales) return FP8LIN_PATH_DEQUANT_GEMM;
+    return FP8LIN_PATH_BF16;
+}
+
+void validate_engine(const fp8lin_linear_options& o, const fp8lin_weight& w, const uint16_t* x,
+                     int64_t rows, const uint16_t* y, int64_t ldy) {
+    require(x && y && w.data, FP8LIN_ERR_ARGUMENT, "Engine linear: null pointer");
+    check_dims(rows, w.N, w.K);
+    require(ldy >= w.N, FP8LIN_ERR_SHAPE, "Engine linear: ldy < N");
+    if (w.scales) check_scales(w.scales, w.scale_cols, w.K);
+    require(o.fp8_tensor_split == 1 || o.fp8_tensor_split == 4, FP8LIN_ERR_ARGUMENT,
+            "fp8_tensor_split must be 1 or 4");
+}
+
+int engine_impl(const fp8lin_linear_options& o, const fp8lin_weight& w, const uint16_t* x,
+                int64_t rows, uint16_t* y, int64_t ldy, void* ws, size_t ws_bytes,
+                hipStream_t stream) {
+    validate_engine(o, w, x, rows, y, ldy);
+    const auto* codes = static_cast<const uint8_t*>(w.data);
+    // src/engine.cpp:206-213
+    if (tensor_small_eligible(o, w, rows)) {
+        tensor_small_impl(x, codes, w.scales, y, ldy, rows, w.N, w.K, o.fp8_tensor_split, ws,
+                          ws_bytes, stream);
+        return FP8LIN_PATH_TENSOR_SMALL;
+    }
+    // :214-219
+    if (o.multi_token_gemv && rows > 1 && rows <= 8) {
+        const bool use_cached = w.cached_bf16 && !(o.shared_gemv_fp8 && w.scales);
+        if (use_cached)
+            shared_impl(x, w.cached_bf16, nullptr, 1, y, ldy, rows, w.N, w.K, stream);
+        else
+            shared_impl(x, w.data, w.scales, w.scale_cols, y, ldy, rows, w.N, w.K, stream);
+        return FP8LIN_PATH_SHARED_GEMV;
+    }
+    // :220-221
+    if (w.cached_bf16 && rows > 1) {
+        gemm_bf16_impl(x, w.cached_bf16, y, ldy, rows, w.N, w.K, stream);
+        return FP8LIN_PATH_CACHED_BF16;
+    }
+    // :222-224
+    if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) {
+        linear_impl(x, codes, w.scales, w.scale_cols, y, ldy, rows, w.N, w.K, stream);
+        return rows <= 8 ? FP8LIN_PATH_FP8_GEMV : FP8LIN_PATH_FP8_GEMM;
+    }
+    // :225-233, 2048-row BF16 slabs, each GEMM writing its column slice of y.
+    if (w.scales) {
+        const size_t need = dequant_gemm_ws(w.N, w.K);
+        require(ws != nullptr && ws_bytes >= need && aligned16(ws), FP8LIN_ERR_WORKSPACE,
+                "dequant-then-GEMM slab workspace missing, too small or unaligned");
+        auto* slab = static_cast<uint16_t*>(ws);
+        for (int64_t begin = 0; begin < w.N; begin += kSlabRows) {
+            const int64_t count = w.N - begin < kSlabRows ? w.N - begin : kSlabRows;
+            const float* s = w.scales + begin * w.scale_cols;
+            check_hip(fp8lin::launch_dequant(codes + begin * w.K, s, w.scale_cols, slab, w.K, count,
+                                             w.K, stream),
+                      "dequant launch");
+            gemm_bf16_impl(x, slab, y + begin, ldy, rows, count, w.K, stream);
+        }
+        return FP8LIN_PATH_DEQUANT_GEMM;
+    }
+    // :234-237
+    gemm_bf16_impl(x, static_cast<const uint16_t*>(w.data), y, ldy, rows, w.N, w.K, stream);
+    return FP8LIN_PATH_BF16;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fp8lin_version(void) { return FP8LIN_VERSION; }
+
+const char* fp8lin_last_error(void) { return g_last_error.c_str(); }
+
+int fp8lin_init(void) {
+    return guarded([&] { ensure_device(); });
+}
+
+int fp8lin_decode(const uint8_t* codes, const float* scales, int64_t scale_cols, uint16_t* y,
+                  int64_t rows, int64_t cols, fp8lin_stream_t stream) {
+    return guarded([&] {
+        // src/kernels.cu:18-19
+        require(rows >= 0 && cols >= 0, FP8LIN_ERR_SHAPE, "FP8 codes must be a [rows, cols] matrix");
+        if (rows == 0 || cols == 0) return;
+        require(codes && y, FP8LIN_ERR_ARGUMENT, "fp8_decode: null pointer");
+        check_scales(scales, scale_cols, cols);
+        ensure_device();
+        check_hip(fp8lin::launch_dequant(codes, scales, scale_cols, y, cols, rows, cols,
+                                         as_stream(stream)),
+                  "dequant launch");
+    });
+}
+
+int fp8lin_linear_ld(const uint16_t* x, const uint8_t* codes, const float* scales,
+                     int64_t scale_cols, uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                     int vector_gemv, fp8lin_stream_t stream) {
+    (void)vector_gemv;  // wide and byte loads give identical bits; alignment decides
+    return guarded([&] {
+        // src/optimized.cu:62-65
+        require(x && codes && y, FP8LIN_ERR_ARGUMENT, "FP8 linear: null pointer");
+        check_dims(M, N, K);
+        check_scales(scales, scale_cols, K);
+        require(ldy >= N, FP8LIN_ERR_SHAPE, "FP8 linear: ldy < N");
+        ensure_device();
+        linear_impl(x, codes, scales, scale_cols, y, ldy, M, N, K, as_stream(stream));
+    });
+}
+
+int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t scale_cols,
+                  uint16_t* y, int64_t M, int64_t N, int64_t K, int vector_gemv,
+                  fp8lin_stream_t stream) {
+    return fp8lin_linear_ld(x, codes, scales, scale_cols, y, N, M, N, K, vector_gemv, stream);
+}
+
+int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* scales,
+                         int64_t scale_cols, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                         fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(x && codes && y, FP8LIN_ERR_ARGUMENT, "FP8 linear+SwiGLU: null pointer");
+        check_dims(M, N, K);
+        require(N % 2 == 0, FP8LIN_ERR_SHAPE, "Invalid SwiGLU input: N must be even");
+        check_scales(scales, scale_cols, K);
+        ensure_device();
+        check_hip(fp8lin::launch_gemm(x, codes, scales, (int)scale_cols, y, N / 2, (int)M, (int)N,
+                                      (int)K, true, as_stream(stream)),
+                  "fp8 gemm+swiglu launch");
+    });
+}
+
+int fp8lin_swiglu(const uint16_t* gate_up, uint16_t* y, int64_t M, int64_t D,
+                  fp8lin_stream_t stream) {
+    return guarded([&] {
+        // src/optimized.cu:74
+        require(M >= 0 && D >= 0, FP8LIN_ERR_SHAPE, "Invalid SwiGLU input shape");
+        if (M == 0 || D == 0) return;
+        require(gate_up && y, FP8LIN_ERR_ARGUMENT, "SwiGLU: null pointer");
+        ensure_device();
+        check_hip(fp8lin::launch_swiglu(gate_up, y, M, D, as_stream(stream)), "swiglu launch");
+    });
+}
+
+int fp8lin_linear_shared(const uint16_t* x, const void* weight, const float* scales,
+                         int64_t scale_cols, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                         fp8lin_stream_t stream) {
+    return guarded([&] {
+        shared_impl(x, weight, scales, scale_cols, y, N, M, N, K, as_stream(stream));
+    });
+}
+
+size_t fp8lin_tensor_small_workspace_bytes(int64_t M, int64_t N, int split) {
+    if (M <= 0 || N <= 0) return 0;
+    return tensor_small_ws(M, N, split);
+}
+
+int fp8lin_tensor_small(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                        int64_t M, int64_t N, int64_t K, int split, void* workspace,
+                        size_t workspace_bytes, fp8lin_stream_t stream) {
+    return guarded([&] {
+        tensor_small_impl(x, codes, scales, y, N, M, N, K, split, workspace, workspace_bytes,
+                          as_stream(stream));
+    });
+}
+
+int fp8lin_gemm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t ldy, int64_t M,
+                     int64_t N, int64_t K, fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(x && w && y, FP8LIN_ERR_ARGUMENT, "BF16 GEMM: null pointer");
+        check_dims(M, N, K);
+        require(ldy >= N, FP8LIN_ERR_SHAPE, "BF16 GEMM: ldy < N");
+        ensure_device();
+        gemm_bf16_impl(x, w, y, ldy, M, N, K, as_stream(stream));
+    });
+}
+
+size_t fp8lin_engine_linear_workspace_bytes(const fp8lin_linear_options* options,
+                                            const fp8lin_weight* weight, int64_t rows) {
+    if (!options || !weight || rows <= 0) return 0;
+    return engine_ws(*options, *weight, rows);
+}
+
+int fp8lin_engine_linear_path(const fp8lin_linear_options* options, const fp8lin_weight* weight,
+                              int64_t rows) {
+    if (!options || !weight || rows <= 0) return 0;
+    return engine_path(*options, *weight, rows);
+}
+
+int fp8lin_engine_linear(const fp8lin_linear_options* options, const fp8lin_weight* weight,
+                         const uint16_t* x, int64_t rows, uint16_t* y, int64_t ldy, void* workspace,
+                         size_t workspace_bytes, int* path_out, fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(options && weight, FP8LIN_ERR_ARGUMENT, "Engine linear: null options or weight");
+        validate_engine(*options, *weight, x, rows, y, ldy);
+        ensure_device();
+        const int path = engine_impl(*options, *weight, x, rows, y, ldy, workspace, workspace_bytes,
+                                     as_stream(stream));
+        if (path_out) *path_out = path;
+    });
+}
+
+int fp8lin_engine_linear_groups(const fp8lin_linear_options* options, const fp8lin_weight* groups,
+                                int ngroups, const uint16_t* x, int64_t rows, uint16_t* y,
+                                int64_t ldy, void* workspace, size_t workspace_bytes,
+                                fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(options && groups && ngroups > 0, FP8LIN_ERR_ARGUMENT,
+                "Engine linear groups: null options/groups or no group");
+        int64_t total = 0;
+        for (int g = 0; g < ngroups; ++g) {
+            require(groups[g].K == groups[0].K, FP8LIN_ERR_SHAPE,
+                    "Engine linear groups: every group must share K");
+            total += groups[g].N;
+        }
+        require(ldy >= total, FP8LIN_ERR_SHAPE, "Engine linear groups: ldy < sum of group N");
+        for (int g = 0; g < ngroups; ++g) validate_engine(*options, groups[g], x, rows, y, ldy);
+        ensure_device();
+        int64_t offset = 0;
+        for (int g = 0; g < ngroups; ++g) {
+            engine_impl(*options, groups[g], x, rows, y + offset, ldy, workspace, workspace_bytes,
+                        as_stream(stream));
+            offset += groups[g].N;
+        }
+    });
+}
+
+int fp8lin_gen_weights(uint64_t seed, uint32_t tag, int64_t N, int64_t K, float std_dev,
+                       uint8_t* codes, float* scales, fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(codes && scales, FP8LIN_ERR_ARGUMENT, "gen_weights: null pointer");
+        require(N > 0 && K > 0 && N < kMaxDim && K < kMaxDim, FP8LIN_ERR_SHAPE,
+                "gen_weights: N and K must be positive");
+        ensure_device();
+        check_hip(fp8lin::launch_gen_weights(seed, tag, N, K, std_dev, codes, scales,
+                                             as_stream(stream)),
+                  "gen_weights launch");
+    });
+}
+
+int fp8lin_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_t K, uint16_t* x,
+                           fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(x != nullptr, FP8LIN_ERR_ARGUMENT, "gen_activations: null pointer");
+        require(M > 0 && K > 0, FP8LIN_ERR_SHAPE, "gen_activations: M and K must be positive");
+        ensure_device();
+        check_hip(fp8lin::launch_gen_activations(seed, tag, M, K, x, as_stream(stream)),
+                  "gen_activations launch");
+    });
+}
+
+int fp8lin_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n, float* out,
+                      fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(out != nullptr && n > 0, FP8LIN_ERR_ARGUMENT, "gen_normal: bad arguments");
+        ensure_device();
+        check_hip(fp8lin::launch_gen_normal(seed, tag, first, n, out, as_stream(stream)),
+                  "gen_normal launch");
+    });
+}
+
+int fp8lin_stream_read(const void* src, size_t bytes, float* sink, fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(src && sink && bytes >= 16, FP8LIN_ERR_ARGUMENT, "stream_read: bad arguments");
+        require(aligned16(src), FP8LIN_ERR_ARGUMENT, "stream_read: source must be 16-byte aligned");
+        ensure_device();
+        check_hip(fp8lin::launch_stream_read(src, bytes, sink, as_stream(stream)),
+                  "stream_read launch");
+    });
+}
+
+}  // extern "C"

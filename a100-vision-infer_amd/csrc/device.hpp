@@ -1,0 +1,94 @@
+// Device-side helpers shared by the fp8lin kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fp8lin {
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// Two E4M3FN bytes of `word` (bytes 0,1 when hi == false, bytes 2,3 when
+// hi == true) to two exact floats.  gfx950's v_cvt_pk_f32_fp8 uses the OCP
+// E4M3FN encoding: bias 7, subnormals m*2^-9, 0x7f/0xff NaN -- the decode of
+// include/avi/fp8_codec.cuh:5-10 (checked over all 256 codes by the tests).
+template <bool HI>
+__device__ __forceinline__ f32x2 fp8x2_to_f32(uint32_t word) {
+    return __builtin_amdgcn_cvt_pk_f32_fp8(word, HI);
+}
+
+// Two floats to packed BF16 with round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(f32x2 v) {
+    bf16x2 p = __builtin_convertvector(v, bf16x2);
+    return __builtin_bit_cast(uint32_t, p);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float v) {
+    __bf16 b = (__bf16)v;
+    return __builtin_bit_cast(uint16_t, b);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+    return __builtin_bit_cast(float, bits16 << 16);
+}
+
+// Four E4M3FN codes (one dword) times `s`, rounded to BF16 at the reference's
+// rounding point bf16(decode(c) * s) (src/optimized.cu:22), as two packed
+// BF16 pairs: out0 = (c0, c1), out1 = (c2, c3).
+__device__ __forceinline__ void dequant4(uint32_t codes, float s, uint32_t& out0, uint32_t& out1) {
+    f32x2 lo = fp8x2_to_f32<false>(codes);
+    f32x2 hi = fp8x2_to_f32<true>(codes);
+    lo.x *= s;
+    lo.y *= s;
+    hi.x *= s;
+    hi.y *= s;
+    out0 = pack_bf16x2(lo);
+    out1 = pack_bf16x2(hi);
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi over packed BF16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), acc, false);
+}
+
+// Butterfly sum over the 64 lanes of a wave; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+    return v;
+}
+
+__device__ __forceinline__ u32x4 load_u32x4(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Non-temporal 128-bit load for data that is read exactly once (weights).
+__device__ __forceinline__ u32x4 load_u32x4_stream(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+}  // namespace fp8lin
+
+namespace fp8lin {
+
+// SwiGLU of one (gate, up) pair of FP32 GEMM results, with the reference's
+// rounding points (src/optimized.cu:73): both inputs are first rounded to BF16
+// (they are BF16 tensors in the reference), g = bf16(a / (1 + exp(-a))),
+// y = bf16(g * u).  Shared by the standalone kernel and the GEMM epilogues so
+// the fused and unfused paths agree bit for bit.
+__device__ __forceinline__ uint16_t swiglu_bf16_bits(uint16_t a_bits, uint16_t u_bits) {
+    const float a = bf16_bits_to_f32(a_bits);
+    const float u = bf16_bits_to_f32(u_bits);
+    const float g = bf16_bits_to_f32(f32_to_bf16_bits(a / (1.0f + expf(-a))));
+    return f32_to_bf16_bits(g * u);
+}
+
+}  // namespace fp8lin

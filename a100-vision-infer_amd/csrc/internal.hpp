@@ -1,0 +1,42 @@
+// Host-side launchers shared between the kernel files and the C ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fp8lin {
+
+// Decode GEMV, 1 <= M <= 8 (gemv.hip).  `w` is E4M3FN codes when fp8, else
+// BF16.  `wide` selects 128-bit loads (caller checked alignment and K % 16).
+hipError_t launch_gemv(const uint16_t* x, const void* w, bool fp8, const float* scales, int S,
+                       uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
+                       hipStream_t stream);
+
+// Small-M matrix-core kernel, 1 <= M <= 16, K % 128 == 0, block scales
+// (small_m.hip).  split == 1 writes BF16 y; split > 1 writes FP32 partials
+// [split, M, N] and then reduces them in order into y.
+hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales,
+                          uint16_t* y, int64_t ldy, int M, int N, int K, int split,
+                          float* partial, hipStream_t stream);
+
+// MFMA GEMM (gemm.hip).  B is E4M3FN codes (scales != nullptr, dequantized
+// to BF16 in LDS) or BF16 (scales == nullptr).  When swiglu, N is the number
+// of weight rows (gate rows [0,N/2), up rows [N/2,N)) and y is [M, N/2].
+hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, int S,
+                       uint16_t* y, int64_t ldy, int M, int N, int K, bool swiglu,
+                       hipStream_t stream);
+
+// Elementwise kernels (elementwise.hip).
+hipError_t launch_dequant(const uint8_t* codes, const float* scales, int64_t S, uint16_t* y,
+                          int64_t ldy, int64_t rows, int64_t cols, hipStream_t stream);
+hipError_t launch_swiglu(const uint16_t* in, uint16_t* y, int64_t M, int64_t D,
+                         hipStream_t stream);
+hipError_t launch_gen_weights(uint64_t seed, uint32_t tag, int64_t N, int64_t K, float std_dev,
+                              uint8_t* codes, float* scales, hipStream_t stream);
+hipError_t launch_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_t K,
+                                  uint16_t* x, hipStream_t stream);
+hipError_t launch_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n,
+                             float* out, hipStream_t stream);
+hipError_t launch_stream_read(const void* src, size_t bytes, float* sink, hipStream_t stream);
+
+}  // namespace fp8lin

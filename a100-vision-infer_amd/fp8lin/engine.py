@@ -1,0 +1,150 @@
+"""Host mirror of the reference engine's linear path: the name-keyed weight
+store, load-time fusion of projections, the bounded decoded-weight cache and
+the `Engine::linear` dispatch (laoyin/a100-vision-infer src/engine.cpp:94-177,
+196-242).
+
+The decision table itself runs in the native library
+(`fp8lin_engine_linear`, include/fp8lin.h); this class keeps the weights as
+device tensors and hands them over as `fp8lin_weight` records.  The
+tensor-parallel reduce and the bias add that follow `linear` in the reference
+(src/engine.cpp:239-240) are outside this path.
+"""
+import ctypes
+
+import torch
+
+from ._lib import ERR_ARGUMENT, Fp8linError, LinearOptions, Weight, check, lib
+from .ops import fp8_decode
+
+
+class StoredWeight:
+    """`struct Weight { Tensor data, scale; }` (include/avi/engine.h:15)."""
+
+    def __init__(self, data, scale=None):
+        self.data = data
+        self.scale = scale
+
+    def compatible(self, other):
+        # src/engine.cpp:154-158
+        if self.data.dtype != other.data.dtype or (self.scale is None) != (other.scale is None):
+            return False
+        if self.scale is None:
+            return True
+        return self.scale.dim() == other.scale.dim() and (
+            self.scale.dim() == 1 or self.scale.size(1) == other.scale.size(1))
+
+
+class LinearEngine:
+    def __init__(self, options=None, weight_cache_bytes=0):
+        self.options = options or LinearOptions()
+        self.weight_cache_bytes = int(weight_cache_bytes)
+        self.weights = {}
+        self.mixed_projections = {}
+        self.decoded_weights = {}
+        self.decoded_bytes = 0
+        self._workspace = None
+
+    # -- loading -------------------------------------------------------------
+    def add(self, name, data, scale=None):
+        """Register `name` (e.g. "...mlp.gate_proj.weight") with device
+        tensors: uint8 codes [N,K] + float32 scales, or BF16 [N,K]."""
+        if data.dim() != 2 or not data.is_contiguous():
+            raise Fp8linError(ERR_ARGUMENT, f"Invalid matrix {name}")
+        self.weights[name] = StoredWeight(data, scale)
+
+    def fuse_weights(self, dest, sources):
+        """Row-concatenate compatible projections (src/engine.cpp:147-177):
+        `dest.weight = cat(sources)`; incompatible runs (e.g. FP8 qkv+z next
+        to BF16 b+a) become groups whose outputs are concatenated."""
+        ws = [self.weights[s + ".weight"] for s in sources]
+        scaled = [w for w in ws if w.scale is not None]
+        mixed = scaled and (len(scaled) != len(ws) or any(
+            w.scale.dim() != scaled[0].scale.dim() or
+            (w.scale.dim() == 2 and w.scale.size(1) != scaled[0].scale.size(1)) for w in scaled))
+        if mixed:
+            groups = []
+            for s in sources:
+                if not groups or not self.weights[groups[-1][-1] + ".weight"].compatible(
+                        self.weights[s + ".weight"]):
+                    groups.append([])
+                groups[-1].append(s)
+            children = []
+            for i, g in enumerate(groups):
+                if len(g) == 1:
+                    children.append(g[0])
+                    continue
+                child = f"{dest}.group{i}"
+                self.fuse_weights(child, g)
+                children.append(child)
+            self.mixed_projections[dest] = children
+            return
+        data = torch.cat([w.data for w in ws], 0)
+        scale = torch.cat([w.scale for w in ws], 0) if scaled else None
+        self.weights[dest + ".weight"] = StoredWeight(data, scale)
+        for s in sources:
+            del self.weights[s + ".weight"]
+
+    def build_cache(self, names=None):
+        """Bounded decoded-BF16 cache, sorted by name (src/engine.cpp:127-143)."""
+        names = sorted(names if names is not None else
+                       [n for n, w in self.weights.items() if w.scale is not None])
+        for name in names:
+            w = self.weights[name]
+            nbytes = w.data.numel() * 2
+            if nbytes <= self.weight_cache_bytes - self.decoded_bytes:
+                self.decoded_weights[name] = fp8_decode(w.data, w.scale)
+                self.decoded_bytes += nbytes
+
+    # -- dispatch --------------------------------------------------------------
+    def _record(self, name):
+        w = self.weights.get(name + ".weight")
+        if w is None:
+            raise Fp8linError(ERR_ARGUMENT, f"Missing linear {name}")
+        cached = self.decoded_weights.get(name + ".weight")
+        rec = Weight()
+        rec.data = w.data.data_ptr()
+        rec.scales = w.scale.data_ptr() if w.scale is not None else None
+        rec.scale_cols = (1 if w.scale.dim() == 1 else w.scale.size(1)) if w.scale is not None else 1
+        rec.cached_bf16 = cached.data_ptr() if cached is not None else None
+        rec.N, rec.K = w.data.size(0), w.data.size(1)
+        return rec
+
+    def _ws(self, nbytes, device):
+        if nbytes == 0:
+            return None
+        if self._workspace is None or self._workspace.numel() < nbytes:
+            self._workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        return self._workspace
+
+    def linear(self, x, name, return_path=False):
+        """`Engine::linear(x, name)` without reduce/bias (src/engine.cpp:196-242)."""
+        rows = x.numel() // x.size(-1)
+        x2 = x.reshape(rows, x.size(-1)).contiguous()
+        stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        opt = self.options
+        if name in self.mixed_projections:
+            recs = [self._record(c) for c in self.mixed_projections[name]]
+            total = sum(r.N for r in recs)
+            y = torch.empty((rows, total), dtype=torch.bfloat16, device=x.device)
+            need = max(lib().fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(r),
+                                                                  rows) for r in recs)
+            ws = self._ws(need, x.device)
+            arr = (Weight * len(recs))(*recs)
+            check(lib().fp8lin_engine_linear_groups(
+                ctypes.byref(opt), arr, len(recs), ctypes.c_void_p(x2.data_ptr()), rows,
+                ctypes.c_void_p(y.data_ptr()), total,
+                ctypes.c_void_p(ws.data_ptr()) if ws is not None else None, need, stream))
+            out = y.reshape(*x.shape[:-1], total)
+            return (out, None) if return_path else out
+        rec = self._record(name)
+        y = torch.empty((rows, rec.N), dtype=torch.bfloat16, device=x.device)
+        need = lib().fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(rec), rows)
+        ws = self._ws(need, x.device)
+        path = ctypes.c_int(0)
+        check(lib().fp8lin_engine_linear(
+            ctypes.byref(opt), ctypes.byref(rec), ctypes.c_void_p(x2.data_ptr()), rows,
+            ctypes.c_void_p(y.data_ptr()), rec.N,
+            ctypes.c_void_p(ws.data_ptr()) if ws is not None else None, need,
+            ctypes.byref(path), stream))
+        out = y.reshape(*x.shape[:-1], rec.N)
+        return (out, path.value) if return_path else out

@@ -1,0 +1,207 @@
+"""Tensor-level host mirror of the reference's linear-path operators.
+
+Same names, argument meaning and error behaviour as the reference's ATen
+functions (laoyin/a100-vision-infer include/avi/ops.h:10,11,18,20 and
+include/avi/engine.h:13): inputs are device tensors, the output is allocated
+on the input's device, work is enqueued on torch's current stream, and a
+violated precondition raises (Fp8linError, a RuntimeError, where the
+reference's TORCH_CHECK raises c10::Error).  All arithmetic runs in the HIP
+library through the C ABI; torch only provides memory and the stream.
+"""
+import ctypes
+
+import torch
+
+from ._lib import (ERR_ARGUMENT, ERR_SHAPE, Fp8linError, LinearOptions, Weight, check, lib)
+
+
+def _fail(code, msg):
+    raise Fp8linError(code, msg)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _is_dev(t):
+    return isinstance(t, torch.Tensor) and t.is_cuda
+
+
+def _scale_cols(scales, codes_rows, k, what="Invalid FP8 scales"):
+    # src/optimized.cu:64
+    ok = (_is_dev(scales) and scales.dtype == torch.float32 and scales.is_contiguous() and
+          ((scales.dim() == 1 and scales.numel() == codes_rows) or
+           (scales.dim() == 2 and scales.size(0) == codes_rows and scales.size(1) == (k + 127) // 128)))
+    if not ok:
+        _fail(ERR_ARGUMENT, what)
+    return 1 if scales.dim() == 1 else scales.size(1)
+
+
+def _check_x(x, what):
+    if not (_is_dev(x) and x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous()):
+        _fail(ERR_ARGUMENT, what)
+
+
+def _check_codes(codes, x, what="Invalid FP8 weights"):
+    if not (_is_dev(codes) and codes.device == x.device and codes.dtype == torch.uint8 and
+            codes.dim() == 2 and codes.is_contiguous() and codes.size(1) == x.size(1)):
+        _fail(ERR_ARGUMENT, what)
+
+
+def fp8_decode(codes, scales):
+    """`Tensor fp8_decode(Tensor codes, Tensor scales)` -- src/kernels.cu:17-27."""
+    if not (_is_dev(codes) and codes.dtype == torch.uint8 and codes.dim() == 2 and
+            codes.is_contiguous()):
+        _fail(ERR_ARGUMENT, "FP8 codes must be contiguous CUDA uint8 matrix")
+    sc = _scale_cols(scales, codes.size(0), codes.size(1), "Invalid FP8 row scales")
+    y = torch.empty(codes.shape, dtype=torch.bfloat16, device=codes.device)
+    if codes.numel():
+        check(lib().fp8lin_decode(_ptr(codes), _ptr(scales), sc, _ptr(y), codes.size(0),
+                                  codes.size(1), _stream(codes)))
+    return y
+
+
+def fp8_linear(x, codes, scales, vector_gemv=False):
+    """`at::Tensor fp8_linear(x, codes, scales, bool vector_gemv=false)` --
+    src/optimized.cu:61-70."""
+    _check_x(x, "FP8 linear expects CUDA BF16 [M,K]")
+    _check_codes(codes, x)
+    sc = _scale_cols(scales, codes.size(0), codes.size(1))
+    M, N, K = x.size(0), codes.size(0), codes.size(1)
+    if not (M > 0 and N > 0 and K > 0):
+        _fail(ERR_SHAPE, "Empty GEMM")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    check(lib().fp8lin_linear(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K,
+                              int(bool(vector_gemv)), _stream(x)))
+    return y
+
+
+def linear_swiglu(x, codes, scales):
+    """Fused `fused_swiglu(fp8_linear(x, gate_up))` (src/engine.cpp:415)."""
+    _check_x(x, "FP8 linear expects CUDA BF16 [M,K]")
+    _check_codes(codes, x)
+    sc = _scale_cols(scales, codes.size(0), codes.size(1))
+    M, N, K = x.size(0), codes.size(0), codes.size(1)
+    if not (M > 0 and N > 0 and K > 0) or N % 2:
+        _fail(ERR_SHAPE, "Invalid gate/up geometry")
+    y = torch.empty((M, N // 2), dtype=torch.bfloat16, device=x.device)
+    check(lib().fp8lin_linear_swiglu(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K,
+                                     _stream(x)))
+    return y
+
+
+def fused_swiglu(gate_up):
+    """`at::Tensor fused_swiglu(at::Tensor gate_up)` -- src/optimized.cu:73-74."""
+    if not (_is_dev(gate_up) and gate_up.is_contiguous() and gate_up.dim() == 2 and
+            gate_up.dtype == torch.bfloat16 and gate_up.size(1) % 2 == 0):
+        _fail(ERR_ARGUMENT, "Invalid SwiGLU input")
+    M, D = gate_up.size(0), gate_up.size(1) // 2
+    y = torch.empty((M, D), dtype=torch.bfloat16, device=gate_up.device)
+    check(lib().fp8lin_swiglu(_ptr(gate_up), _ptr(y), M, D, _stream(gate_up)))
+    return y
+
+
+def small_linear_shared(x, weight, scales=None):
+    """`at::Tensor small_linear_shared(x, weight, scales={})` --
+    src/deep_kernels.cu:134-157."""
+    if not (_is_dev(x) and x.dim() == 2 and x.is_contiguous() and x.dtype == torch.bfloat16 and
+            _is_dev(weight) and weight.dim() == 2 and weight.is_contiguous() and
+            weight.device == x.device and x.size(1) == weight.size(1)):
+        _fail(ERR_ARGUMENT, "Invalid shared GEMV inputs")
+    M, N, K = x.size(0), weight.size(0), x.size(1)
+    if not (1 <= M <= 8 and N > 0 and K > 0):
+        _fail(ERR_SHAPE, "Shared GEMV requires 1..8 rows")
+    if scales is not None:
+        if weight.dtype != torch.uint8:
+            _fail(ERR_ARGUMENT, "Invalid shared FP8 scales")
+        sc = _scale_cols(scales, N, K, "Invalid shared FP8 scales")
+    else:
+        if weight.dtype != torch.bfloat16:
+            _fail(ERR_ARGUMENT, "Shared GEMV expects BF16 or FP8 weights")
+        sc = 1
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    check(lib().fp8lin_linear_shared(_ptr(x), _ptr(weight), _ptr(scales), sc, _ptr(y), M, N, K,
+                                     _stream(x)))
+    return y
+
+
+def _tensor_small_checks(x, codes, scales, split, what, n16=False):
+    ok = (_is_dev(x) and x.dtype == torch.bfloat16 and x.dim() == 2 and x.is_contiguous() and
+          _is_dev(codes) and codes.device == x.device and codes.dtype == torch.uint8 and
+          codes.dim() == 2 and codes.is_contiguous() and
+          _is_dev(scales) and scales.device == x.device and scales.dtype == torch.float32 and
+          scales.dim() == 2 and scales.is_contiguous() and
+          2 <= x.size(0) <= 8 and x.size(1) > 0 and x.size(1) == codes.size(1) and
+          x.size(1) % 128 == 0 and codes.size(0) > 0 and scales.size(0) == codes.size(0) and
+          scales.size(1) == x.size(1) // 128 and split in (1, 4) and
+          (not n16 or codes.size(0) % 16 == 0))
+    if not ok:
+        _fail(ERR_ARGUMENT, what)
+
+
+def fp8_tensor_small(x, codes, scales, split=1):
+    """`at::Tensor fp8_tensor_small(x, codes, scales, int split=1)` --
+    src/fp8_tensor.cu:53-71."""
+    _tensor_small_checks(x, codes, scales, split, "Invalid Ampere FP8 W8A16 geometry/dtype")
+    return _run_tensor_small(x, codes, scales, split)
+
+
+def tilelang_fp8_small(x, codes, scales, split):
+    """`at::Tensor tilelang_fp8_small(x, codes, scales, int split)` --
+    src/tilelang.cpp:94-107 (same contract plus N % 16 == 0; served by the
+    same matrix-core kernel)."""
+    _tensor_small_checks(x, codes, scales, split, "Invalid TileLang FP8 W8A16 inputs", n16=True)
+    return _run_tensor_small(x, codes, scales, split)
+
+
+def _run_tensor_small(x, codes, scales, split):
+    M, N, K = x.size(0), codes.size(0), x.size(1)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    nbytes = lib().fp8lin_tensor_small_workspace_bytes(M, N, split)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device) if nbytes else None
+    check(lib().fp8lin_tensor_small(_ptr(x), _ptr(codes), _ptr(scales), _ptr(y), M, N, K, split,
+                                    _ptr(ws), nbytes, _stream(x)))
+    return y
+
+
+def gemm_bf16(x, w, out=None):
+    """BF16 `at::matmul(x, w.t())` (src/engine.cpp:221,236) on the HIP GEMM."""
+    _check_x(x, "BF16 GEMM expects CUDA BF16 [M,K]")
+    if not (_is_dev(w) and w.dtype == torch.bfloat16 and w.dim() == 2 and w.is_contiguous() and
+            w.size(1) == x.size(1)):
+        _fail(ERR_ARGUMENT, "Invalid BF16 weights")
+    M, N, K = x.size(0), w.size(0), x.size(1)
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    check(lib().fp8lin_gemm_bf16(_ptr(x), _ptr(w), _ptr(y), y.stride(0), M, N, K, _stream(x)))
+    return y
+
+
+def gen_weights(n, k, seed=0, tag=1, std=0.02, device="cuda"):
+    """Synthetic block-FP8 weights on the device (codes [n,k] u8, scales
+    [n, ceil(k/128)] f32)."""
+    codes = torch.empty((n, k), dtype=torch.uint8, device=device)
+    scales = torch.empty((n, (k + 127) // 128), dtype=torch.float32, device=device)
+    check(lib().fp8lin_gen_weights(seed, tag, n, k, float(std), _ptr(codes), _ptr(scales),
+                                   _stream(codes)))
+    return codes, scales
+
+
+def gen_activations(m, k, seed=0, tag=2, device="cuda"):
+    x = torch.empty((m, k), dtype=torch.bfloat16, device=device)
+    check(lib().fp8lin_gen_activations(seed, tag, m, k, _ptr(x), _stream(x)))
+    return x
+
+
+def gen_normal(n, seed=0, tag=1, first=0, device="cuda"):
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    check(lib().fp8lin_gen_normal(seed, tag, first, n, _ptr(out), _stream(out)))
+    return out
+
+
+def stream_read(src, sink):
+    check(lib().fp8lin_stream_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink),
+                                   _stream(src)))

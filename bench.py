@@ -1,0 +1,269 @@
+"""fp8lin benchmark: block-FP8 decode GEMV (HBM roofline) and prefill GEMM
+(MFMA roofline) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+
+A step is one decode pass of the one-rank layer chain at M=1 (BASELINE
+config 2): gate/up 17408x5120, down 5120x8704 and QKV-gate 7168x5120, E4M3FN
+weights with 128x128 block scales (seed 0, N(0, 0.02)), BF16 activations
+N(0,1).  Weight sets are rotated so the working set exceeds twice the 256 MB
+Infinity Cache, so the GB/s figures are HBM, not cache.  `value` is the
+algorithmic bytes of the timed steps divided by their wall time on the GPU
+(HIP events bracketing the timed region).  One JSON line is printed last.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "a100-vision-infer_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+METRIC = "FP8 GEMV HBM GB/s (% peak) at M=1; prefill GEMM TFLOP/s (% MFMA peak)"
+SHAPES = [("gate_up", 17408, 5120), ("down", 5120, 8704), ("qkv_gate", 7168, 5120)]
+
+
+def algo_bytes(m, n, k, n_out=None):
+    """N*K codes + 4*N*ceil(K/128) scales + 2*M*K activations + 2*M*N_out output."""
+    n_out = n if n_out is None else n_out
+    return n * k + 4 * n * ((k + 127) // 128) + 2 * m * k + 2 * m * n_out
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--copies", type=int, default=4, help="rotated weight sets (>= 512 MB total)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
+    return p.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "tensor-parallel sharding is described in DESIGN.md but not run", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import fp8lin
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    assert fp8lin.lib().fp8lin_init() == 0, fp8lin.lib().fp8lin_last_error()
+
+    # ---- inputs: seed 0, generated on the device ---------------------------------
+    sets = []
+    for c in range(args.copies):
+        ws = {}
+        for i, (name, n, k) in enumerate(SHAPES):
+            ws[name] = fp8lin.gen_weights(n, k, seed=0, tag=1 + 16 * c + i, device=dev)
+        sets.append(ws)
+    xs = {k: fp8lin.gen_activations(1, k, seed=0, tag=2, device=dev) for k in {5120, 8704}}
+    ys = {name: torch.empty((1, n), dtype=torch.bfloat16, device=dev) for name, n, _ in SHAPES}
+    torch.cuda.synchronize()
+    step_bytes = sum(algo_bytes(1, n, k) for _, n, k in SHAPES)
+    working_set = args.copies * sum(n * k + 4 * n * ((k + 127) // 128) for _, n, k in SHAPES)
+    log(f"working set {working_set / 1e6:.1f} MB over {args.copies} weight copies")
+
+    L = fp8lin.lib()
+    import ctypes
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def gemv(name, ws, y):
+        n, k = {s[0]: (s[1], s[2]) for s in SHAPES}[name]
+        codes, scales = ws[name]
+        rc = L.fp8lin_linear(ctypes.c_void_p(xs[k].data_ptr()), ctypes.c_void_p(codes.data_ptr()),
+                             ctypes.c_void_p(scales.data_ptr()), (k + 127) // 128,
+                             ctypes.c_void_p(y.data_ptr()), 1, n, k, 1, sp)
+        if rc:
+            raise RuntimeError(L.fp8lin_last_error())
+
+    def step(i, ev=None):
+        ws = sets[i % len(sets)]
+        if ev is not None:
+            ev[0].record(stream)
+        gemv("gate_up", ws, ys["gate_up"])
+        if ev is not None:
+            ev[1].record(stream)
+        gemv("down", ws, ys["down"])
+        gemv("qkv_gate", ws, ys["qkv_gate"])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # ---- timed region -------------------------------------------------------------
+    kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for i in range(args.steps):
+        step(i, kev[i])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    ms_per_step = total_ms / args.steps
+    value = step_bytes * args.steps / (total_ms * 1e-3) / 1e9
+    gu_ms = sorted(a.elapsed_time(b) for a, b in kev)
+    gu_avg_ms = sum(gu_ms) / len(gu_ms)
+    gu_bytes = algo_bytes(1, 17408, 5120)
+    gu_gbs = gu_bytes / (gu_avg_ms * 1e-3) / 1e9
+    log(f"decode chain: {ms_per_step * 1e3:.2f} us/step, {value:.1f} GB/s; gate/up GEMV "
+        f"avg {gu_avg_ms * 1e3:.2f} us ({gu_gbs:.1f} GB/s), median {gu_ms[len(gu_ms) // 2] * 1e3:.2f} us")
+
+    extra = {}
+    if not args.quick:
+        extra = secondary(torch, fp8lin, dev, sets, log)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(sets[0], xs, args.cpu_seconds, log)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed-0 Philox N(0,0.02) weights quantized to E4M3FN per 128x128 block; "
+                "BF16 N(0,1) activations)",
+        "config": {
+            "workload": "decode GEMV, M=1, one TP-rank layer chain: gate/up 17408x5120 + "
+                        "down 5120x8704 + QKV-gate 7168x5120 (BASELINE config 2)",
+            "batch_rows": 1,
+            "weight_format": "E4M3FN codes + FP32 128x128 block scales (row-expanded)",
+            "accumulate": "fp32",
+            "bytes_per_step": step_bytes,
+            "working_set_bytes": working_set,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_kernel<1,4,wide,fp8> (gate/up 17408x5120)",
+            "achieved": round(gu_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(gu_avg_ms * 1e3, 3),
+            "algorithmic_bytes_per_launch": gu_bytes,
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def timed(torch, fn, iters, warm=3):
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def secondary(torch, fp8lin, dev, sets, log):
+    extra = {}
+    # per-shape decode GEMV (rotating copies)
+    for name, n, k in SHAPES:
+        x = fp8lin.gen_activations(1, k, seed=0, tag=2, device=dev)
+        i = [0]
+
+        def run():
+            c, s = sets[i[0] % len(sets)][name]
+            i[0] += 1
+            fp8lin.fp8_linear(x, c, s, True)
+        ms = timed(torch, run, 200)
+        gbs = algo_bytes(1, n, k) / (ms * 1e-3) / 1e9
+        extra[f"gemv_m1_{name}_GBs"] = round(gbs, 1)
+        log(f"gemv M=1 {name}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
+    # small M (config 3): GEMV and matrix-core paths on gate/up
+    n, k = 17408, 5120
+    for m in (2, 4, 8):
+        x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
+        for label, fn in [("gemv", lambda c, s: fp8lin.fp8_linear(x, c, s, True)),
+                          ("tensor_s1", lambda c, s: fp8lin.fp8_tensor_small(x, c, s, 1)),
+                          ("tensor_s4", lambda c, s: fp8lin.fp8_tensor_small(x, c, s, 4))]:
+            i = [0]
+
+            def run():
+                c, s = sets[i[0] % len(sets)]["gate_up"]
+                i[0] += 1
+                fn(c, s)
+            ms = timed(torch, run, 100)
+            gbs = algo_bytes(m, n, k) / (ms * 1e-3) / 1e9
+            extra[f"m{m}_gate_up_{label}_GBs"] = round(gbs, 1)
+            log(f"M={m} gate/up {label}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
+    # prefill GEMM with fused SwiGLU (config 4)
+    c, s = sets[0]["gate_up"]
+    for m in (512, 1024, 4096):
+        x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
+        ms = timed(torch, lambda: fp8lin.linear_swiglu(x, c, s), 10 if m == 4096 else 20)
+        tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        extra[f"prefill_swiglu_m{m}_TFLOPs"] = round(tflops, 1)
+        extra[f"prefill_swiglu_m{m}_frac"] = round(tflops / BF16_PEAK_TFLOPS, 4)
+        log(f"prefill M={m} gate/up+SwiGLU: {ms:.3f} ms {tflops:.1f} TFLOP/s "
+            f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of BF16 peak)")
+    # streaming-read ceiling
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4096, dtype=torch.float32, device=dev)
+    ms = timed(torch, lambda: fp8lin.stream_read(buf, sink), 20)
+    extra["stream_read_GBs"] = round(buf.numel() / (ms * 1e-3) / 1e9, 1)
+    log(f"stream read 1 GiB: {extra['stream_read_GBs']} GB/s")
+    return extra
+
+
+def cpu_baseline(ws, xs, seconds, log):
+    """The CPU oracle (C restatement of tests/fp8_tensor_test.cpp:11-22,
+    OpenMP over output rows) on the same step, repeated for ~`seconds`."""
+    import numpy as np
+    from oracle import oracle as O  # test infrastructure: the checker, timed as a baseline
+    host = {name: (c.cpu().numpy(), s.cpu().numpy()) for name, (c, s) in ws.items()}
+    xh = {k: x.view(dtype=__import__("torch").int16).cpu().numpy().view(np.uint16) for k, x in xs.items()}
+    threads = O.max_threads()
+
+    def one():
+        for name, n, k in SHAPES:
+            c, s = host[name]
+            O.linear(xh[k], c, s, threads=threads)
+    one()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 1000:
+            break
+    per = el / reps
+    step_bytes = sum(algo_bytes(1, n, k) for _, n, k in SHAPES)
+    gbs = step_bytes / per / 1e9
+    log(f"cpu oracle: {per * 1e3:.1f} ms/step on {threads} threads ({gbs:.2f} GB/s)")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} full decode steps (3 GEMVs, M=1) in {el:.1f} s; "
+                      f"{per * 1e3:.1f} ms per step; FP64 oracle, OpenMP over output rows"}
+
+
+if __name__ == "__main__":
+    main()

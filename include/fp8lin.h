@@ -1,0 +1,229 @@
+/*
+ * fp8lin -- MI355X (gfx950) block-FP8 linear layers, C ABI.
+ *
+ * E4M3FN weight codes [N,K] (uint8, row-major) with FP32 scales, times BF16
+ * activations [M,K] (row-major), FP32 accumulation, BF16 output [M,N].
+ * Scales are either per row ([N], scale_cols == 1) or 128x128 block scales
+ * expanded along rows ([N, ceil(K/128)], scale_cols == ceil(K/128)); the
+ * weight used for element (n,k) is bf16(decode(code[n,k]) * scale[n, k/128]).
+ *
+ * Conventions for every entry point:
+ *  - all tensors are device pointers owned by the caller; the library never
+ *    allocates or frees them and never synchronises the stream;
+ *  - BF16 data is passed as uint16_t bit patterns;
+ *  - `stream` is a hipStream_t (NULL = the null stream); work is enqueued
+ *    on it and is capturable into a HIP graph;
+ *  - the return value is FP8LIN_OK or one of the FP8LIN_ERR_* codes below;
+ *    fp8lin_last_error() gives a message for the calling thread's last
+ *    failure.  No C++ exception crosses this boundary.
+ *
+ * Each declaration names the reference (laoyin/a100-vision-infer) interface it
+ * replaces.  The reference takes at::Tensor arguments, allocates its outputs
+ * and reports errors with TORCH_CHECK; here the same checks become status
+ * codes and the caller passes the output buffer.
+ */
+#ifndef FP8LIN_H
+#define FP8LIN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FP8LIN_VERSION 100 /* 1.0.0 */
+
+enum fp8lin_status {
+    FP8LIN_OK = 0,
+    FP8LIN_ERR_SHAPE = 1,       /* invalid or inconsistent dimensions */
+    FP8LIN_ERR_ARGUMENT = 2,    /* null pointer, bad scale layout, bad flag value */
+    FP8LIN_ERR_UNSUPPORTED = 3, /* valid request outside this entry point's contract */
+    FP8LIN_ERR_WORKSPACE = 4,   /* workspace missing or smaller than required */
+    FP8LIN_ERR_LAUNCH = 5,      /* HIP runtime or kernel launch failure */
+    FP8LIN_ERR_DEVICE = 6       /* the current device is not a gfx950 GPU */
+};
+
+typedef void* fp8lin_stream_t; /* hipStream_t */
+
+int fp8lin_version(void);
+/* Message for the calling thread's most recent failure ("" if none). */
+const char* fp8lin_last_error(void);
+/* Checks that the current device is gfx950 and loads the kernels.  Optional:
+ * every entry point calls it on first use.  TileLang plugin precedent:
+ * init()/get_last_error() of src/tilelang.cpp:80-82. */
+int fp8lin_init(void);
+
+/* ---------------------------------------------------------------------------
+ * Dequantization: y[r,c] = bf16(decode(codes[r,c]) * scales[r, c/128]).
+ * Replaces `Tensor fp8_decode(Tensor codes, Tensor scales)`
+ * (include/avi/engine.h:13, src/kernels.cu:17-27).  rows == 0 or cols == 0
+ * is a no-op, as in the reference.
+ */
+int fp8lin_decode(const uint8_t* codes, const float* scales, int64_t scale_cols,
+                  uint16_t* y, int64_t rows, int64_t cols, fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * y[M,N] = x[M,K] * W^T.  Replaces
+ * `at::Tensor fp8_linear(at::Tensor x, at::Tensor codes, at::Tensor scales,
+ *                        bool vector_gemv=false)`
+ * (include/avi/ops.h:18, src/optimized.cu:61-70).  M <= 8 runs the decode
+ * GEMV (wide 128-bit loads when vector_gemv is set and K, x and codes are
+ * 16-byte aligned, otherwise byte loads with bit-identical results); M > 8
+ * runs the MFMA GEMM that dequantizes FP8 tiles to BF16 in LDS.
+ * Requires M, N, K > 0 and scale_cols in {1, ceil(K/128)}.
+ */
+int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales,
+                  int64_t scale_cols, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                  int vector_gemv, fp8lin_stream_t stream);
+
+/* Same as fp8lin_linear with an output row stride ldy >= N (elements), so a
+ * caller can write into a column slice of a wider output (the mixed-group
+ * concatenation of src/engine.cpp:199 without a copy). */
+int fp8lin_linear_ld(const uint16_t* x, const uint8_t* codes, const float* scales,
+                     int64_t scale_cols, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
+                     int64_t K, int vector_gemv, fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused gate/up projection + SwiGLU: with G = fp8lin_linear(x, W) of shape
+ * [M, N] (N even, rows [0, N/2) = gate, [N/2, N) = up, the row concatenation
+ * of src/engine.cpp:116,167), y[M, N/2] = fused_swiglu(G) bit for bit.
+ * Replaces the pair linear(gate_up) -> fused_swiglu at src/engine.cpp:415.
+ */
+int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* scales,
+                         int64_t scale_cols, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                         fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * SwiGLU: y[r,j] = bf16(bf16(a/(1+exp(-a))) * u), a = in[r,j], u = in[r,D+j],
+ * in is [M, 2D].  Replaces `at::Tensor fused_swiglu(at::Tensor gate_up)`
+ * (include/avi/ops.h:20, src/optimized.cu:73-74).
+ */
+int fp8lin_swiglu(const uint16_t* gate_up, uint16_t* y, int64_t M, int64_t D,
+                  fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Shared-weight multi-row GEMV, 1 <= M <= 8: every row of x is multiplied
+ * against one pass over the weights.  `scales == NULL` means `weight` is BF16
+ * [N,K] (a decoded-weight cache); otherwise it is E4M3FN codes.  The FP8 and
+ * the BF16-decoded forms give bit-identical outputs.  Replaces
+ * `at::Tensor small_linear_shared(at::Tensor x, at::Tensor weight,
+ *                                 at::Tensor scales={})`
+ * (include/avi/ops.h:11, src/deep_kernels.cu:134-157).
+ */
+int fp8lin_linear_shared(const uint16_t* x, const void* weight, const float* scales,
+                         int64_t scale_cols, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                         fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Small-M matrix-core path, 2 <= M <= 8, K % 128 == 0, block scales
+ * [N, K/128], split in {1, 4}.  split == 4 writes FP32 partial sums of four
+ * K ranges to `workspace` and reduces them in the fixed order
+ * ((p0+p1)+p2)+p3.  Replaces
+ * `at::Tensor fp8_tensor_small(at::Tensor x, at::Tensor codes,
+ *                              at::Tensor scales, int split=1)`
+ * (include/avi/ops.h:10, src/fp8_tensor.cu:53-71); the same contract serves
+ * `tilelang_fp8_small` (include/avi/tilelang.h:11, src/tilelang.cpp:94-107).
+ */
+size_t fp8lin_tensor_small_workspace_bytes(int64_t M, int64_t N, int split);
+int fp8lin_tensor_small(const uint16_t* x, const uint8_t* codes, const float* scales,
+                        uint16_t* y, int64_t M, int64_t N, int64_t K, int split,
+                        void* workspace, size_t workspace_bytes, fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * BF16 GEMM y[M,N] = x[M,K] * W^T with BF16 weights W [N,K] (the decoded-weight
+ * cache and unquantized weights, `at::matmul(x, w.t())` at
+ * src/engine.cpp:221,236).  MFMA kernel, FP32 accumulation, BF16 output.
+ */
+int fp8lin_gemm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t ldy,
+                     int64_t M, int64_t N, int64_t K, fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Engine::linear dispatch (src/engine.cpp:196-242) over one weight, with the
+ * EngineOptions linear-path flags (include/avi/engine.h:16).  The decision
+ * order is the reference's: tensor-small (rows 2..8, K%128==0, block scales;
+ * tilelang_fp8 additionally N%16==0) -> multi-token shared GEMV (rows 2..8)
+ * -> cached BF16 GEMM (rows > 1) -> fp8_linear (optimized, unless
+ * cublas_prefill and rows > 8) -> dequant-then-GEMM in 2048-row slabs
+ * (src/engine.cpp:225-233) -> BF16 GEMM for unquantized weights.
+ * The bias add and the tensor-parallel reduce that follow in the reference
+ * are outside this call.
+ */
+typedef struct fp8lin_weight {
+    const void* data;            /* uint8 codes [N,K], or BF16 [N,K] if scales == NULL */
+    const float* scales;         /* [N] or [N, ceil(K/128)]; NULL for BF16 weights */
+    int64_t scale_cols;          /* 1 or ceil(K/128); ignored for BF16 weights */
+    const uint16_t* cached_bf16; /* optional decoded copy [N,K] (bounded cache) or NULL */
+    int64_t N, K;
+} fp8lin_weight;
+
+typedef struct fp8lin_linear_options {
+    int optimized;        /* EngineOptions::optimized (false with --baseline) */
+    int vector_gemv;      /* --vector-gemv */
+    int cublas_prefill;   /* dequant-then-GEMM for rows > 8 */
+    int fp8_tensor_small; /* small-M matrix-core path */
+    int fp8_tensor_split; /* 1 or 4 */
+    int tilelang_fp8;     /* same contract as fp8_tensor_small, N % 16 == 0 */
+    int multi_token_gemv; /* shared-weight GEMV for rows 2..8 */
+    int shared_gemv_fp8;  /* shared GEMV reads FP8 codes even if a cache exists */
+} fp8lin_linear_options;
+
+/* Workspace needed by fp8lin_engine_linear for this weight and row count
+ * (split-K partials or a 2048-row BF16 slab); 0 if none. */
+size_t fp8lin_engine_linear_workspace_bytes(const fp8lin_linear_options* options,
+                                            const fp8lin_weight* weight, int64_t rows);
+/* Id of the branch fp8lin_engine_linear takes for this weight, options and
+ * row count (FP8LIN_PATH_*), without launching anything; 0 on bad arguments. */
+int fp8lin_engine_linear_path(const fp8lin_linear_options* options, const fp8lin_weight* weight,
+                              int64_t rows);
+/* y has row stride ldy >= weight->N.  Writes the id of the path it took to
+ * *path_out when path_out != NULL (FP8LIN_PATH_*). */
+int fp8lin_engine_linear(const fp8lin_linear_options* options, const fp8lin_weight* weight,
+                         const uint16_t* x, int64_t rows, uint16_t* y, int64_t ldy,
+                         void* workspace, size_t workspace_bytes, int* path_out,
+                         fp8lin_stream_t stream);
+/* Mixed projection groups (src/engine.cpp:198-199, fuse_weights :147-177):
+ * each group's output is written to consecutive column slices of y, in
+ * order, exactly like at::cat(parts, -1). */
+int fp8lin_engine_linear_groups(const fp8lin_linear_options* options,
+                                const fp8lin_weight* groups, int ngroups,
+                                const uint16_t* x, int64_t rows, uint16_t* y, int64_t ldy,
+                                void* workspace, size_t workspace_bytes,
+                                fp8lin_stream_t stream);
+
+enum fp8lin_path {
+    FP8LIN_PATH_TENSOR_SMALL = 1,
+    FP8LIN_PATH_SHARED_GEMV = 2,
+    FP8LIN_PATH_CACHED_BF16 = 3,
+    FP8LIN_PATH_FP8_GEMV = 4,
+    FP8LIN_PATH_FP8_GEMM = 5,
+    FP8LIN_PATH_DEQUANT_GEMM = 6,
+    FP8LIN_PATH_BF16 = 7
+};
+
+/* ---------------------------------------------------------------------------
+ * Deterministic synthetic inputs (no reference counterpart; used by the
+ * benchmark and tests so that the device and a host checker see the same
+ * bits).  Element i of stream `tag` is a standard normal from Philox4x32-10
+ * (counter (i lo, i hi, tag, 0x6a09e667), key (seed lo, seed hi)) through
+ * Box-Muller.  Weights are std * normal, quantized per 128x128 block with
+ * scale = max(amax, 1e-12) / 448 and codes = E4M3FN(w / scale) (round to
+ * nearest even), the recipe of tools/make_tiny_fixture.py:56-61; scales are
+ * written row-expanded [N, ceil(K/128)].  Activations are bf16(normal).
+ */
+int fp8lin_gen_weights(uint64_t seed, uint32_t tag, int64_t N, int64_t K, float std_dev,
+                       uint8_t* codes, float* scales, fp8lin_stream_t stream);
+int fp8lin_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_t K, uint16_t* x,
+                           fp8lin_stream_t stream);
+int fp8lin_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n, float* out,
+                      fp8lin_stream_t stream);
+
+/* Streaming-read probe (no reference counterpart): reads `bytes` bytes with
+ * 128-bit loads and writes one checksum word per workgroup into sink
+ * (>= 4096 floats).  Used to measure the practical HBM read ceiling. */
+int fp8lin_stream_read(const void* src, size_t bytes, float* sink, fp8lin_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FP8LIN_H */

@@ -1,0 +1,140 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+include/fp8lin.h declares, rejects bad arguments with the documented status
+codes before touching a device, and chooses Engine::linear's branch in the
+reference's order (src/engine.cpp:206-237)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "fp8lin.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fp8lin_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported(fp8lin):
+    names = header_functions()
+    assert len(names) >= 20
+    L = fp8lin.lib()
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in include/fp8lin.h but not exported"
+    assert sorted(set(fp8lin.EXPORTED) | {"fp8lin_engine_linear_path"}) == names
+
+
+def test_version_and_error_string(fp8lin):
+    L = fp8lin.lib()
+    assert L.fp8lin_version() == 100
+    assert isinstance(L.fp8lin_last_error(), bytes)
+
+
+# Fake, 16-byte aligned, never dereferenced: every call below fails validation
+# before any device access.
+P = ctypes.c_void_p(0x10000)
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, P, P, 1, P, 1, 8, 8, 0, None), 2),            # null x
+    ((P, P, P, 1, P, 0, 8, 8, 0, None), 1),               # M == 0 ("Empty GEMM")
+    ((P, P, P, 1, P, 1, 8, -1, 0, None), 1),              # K < 0
+    ((P, P, P, 3, P, 1, 8, 256, 0, None), 2),             # scale_cols not in {1, 2}
+    ((P, P, None, 1, P, 1, 8, 256, 0, None), 2),          # null scales
+])
+def test_linear_validation(fp8lin, args, code):
+    L = fp8lin.lib()
+    assert L.fp8lin_linear(*args) == code
+    assert L.fp8lin_last_error()
+
+
+@pytest.mark.parametrize("m,n,k,split,ws,code", [
+    (1, 16, 128, 1, None, 1),      # M < 2
+    (9, 16, 128, 1, None, 1),      # M > 8
+    (4, 16, 130, 1, None, 1),      # K % 128 != 0
+    (4, 16, 128, 2, None, 2),      # split not in {1, 4}
+    (4, 16, 128, 4, None, 4),      # split 4 without workspace
+])
+def test_tensor_small_validation(fp8lin, m, n, k, split, ws, code):
+    L = fp8lin.lib()
+    assert L.fp8lin_tensor_small(P, P, P, P, m, n, k, split, ws, 0, None) == code
+
+
+def test_workspace_sizes(fp8lin):
+    L = fp8lin.lib()
+    assert L.fp8lin_tensor_small_workspace_bytes(4, 100, 1) == 0
+    assert L.fp8lin_tensor_small_workspace_bytes(4, 100, 4) == 4 * 4 * 100 * 4
+
+
+def test_shared_and_swiglu_validation(fp8lin):
+    L = fp8lin.lib()
+    assert L.fp8lin_linear_shared(P, P, None, 1, P, 9, 8, 8, None) == 1   # 1..8 rows
+    assert L.fp8lin_linear_shared(P, P, P, 5, P, 2, 8, 300, None) == 2    # bad scale cols
+    assert L.fp8lin_linear_swiglu(P, P, P, 1, P, 1, 7, 8, None) == 1      # odd N
+    assert L.fp8lin_swiglu(P, P, -1, 4, None) == 1
+    assert L.fp8lin_swiglu(P, P, 0, 4, None) == 0                         # empty: no-op
+    assert L.fp8lin_decode(P, P, 1, P, 0, 5, None) == 0                   # empty: no-op
+    assert L.fp8lin_decode(P, P, 7, P, 4, 256, None) == 2
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error path")
+def test_no_device_is_reported(fp8lin):
+    L = fp8lin.lib()
+    assert L.fp8lin_init() == fp8lin.ERR_DEVICE
+
+
+def _weight(fp8lin, n=256, k=512, scales=True, scale_cols=None, cached=False):
+    w = fp8lin.Weight()
+    w.data = 0x10000
+    w.scales = 0x20000 if scales else None
+    w.scale_cols = scale_cols if scale_cols is not None else (k + 127) // 128
+    w.cached_bf16 = 0x30000 if cached else None
+    w.N, w.K = n, k
+    return w
+
+
+def _path(fp8lin, opt, w, rows):
+    return fp8lin.lib().fp8lin_engine_linear_path(ctypes.byref(opt), ctypes.byref(w), rows)
+
+
+def test_engine_decision_table(fp8lin):
+    F, O = fp8lin, fp8lin.LinearOptions
+    w = _weight(F)
+    assert _path(F, O(), w, 1) == F.PATH_FP8_GEMV
+    assert _path(F, O(), w, 8) == F.PATH_FP8_GEMV
+    assert _path(F, O(), w, 9) == F.PATH_FP8_GEMM
+    assert _path(F, O(cublas_prefill=True), w, 9) == F.PATH_DEQUANT_GEMM
+    assert _path(F, O(cublas_prefill=True), w, 8) == F.PATH_FP8_GEMV
+    assert _path(F, O(optimized=False), w, 1) == F.PATH_DEQUANT_GEMM
+    # tensor-small precedes everything for rows 2..8 with block scales, K%128 == 0
+    assert _path(F, O(fp8_tensor_small=True, multi_token_gemv=True), w, 4) == F.PATH_TENSOR_SMALL
+    assert _path(F, O(fp8_tensor_small=True), w, 1) == F.PATH_FP8_GEMV
+    assert _path(F, O(fp8_tensor_small=True), _weight(F, k=500), 4) == F.PATH_FP8_GEMV
+    assert _path(F, O(fp8_tensor_small=True), _weight(F, scale_cols=1), 4) == F.PATH_FP8_GEMV
+    assert _path(F, O(tilelang_fp8=True), _weight(F, n=250), 4) == F.PATH_FP8_GEMV
+    assert _path(F, O(tilelang_fp8=True), _weight(F, n=256), 4) == F.PATH_TENSOR_SMALL
+    # multi-token GEMV for rows 2..8, then the cache for rows > 1
+    assert _path(F, O(multi_token_gemv=True), w, 2) == F.PATH_SHARED_GEMV
+    assert _path(F, O(multi_token_gemv=True), w, 9) == F.PATH_FP8_GEMM
+    wc = _weight(F, cached=True)
+    assert _path(F, O(), wc, 2) == F.PATH_CACHED_BF16
+    assert _path(F, O(), wc, 1) == F.PATH_FP8_GEMV
+    assert _path(F, O(), _weight(F, scales=False), 4) == F.PATH_BF16
+
+
+def test_engine_validation(fp8lin):
+    F = fp8lin
+    L = F.lib()
+    opt = F.LinearOptions(fp8_tensor_split=3)
+    w = _weight(F)
+    rc = L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(w), P, 2, P, 256, None, 0, None, None)
+    assert rc == F.ERR_ARGUMENT
+    opt = F.LinearOptions()
+    rc = L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(w), P, 2, P, 100, None, 0, None, None)
+    assert rc == F.ERR_SHAPE   # ldy < N
+    w.scale_cols = 3
+    rc = L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(w), P, 2, P, 256, None, 0, None, None)
+    assert rc == F.ERR_ARGUMENT

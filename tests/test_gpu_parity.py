@@ -1,0 +1,343 @@
+"""GPU parity: every HIP path against the CPU oracle on identical inputs.
+
+Shapes and data follow the reference's own kernel tests
+(tests/kernel_test.cpp, tests/optimized_test.cpp, tests/fp8_tensor_test.cpp)
+with numpy's seeded RNG in place of the CUDA RNG, plus the BASELINE shapes.
+Bar: <= 1 BF16 ulp from the FP64 oracle (or rel-L2 <= 1e-2 and cosine >=
+0.9999), allclose(rtol .01, atol .001), and -- for the kernels that keep the
+reference rounding point -- >= 90% of outputs bit-identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+from parity import assert_parity, bf16_to_f32, ulp_distance
+
+pytestmark = pytest.mark.gpu
+
+
+def up(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if a.dtype == np.uint16:
+        t = t.view(torch.bfloat16)
+    return t.to(dev)
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def rand_bf16(rng, shape, scale=1.0):
+    f = (rng.standard_normal(shape) * scale).astype(np.float32)
+    return torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def rand_codes(rng, n, k, signed=True):
+    c = rng.integers(0, 127, (n, k), dtype=np.uint8)
+    if signed:
+        c = c | (rng.integers(0, 2, (n, k), dtype=np.uint8) << 7)
+    return c
+
+
+# ------------------------------------------------------------- decode / dequant
+def test_decode_all_codes(fp8lin, gpu, oracle):
+    """tests/kernel_test.cpp:16-24 on the device: every code, scale 1."""
+    codes = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    y = fp8lin.fp8_decode(up(codes, gpu), torch.ones(1, device=gpu))
+    got = bf16_to_f32(bits(y))[0]
+    ref = oracle.decode_table()
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+    assert np.array_equal(np.signbit(got[~nan]), np.signbit(ref[~nan]))
+
+
+@pytest.mark.parametrize("n,k,blockscale", [(137, 257, True), (64, 512, True), (19, 132, False),
+                                            (300, 5120, True), (3, 17, True)])
+def test_dequant_bit_exact(fp8lin, gpu, oracle, n, k, blockscale):
+    rng = np.random.default_rng(n * 7 + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, (k + 127) // 128) if blockscale else n) * .01 + .001).astype(np.float32)
+    y = fp8lin.fp8_decode(up(codes, gpu), up(scales, gpu))
+    assert np.array_equal(bits(y), oracle.dequant(codes, scales))
+
+
+# ------------------------------------------------------------------ generators
+def test_generators_match_oracle(fp8lin, gpu, oracle):
+    z = fp8lin.gen_normal(1 << 20, seed=0, tag=1, first=12345, device=gpu).cpu().numpy()
+    assert np.array_equal(z.view(np.uint32), oracle.normal(0, 1, 12345, 1 << 20).view(np.uint32))
+    codes, scales = fp8lin.gen_weights(300, 520, seed=0, tag=1, device=gpu)
+    oc, os_ = oracle.gen_weights(0, 1, 300, 520, 0.02)
+    assert np.array_equal(codes.cpu().numpy(), oc)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    x = fp8lin.gen_activations(3, 1000, seed=5, tag=2, device=gpu)
+    assert np.array_equal(bits(x), oracle.gen_activations(5, 2, 3, 1000))
+
+
+# ------------------------------------------------------------ decode GEMV (A3-A5)
+@pytest.mark.parametrize("m", [1, 2, 8])
+@pytest.mark.parametrize("k", [4, 128, 132, 257, 5120])
+def test_gemv_signed_subnormal(fp8lin, gpu, oracle, m, k):
+    """tests/optimized_test.cpp:49-56: signed/subnormal codes, block
+    boundaries, batch rows, scalar fallback (K % 16 != 0)."""
+    rng = np.random.default_rng(m * 100 + k)
+    n = 19
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, (k + 127) // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    y = fp8lin.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu), vector_gemv=True)
+    assert_parity(bits(y), oracle.linear(x, codes, scales), f"gemv m={m} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 17, 33])
+@pytest.mark.parametrize("k", [32, 70])
+def test_linear_row_scales(fp8lin, gpu, oracle, m, k):
+    """tests/optimized_test.cpp:71-77: 1-D per-row scales, GEMV and GEMM."""
+    rng = np.random.default_rng(m * 10 + k)
+    n = 79
+    codes = rng.integers(0, 126, (n, k), dtype=np.uint8)
+    scales = (rng.random(n) * .01).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    y = fp8lin.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu))
+    assert_parity(bits(y), oracle.linear(x, codes, scales), f"row scales m={m} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 17])
+def test_linear_block_tail(fp8lin, gpu, oracle, m):
+    """tests/optimized_test.cpp:79-88: N=137, K=257, three scale blocks."""
+    rng = np.random.default_rng(m)
+    n, k = 137, 257
+    codes = rng.integers(0, 126, (n, k), dtype=np.uint8)
+    scales = (rng.random((n, 3)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    y = fp8lin.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu))
+    assert_parity(bits(y), oracle.linear(x, codes, scales), f"block tail m={m}")
+
+
+def test_unaligned_view_bit_equal(fp8lin, gpu, oracle):
+    """tests/optimized_test.cpp:57-62: an unaligned contiguous view takes the
+    byte-load path and gives the same bits as the aligned one."""
+    rng = np.random.default_rng(9)
+    k = 5120
+    x = rand_bf16(rng, (1, k))
+    codes = rand_codes(rng, 64, k)
+    scales = (rng.random((64, k // 128)) * .01 + .001).astype(np.float32)
+    big = torch.zeros(k + 1, dtype=torch.bfloat16, device=gpu)
+    big[1:] = up(x, gpu)[0]
+    xu = big.narrow(0, 1, k).reshape(1, k)
+    cbig = torch.zeros(64 * k + 1, dtype=torch.uint8, device=gpu)
+    cbig[1:] = up(codes, gpu).reshape(-1)
+    cu = cbig.narrow(0, 1, 64 * k).reshape(64, k)
+    ya = fp8lin.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu), True)
+    yu = fp8lin.fp8_linear(xu, cu, up(scales, gpu), True)
+    assert torch.equal(ya, yu)
+    assert_parity(bits(ya), oracle.linear(x, codes, scales), "aligned")
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 6, 8])
+@pytest.mark.parametrize("k", [17, 128, 257, 5120])
+def test_shared_gemv_fp8_equals_bf16(fp8lin, gpu, oracle, m, k):
+    """tests/optimized_test.cpp:7-14: shared GEMV on FP8 == on the decoded
+    BF16 weights, bit for bit (pins the rounding point)."""
+    rng = np.random.default_rng(m * 1000 + k)
+    n = 19
+    codes = rng.integers(0, 126, (n, k), dtype=np.uint8)
+    scales = (rng.random((n, (k + 127) // 128)) * .01 + .001).astype(np.float32)
+    x = up(rand_bf16(rng, (m, k)), gpu)
+    c, s = up(codes, gpu), up(scales, gpu)
+    decoded = fp8lin.fp8_decode(c, s)
+    a = fp8lin.small_linear_shared(x, c, s)
+    b = fp8lin.small_linear_shared(x, decoded)
+    assert torch.equal(a, b)
+    assert_parity(bits(a), oracle.linear(bits(x), codes, scales), f"shared m={m} k={k}")
+
+
+# ---------------------------------------------------------- small-M tensor path
+@pytest.mark.parametrize("m", [2, 3, 5, 8])
+@pytest.mark.parametrize("k", [128, 384, 5120])
+@pytest.mark.parametrize("n", [17, 80, 144])
+def test_tensor_small_vs_fp64(fp8lin, gpu, oracle, m, k, n):
+    """tests/fp8_tensor_test.cpp:28-39: M 2..8, tails, empty split ranges."""
+    rng = np.random.default_rng(m * 10000 + k + n)
+    codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    codes[(codes == 127) | (codes == 255)] = 0
+    scales = (rng.random((n, k // 128)) * .001 + .0001).astype(np.float32)
+    x = rand_bf16(rng, (m, k), 0.1)
+    ref = oracle.linear(x, codes, scales)
+    for split in (1, 4):
+        y = fp8lin.fp8_tensor_small(up(x, gpu), up(codes, gpu), up(scales, gpu), split)
+        assert_parity(bits(y), ref, f"tensor_small m={m} k={k} n={n} split={split}")
+        if n % 16 == 0:
+            y2 = fp8lin.tilelang_fp8_small(up(x, gpu), up(codes, gpu), up(scales, gpu), split)
+            assert torch.equal(y, y2)
+
+
+def test_tensor_small_graph_replay(fp8lin, gpu, oracle):
+    """tests/fp8_tensor_test.cpp:40-52: a captured graph sees updated
+    activations on every replay."""
+    rng = np.random.default_rng(11)
+    x = up(rand_bf16(rng, (4, 384), 0.1), gpu)
+    codes_np = np.full((144, 384), 24, np.uint8)
+    scales_np = (rng.random((144, 3)) * .1).astype(np.float32)
+    codes, scales = up(codes_np, gpu), up(scales_np, gpu)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        out = fp8lin.fp8_tensor_small(x, codes, scales, 4)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = fp8lin.fp8_tensor_small(x, codes, scales, 4)
+    for i in range(4):
+        if i:
+            x.add_(0.015625)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_parity(bits(out), oracle.linear(bits(x), codes_np, scales_np), f"replay {i}")
+
+
+# ----------------------------------------------------------------- prefill GEMM
+@pytest.mark.parametrize("m,n,k", [(17, 137, 257), (33, 256, 384), (256, 512, 1024),
+                                   (300, 520, 640), (9, 75, 64)])
+def test_gemm_fp8(fp8lin, gpu, oracle, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, (k + 127) // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    y = fp8lin.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu))
+    assert_parity(bits(y), oracle.linear(x, codes, scales), f"gemm {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 137, 257), (300, 520, 640)])
+def test_gemm_bf16(fp8lin, gpu, oracle, m, n, k):
+    rng = np.random.default_rng(m * n)
+    w = rand_bf16(rng, (n, k), 0.05)
+    x = rand_bf16(rng, (m, k))
+    y = fp8lin.gemm_bf16(up(x, gpu), up(w, gpu))
+    assert_parity(bits(y), oracle.linear_bf16w(x, w), f"bf16 gemm {m}x{n}x{k}")
+
+
+# ---------------------------------------------------------------------- SwiGLU
+def test_swiglu_standalone(fp8lin, gpu, oracle):
+    rng = np.random.default_rng(12)
+    g = rand_bf16(rng, (17, 2 * 257), 3.0)
+    y = bits(fp8lin.fused_swiglu(up(g, gpu)))
+    ref = oracle.swiglu(g)
+    assert ulp_distance(y, ref).max() <= 1
+    assert (y == ref).mean() > 0.99
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 512, 384), (5, 260, 256), (64, 512, 512), (300, 1040, 640)])
+def test_linear_swiglu_fused_equals_unfused(fp8lin, gpu, oracle, m, n, k):
+    """gate/up + SwiGLU fused == fused_swiglu(fp8_linear(x, gate_up))."""
+    rng = np.random.default_rng(m + n)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, (k + 127) // 128)) * .01 + .001).astype(np.float32)
+    x = up(rand_bf16(rng, (m, k)), gpu)
+    c, s = up(codes, gpu), up(scales, gpu)
+    fused = fp8lin.linear_swiglu(x, c, s)
+    gate_up = fp8lin.fp8_linear(x, c, s)
+    if m <= 8:
+        # The decode GEMV and the GEMM sum in different orders; compare each
+        # with the oracle composition instead of bit for bit.
+        ref = oracle.swiglu(oracle.linear(bits(x), codes, scales))
+        assert_parity(bits(fused), ref, "fused swiglu (decode)")
+    else:
+        assert torch.equal(fused, fp8lin.fused_swiglu(gate_up))
+        ref = oracle.swiglu(oracle.linear(bits(x), codes, scales))
+        assert ulp_distance(bits(fused), ref).max() <= 2
+
+
+# ---------------------------------------------------------- Engine::linear paths
+def test_engine_paths(fp8lin, gpu, oracle):
+    F = fp8lin
+    rng = np.random.default_rng(13)
+    n, k = 272, 640
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    ref_w = oracle.dequant(codes, scales)
+    cases = [
+        (F.LinearOptions(), 1, F.PATH_FP8_GEMV, False),
+        (F.LinearOptions(), 20, F.PATH_FP8_GEMM, False),
+        (F.LinearOptions(cublas_prefill=True), 20, F.PATH_DEQUANT_GEMM, False),
+        (F.LinearOptions(optimized=False), 3, F.PATH_DEQUANT_GEMM, False),
+        (F.LinearOptions(fp8_tensor_small=True, fp8_tensor_split=4), 4, F.PATH_TENSOR_SMALL, False),
+        (F.LinearOptions(multi_token_gemv=True), 3, F.PATH_SHARED_GEMV, False),
+        (F.LinearOptions(), 12, F.PATH_CACHED_BF16, True),
+        (F.LinearOptions(multi_token_gemv=True), 3, F.PATH_SHARED_GEMV, True),
+    ]
+    for opt, rows, path, cache in cases:
+        eng = F.LinearEngine(opt, weight_cache_bytes=(1 << 30) if cache else 0)
+        eng.add("w.weight", up(codes, gpu), up(scales, gpu))
+        if cache:
+            eng.build_cache()
+        x = rand_bf16(rng, (rows, k))
+        y, p = eng.linear(up(x, gpu), "w", return_path=True)
+        assert p == path, (opt, rows, p)
+        assert_parity(bits(y), oracle.linear_bf16w(x, ref_w), f"engine path {path}")
+
+
+def test_engine_mixed_groups(fp8lin, gpu, oracle):
+    """tests/optimized_test.cpp:89-98: grouped == separate projections."""
+    F = fp8lin
+    rng = np.random.default_rng(14)
+    for m in (1, 17):
+        qkv = rng.integers(0, 126, (384, 256), dtype=np.uint8)
+        z = rng.integers(0, 126, (128, 256), dtype=np.uint8)
+        qs = (rng.random((384, 2)) * .01).astype(np.float32)
+        zs = (rng.random((128, 2)) * .01).astype(np.float32)
+        b = rand_bf16(rng, (4, 256))
+        a = rand_bf16(rng, (4, 256))
+        eng = F.LinearEngine()
+        for name, d, s in [("qkv", qkv, qs), ("z", z, zs), ("b", b, None), ("a", a, None)]:
+            eng.add(f"p.{name}.weight", up(d, gpu), up(s, gpu) if s is not None else None)
+        eng.fuse_weights("p.all", ["p.qkv", "p.z", "p.b", "p.a"])
+        x = rand_bf16(rng, (m, 256))
+        y = bits(eng.linear(up(x, gpu), "p.all"))
+        sep = np.concatenate([oracle.linear(x, qkv, qs), oracle.linear(x, z, zs),
+                              oracle.linear_bf16w(x, b), oracle.linear_bf16w(x, a)], axis=1)
+        assert_parity(y, sep, f"mixed groups m={m}")
+
+
+# --------------------------------------------------------------- BASELINE shapes
+def test_config1_gemv_seed0(fp8lin, gpu, oracle):
+    """M=1, N=K=4096, seed 0, N(0,0.02) weights."""
+    codes, scales = fp8lin.gen_weights(4096, 4096, seed=0, tag=1, device=gpu)
+    x = fp8lin.gen_activations(1, 4096, seed=0, tag=2, device=gpu)
+    y = fp8lin.fp8_linear(x, codes, scales, True)
+    ref = oracle.linear(bits(x), codes.cpu().numpy(), scales.cpu().numpy())
+    s = assert_parity(bits(y), ref, "config 1")
+    assert s["max_ulp"] <= 1
+
+
+@pytest.mark.parametrize("n,k", [(17408, 5120), (5120, 8704), (7168, 5120)])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_decode_shapes(fp8lin, gpu, oracle, n, k, m):
+    """BASELINE configs 2 and 3 at one TP rank's shard shapes, all rows."""
+    codes, scales = fp8lin.gen_weights(n, k, seed=0, tag=1, device=gpu)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=gpu)
+    c_np, s_np = codes.cpu().numpy(), scales.cpu().numpy()
+    ref = oracle.linear(bits(x), c_np, s_np)
+    assert_parity(bits(fp8lin.fp8_linear(x, codes, scales, True)), ref, f"gemv {m}x{n}x{k}")
+    if m >= 2:
+        for split in (1, 4):
+            y = fp8lin.fp8_tensor_small(x, codes, scales, split)
+            assert_parity(bits(y), ref, f"tensor_small {m}x{n}x{k} s{split}")
+
+
+@pytest.mark.parametrize("m", [512, 4096])
+def test_prefill_swiglu_shape(fp8lin, gpu, oracle, m):
+    """gate/up N=17408, K=5120, fused SwiGLU; oracle on a
+    row sample plus the last rows."""
+    n, k = 17408, 5120
+    codes, scales = fp8lin.gen_weights(n, k, seed=0, tag=1, device=gpu)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=gpu)
+    y = fp8lin.linear_swiglu(x, codes, scales)
+    rng = np.random.default_rng(m)
+    rows = np.unique(np.concatenate([rng.choice(m, 24, replace=False), [0, m - 1]]))
+    xs = bits(x)[rows]
+    ref = oracle.swiglu(oracle.linear(xs, codes.cpu().numpy(), scales.cpu().numpy()))
+    got = bits(y)[rows]
+    assert ulp_distance(got, ref).max() <= 2
+    assert (got == ref).mean() > 0.9
