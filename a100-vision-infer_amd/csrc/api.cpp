@@ -304,9 +304,16 @@ int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* s
         require(N % 2 == 0, FP8LIN_ERR_SHAPE, "Invalid SwiGLU input: N must be even");
         check_scales(scales, scale_cols, K);
         ensure_device();
-        check_hip(fp8lin::launch_gemm(x, codes, scales, (int)scale_cols, y, N / 2, (int)M, (int)N,
-                                      (int)K, true, as_stream(stream)),
-                  "fp8 gemm+swiglu launch");
+        if (M <= 8) {
+            const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
+            check_hip(fp8lin::launch_gemv_swiglu(x, codes, scales, (int)scale_cols, y, N / 2, (int)M,
+                                                 (int)N, (int)K, wide, as_stream(stream)),
+                      "fp8 gemv+swiglu launch");
+        } else {
+            check_hip(fp8lin::launch_gemm(x, codes, scales, (int)scale_cols, y, N / 2, (int)M,
+                                          (int)N, (int)K, true, as_stream(stream)),
+                      "fp8 gemm+swiglu launch");
+        }
     });
 }
 

@@ -75,6 +75,27 @@ __device__ __forceinline__ u32x4 load_u32x4_stream(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// Raw buffer resources (V#) for branch-free loads: a lane whose byte offset is
+// at or beyond `num_records` reads zeros instead of faulting, so a guarded load
+// needs no branch and the compiler's wait counting stays exact.  Dword 3 is the
+// gfx9-family raw-buffer format word.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kBufferOob = 0x80000000u;  // offset used for masked lanes
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes,
+                                             0x00020000);
+}
+
+// AUX: cache policy bits of the load (2 = non-temporal on gfx950).
+template <int AUX>
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX));
+}
+__device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
 }  // namespace fp8lin
 
 namespace fp8lin {

@@ -1,0 +1,526 @@
+// Decode GEMV kernels for 1..8 activation rows sharing one pass over the
+// weights (see gemv.hip for the dispatch and the numerics contract).
+//
+// A weight row is cut into 16-element chunks; lane l of a wave takes chunk
+// c = l + 64*j of its rows at step j, so one wave step reads 1 KiB of
+// contiguous codes per row with 128-bit loads.  Per chunk the 16 codes are
+// converted with v_cvt_pk_f32_fp8, multiplied by the block scale, rounded to
+// BF16 (v_cvt_pk_bf16_f32) and accumulated with v_dot2_f32_bf16.  A lane sums
+// its chunks in step order; the 64 lane sums are then combined by a butterfly.
+//
+// Three kernels share that per-row order, so for one (K, W) they give the same
+// bits whatever the load width, the weight type or the work distribution:
+//  - gemv_kernel: W waves per workgroup split a row's steps (j = w, w+W, ...),
+//    their sums are added in LDS in wave order; pointer loads, with a byte-load
+//    variant for unaligned data or K % 16 != 0;
+//  - gemv_ring_kernel: one wave owns R rows, the step loop is unrolled so every
+//    load of the row group is issued up front (W = 1 order);
+//  - gemv_persist_kernel: each wave streams a list of row groups through a
+//    register ring that crosses row boundaries (W = 1 order).
+// The last two use raw buffer loads: a masked lane gets an out-of-range offset
+// and reads zeros, so there is no branch around any load and the hardware
+// wait counters let the loads run ahead of the arithmetic.
+#pragma once
+#include "device.hpp"
+
+namespace fp8lin {
+namespace gemv {
+
+template <bool FP8>
+struct Chunk;
+
+template <>
+struct Chunk<true> {
+    u32x4 codes;
+    float scale;
+};
+template <>
+struct Chunk<false> {
+    u32x4 lo, hi;
+};
+
+// ------------------------------------------------------------ pointer loads
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+    if constexpr (NT) return load_u32x4_stream(p);
+    return load_u32x4(p);
+}
+
+template <bool FP8, bool WIDE, bool NT>
+__device__ __forceinline__ void load_chunk(Chunk<FP8>& ch, const void* __restrict__ w,
+                                           const float* __restrict__ scales, int S, int64_t row,
+                                           int K, int k0, bool valid) {
+    if constexpr (FP8) {
+        const uint8_t* wr = static_cast<const uint8_t*>(w) + row * (int64_t)K;
+        if (!valid) {
+            ch.codes = u32x4{0, 0, 0, 0};
+            ch.scale = 0.0f;
+            return;
+        }
+        ch.scale = scales[row * S + (S == 1 ? 0 : (k0 >> 7))];
+        if constexpr (WIDE) {
+            ch.codes = ld16<NT>(wr + k0);
+        } else {
+            uint32_t v[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int k = k0 + d * 4 + b;
+                    const uint32_t byte = k < K ? (uint32_t)wr[k] : 0u;
+                    word |= byte << (8 * b);
+                }
+                v[d] = word;
+            }
+            ch.codes = u32x4{v[0], v[1], v[2], v[3]};
+        }
+    } else {
+        const uint16_t* wr = static_cast<const uint16_t*>(w) + row * (int64_t)K;
+        if (!valid) {
+            ch.lo = u32x4{0, 0, 0, 0};
+            ch.hi = u32x4{0, 0, 0, 0};
+            return;
+        }
+        if constexpr (WIDE) {
+            ch.lo = ld16<NT>(wr + k0);
+            ch.hi = ld16<NT>(wr + k0 + 8);
+        } else {
+            uint32_t v[8];
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const int k = k0 + 2 * d;
+                const uint32_t a = k < K ? (uint32_t)wr[k] : 0u;
+                const uint32_t b = k + 1 < K ? (uint32_t)wr[k + 1] : 0u;
+                v[d] = a | (b << 16);
+            }
+            ch.lo = u32x4{v[0], v[1], v[2], v[3]};
+            ch.hi = u32x4{v[4], v[5], v[6], v[7]};
+        }
+    }
+}
+
+template <bool WIDE>
+__device__ __forceinline__ void load_x(uint32_t (&xv)[8], const uint16_t* __restrict__ xr, int K,
+                                       int k0, bool valid) {
+    if (!valid) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = 0;
+        return;
+    }
+    if constexpr (WIDE) {
+        const u32x4 a = load_u32x4(xr + k0), b = load_u32x4(xr + k0 + 8);
+        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+        xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    } else {
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const int k = k0 + 2 * d;
+            const uint32_t a = k < K ? (uint32_t)xr[k] : 0u;
+            const uint32_t b = k + 1 < K ? (uint32_t)xr[k + 1] : 0u;
+            xv[d] = a | (b << 16);
+        }
+    }
+}
+
+// ------------------------------------------------------------- buffer loads
+// Offsets are 32-bit: the host only uses these for matrices below 2 GiB.
+struct Buffers {
+    rsrc_t w, s, x;
+};
+
+__device__ __forceinline__ Buffers make_buffers(const uint16_t* x, const void* w,
+                                                const float* scales, int S, int M, int N, int K,
+                                                bool fp8) {
+    Buffers b;
+    b.w = make_rsrc(w, (uint32_t)((int64_t)N * K * (fp8 ? 1 : 2)));
+    b.s = make_rsrc(scales, fp8 ? (uint32_t)((int64_t)N * S * 4) : 0u);
+    b.x = make_rsrc(x, (uint32_t)((int64_t)M * K * 2));
+    return b;
+}
+
+template <bool FP8, int AUX>
+__device__ __forceinline__ void load_chunk_buf(Chunk<FP8>& ch, const Buffers& b, int S, int64_t row,
+                                               int K, int k0, bool valid) {
+    if constexpr (FP8) {
+        const uint32_t off = valid ? (uint32_t)(row * K + k0) : kBufferOob;
+        const uint32_t soff = valid ? (uint32_t)((row * S + (S == 1 ? 0 : (k0 >> 7))) * 4) : kBufferOob;
+        ch.codes = buf_load16<AUX>(b.w, off);
+        ch.scale = buf_load_f32(b.s, soff);
+    } else {
+        const uint32_t off = valid ? (uint32_t)((row * K + k0) * 2) : kBufferOob;
+        ch.lo = buf_load16<AUX>(b.w, off);
+        ch.hi = buf_load16<AUX>(b.w, valid ? off + 16 : kBufferOob);
+    }
+}
+
+__device__ __forceinline__ void load_x_buf(uint32_t (&xv)[8], const Buffers& b, int m, int K,
+                                           int k0, bool valid) {
+    const uint32_t off = valid ? (uint32_t)((m * K + k0) * 2) : kBufferOob;
+    const u32x4 a = buf_load16<0>(b.x, off);
+    const u32x4 c = buf_load16<0>(b.x, valid ? off + 16 : kBufferOob);
+    xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
+    xv[4] = c.x; xv[5] = c.y; xv[6] = c.z; xv[7] = c.w;
+}
+
+// ------------------------------------------------------------------- shared
+template <bool FP8>
+__device__ __forceinline__ void chunk_to_bf16(const Chunk<FP8>& ch, uint32_t (&wv)[8]) {
+    if constexpr (FP8) {
+        dequant4(ch.codes.x, ch.scale, wv[0], wv[1]);
+        dequant4(ch.codes.y, ch.scale, wv[2], wv[3]);
+        dequant4(ch.codes.z, ch.scale, wv[4], wv[5]);
+        dequant4(ch.codes.w, ch.scale, wv[6], wv[7]);
+    } else {
+        wv[0] = ch.lo.x; wv[1] = ch.lo.y; wv[2] = ch.lo.z; wv[3] = ch.lo.w;
+        wv[4] = ch.hi.x; wv[5] = ch.hi.y; wv[6] = ch.hi.z; wv[7] = ch.hi.w;
+    }
+}
+
+// acc[r][m] += dot(weights of chunk r, activations of row m)
+template <int R, int MR, bool FP8>
+__device__ __forceinline__ void accumulate(float (&acc)[R][MR], const Chunk<FP8> (&ch)[R],
+                                           const uint32_t (&xv)[MR][8]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        uint32_t wv[8];
+        chunk_to_bf16<FP8>(ch[r], wv);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float a = acc[r][m];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) a = dot2_bf16(wv[i], xv[m][i], a);
+            acc[r][m] = a;
+        }
+    }
+}
+
+// Weight row held by slot r of row group g (and whether it exists).
+template <int R, bool SWIGLU>
+__device__ __forceinline__ int64_t slot_row(int64_t g, int r, int N, bool& ok) {
+    if constexpr (SWIGLU) {
+        const int64_t D = N >> 1;
+        const int64_t j = g * (R / 2) + (r % (R / 2));
+        ok = j < D;
+        const int64_t row = r < R / 2 ? j : D + j;
+        return ok ? row : 0;
+    } else {
+        const int64_t row = g * R + r;
+        ok = row < N;
+        return ok ? row : 0;
+    }
+}
+
+// Store the R x MR totals of a row group (lane 0 calls this).
+template <int R, int MR, bool SWIGLU>
+__device__ __forceinline__ void store_group(uint16_t* __restrict__ y, int64_t ldy, int M,
+                                            const int64_t (&rows)[R], const bool (&ok)[R],
+                                            const float (&tot)[R][MR]) {
+    if constexpr (SWIGLU) {
+#pragma unroll
+        for (int r = 0; r < R / 2; ++r) {
+            if (!ok[r]) continue;
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < M)
+                    y[(int64_t)m * ldy + rows[r]] = swiglu_bf16_bits(
+                        f32_to_bf16_bits(tot[r][m]), f32_to_bf16_bits(tot[r + R / 2][m]));
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (!ok[r]) continue;
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < M) y[(int64_t)m * ldy + rows[r]] = f32_to_bf16_bits(tot[r][m]);
+        }
+    }
+}
+
+__device__ __forceinline__ int group_count(int N, int R, bool swiglu) {
+    return swiglu ? ((N >> 1) + R / 2 - 1) / (R / 2) : (N + R - 1) / R;
+}
+
+// ------------------------------------------------- W-split kernel (general)
+// MR: compile-time bound on activation rows (runtime M <= MR).  R: weight rows
+// per workgroup (even for SWIGLU).  W: waves per workgroup.  NT: non-temporal
+// weight loads.  WIDE: 128-bit loads (K % 16 == 0, 16-byte aligned pointers),
+// else byte loads.
+template <int MR, int R, int W, bool WIDE, bool FP8, bool SWIGLU, bool NT>
+__global__ __launch_bounds__(64 * W) void gemv_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
+    int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int64_t g = blockIdx.x;
+
+    int64_t rows[R];
+    bool row_ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rows[r] = slot_row<R, SWIGLU>(g, r, N, row_ok[r]);
+
+    const int chunks = (K + 15) >> 4;
+    const int steps = (chunks + kWave - 1) / kWave;
+
+    float acc[R][MR];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
+
+    Chunk<FP8> cur[R];
+    {
+        const int c = lane + wave * kWave;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            load_chunk<FP8, WIDE, NT>(cur[r], w, scales, S, rows[r], K, c << 4,
+                                      row_ok[r] && wave < steps && c < chunks);
+    }
+    for (int j = wave; j < steps; j += W) {
+        const int c = lane + j * kWave;
+        const int k0 = c << 4;
+        const bool valid = c < chunks;
+        Chunk<FP8> nxt[R];
+        const int cn = c + W * kWave;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            load_chunk<FP8, WIDE, NT>(nxt[r], w, scales, S, rows[r], K, cn << 4,
+                                      row_ok[r] && cn < chunks);
+        uint32_t xv[MR][8];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const int mm = m < M ? m : M - 1;
+            load_x<WIDE>(xv[m], x + (int64_t)mm * K, K, k0, valid);
+        }
+        accumulate<R, MR, FP8>(acc, cur, xv);
+#pragma unroll
+        for (int r = 0; r < R; ++r) cur[r] = nxt[r];
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r][m] = wave_sum(acc[r][m]);
+
+    float total[R][MR];
+    if constexpr (W == 1) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) total[r][m] = acc[r][m];
+    } else {
+        __shared__ float red[W][R * MR];
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) red[wave][r * MR + m] = acc[r][m];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                float t = red[0][r * MR + m];
+#pragma unroll
+                for (int v = 1; v < W; ++v) t += red[v][r * MR + m];
+                total[r][m] = t;
+            }
+    }
+    if (lane == 0) store_group<R, MR, SWIGLU>(y, ldy, M, rows, row_ok, total);
+}
+
+template <int MR, int R, int W, bool FP8, bool SWIGLU, bool NT>
+hipError_t launch(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
+                  int64_t ldy, int M, int N, int K, bool wide, hipStream_t stream) {
+    const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
+    dim3 grid((unsigned)groups);
+    if (wide)
+        hipLaunchKernelGGL((gemv_kernel<MR, R, W, true, FP8, SWIGLU, NT>), grid, dim3(64 * W), 0,
+                           stream, x, w, scales, S, y, ldy, M, N, K);
+    else
+        hipLaunchKernelGGL((gemv_kernel<MR, R, W, false, FP8, SWIGLU, NT>), grid, dim3(64 * W), 0,
+                           stream, x, w, scales, S, y, ldy, M, N, K);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------ unrolled ring kernel
+// K <= 1024 * MAXSTEPS, K % 16 == 0.  One wave per workgroup owns R rows; all
+// loads of the row group are issued before the arithmetic.
+template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX>
+__global__ __launch_bounds__(64) void gemv_ring_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
+    int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
+    const int lane = threadIdx.x;
+    const int64_t g = blockIdx.x;
+    const Buffers b = make_buffers(x, w, scales, S, M, N, K, FP8);
+    int64_t rows[R];
+    bool row_ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rows[r] = slot_row<R, SWIGLU>(g, r, N, row_ok[r]);
+    const int chunks = K >> 4;
+    const int steps = (chunks + kWave - 1) / kWave;
+
+    Chunk<FP8> ring[MAXSTEPS][R];
+    uint32_t xv[MAXSTEPS][MR][8];
+#pragma unroll
+    for (int j = 0; j < MAXSTEPS; ++j) {
+        const int c = lane + j * kWave;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            load_chunk_buf<FP8, AUX>(ring[j][r], b, S, rows[r], K, c << 4, row_ok[r] && c < chunks);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) load_x_buf(xv[j][m], b, m < M ? m : M - 1, K, c << 4, c < chunks);
+    }
+    float acc[R][MR];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXSTEPS; ++j) {
+        // Steps past the end leave acc untouched (a select, not a branch).
+        float nxt[R][MR];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) nxt[r][m] = acc[r][m];
+        accumulate<R, MR, FP8>(nxt, ring[j], xv[j]);
+        const bool live = j < steps;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[r][m] = live ? nxt[r][m] : acc[r][m];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r][m] = wave_sum(acc[r][m]);
+    if (lane == 0) store_group<R, MR, SWIGLU>(y, ldy, M, rows, row_ok, acc);
+}
+
+template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX>
+hipError_t launch_ring(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
+                       int64_t ldy, int M, int N, int K, hipStream_t stream) {
+    const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
+    hipLaunchKernelGGL((gemv_ring_kernel<MR, R, MAXSTEPS, FP8, SWIGLU, AUX>), dim3((unsigned)groups),
+                       dim3(64), 0, stream, x, w, scales, S, y, ldy, M, N, K);
+    return hipGetLastError();
+}
+
+// -------------------------------------------------------- persistent kernel
+// Each wave of a 4-wave workgroup walks row groups g = wave id, + total waves,
+// ... as one flat sequence of (group, step) items held in a DEPTH-deep
+// register ring, so the next group's loads are in flight while the current one
+// is reduced and stored.  The activations are staged once per workgroup in LDS
+// (MR * K * 2 bytes).
+template <int MR, int R, int DEPTH, bool FP8, bool SWIGLU, int AUX>
+__global__ __launch_bounds__(256) void gemv_persist_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
+    int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int groups) {
+    extern __shared__ __align__(16) uint16_t xs[];  // [MR][K]
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int chunks = K >> 4;
+    const int steps = (chunks + kWave - 1) / kWave;
+    const Buffers b = make_buffers(x, w, scales, S, M, N, K, FP8);
+
+    for (int m = 0; m < MR; ++m) {
+        const int mm = m < M ? m : M - 1;
+        for (int c = threadIdx.x; c < chunks * 2; c += 256)
+            *reinterpret_cast<u32x4*>(xs + m * K + c * 8) = buf_load16<0>(b.x, (uint32_t)((mm * K + c * 8) * 2));
+    }
+    __syncthreads();
+
+    const int total_waves = gridDim.x * 4;
+    const int gw = blockIdx.x * 4 + wave;
+    const int my_groups = gw < groups ? (groups - 1 - gw) / total_waves + 1 : 0;
+    const int items = my_groups * steps;
+    const int padded = (items + DEPTH - 1) / DEPTH * DEPTH;
+
+    auto issue = [&](Chunk<FP8> (&dst)[R], int item) {
+        const bool live = item < items;
+        const int it = live ? item : 0;
+        const int64_t g = gw + (int64_t)(it / steps) * total_waves;
+        const int c = lane + (it % steps) * kWave;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            bool ok;
+            const int64_t row = slot_row<R, SWIGLU>(g, r, N, ok);
+            load_chunk_buf<FP8, AUX>(dst[r], b, S, row, K, c << 4, live && ok && c < chunks);
+        }
+    };
+
+    Chunk<FP8> ring[DEPTH][R];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue(ring[d], d);
+
+    float acc[R][MR];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
+
+    for (int t0 = 0; t0 < padded; t0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int t = t0 + d;
+            const int j = t % steps;
+            const int c = lane + j * kWave;
+            const bool cv = c < chunks;
+            const int cc = cv ? c : 0;
+            uint32_t xv[MR][8];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const u32x4 a = *reinterpret_cast<const u32x4*>(xs + m * K + cc * 16);
+                const u32x4 e = *reinterpret_cast<const u32x4*>(xs + m * K + cc * 16 + 8);
+                xv[m][0] = cv ? a.x : 0u; xv[m][1] = cv ? a.y : 0u;
+                xv[m][2] = cv ? a.z : 0u; xv[m][3] = cv ? a.w : 0u;
+                xv[m][4] = cv ? e.x : 0u; xv[m][5] = cv ? e.y : 0u;
+                xv[m][6] = cv ? e.z : 0u; xv[m][7] = cv ? e.w : 0u;
+            }
+            accumulate<R, MR, FP8>(acc, ring[d], xv);
+            issue(ring[d], t + DEPTH);
+            if (j == steps - 1 && t < items) {
+                const int64_t g = gw + (int64_t)(t / steps) * total_waves;
+                int64_t rows[R];
+                bool ok[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) rows[r] = slot_row<R, SWIGLU>(g, r, N, ok[r]);
+                float tot[R][MR];
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) {
+                        tot[r][m] = wave_sum(acc[r][m]);
+                        acc[r][m] = 0.0f;
+                    }
+                if (lane == 0) store_group<R, MR, SWIGLU>(y, ldy, M, rows, ok, tot);
+            }
+        }
+    }
+}
+
+// Waves for the persistent kernel: split the row groups evenly with at most
+// `max_waves` resident waves.
+inline int persist_waves(int64_t groups, int max_waves) {
+    const int64_t per = (groups + max_waves - 1) / max_waves;
+    const int64_t waves = (groups + per - 1) / per;
+    return (int)((waves + 3) / 4 * 4);
+}
+
+template <int MR, int R, int DEPTH, bool FP8, bool SWIGLU, int AUX>
+hipError_t launch_persist(const uint16_t* x, const void* w, const float* scales, int S,
+                          uint16_t* y, int64_t ldy, int M, int N, int K, int max_waves,
+                          hipStream_t stream) {
+    const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
+    const int waves = persist_waves(groups, max_waves);
+    const size_t lds = (size_t)MR * K * 2;
+    hipLaunchKernelGGL((gemv_persist_kernel<MR, R, DEPTH, FP8, SWIGLU, AUX>), dim3(waves / 4),
+                       dim3(256), lds, stream, x, w, scales, S, y, ldy, M, N, K, (int)groups);
+    return hipGetLastError();
+}
+
+}  // namespace gemv
+}  // namespace fp8lin

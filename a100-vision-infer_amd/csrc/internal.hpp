@@ -11,6 +11,11 @@ namespace fp8lin {
 hipError_t launch_gemv(const uint16_t* x, const void* w, bool fp8, const float* scales, int S,
                        uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
                        hipStream_t stream);
+// Decode GEMV with the SwiGLU epilogue: N weight rows (gate [0,N/2), up
+// [N/2,N)), y is [M, N/2].
+hipError_t launch_gemv_swiglu(const uint16_t* x, const uint8_t* codes, const float* scales, int S,
+                              uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
+                              hipStream_t stream);
 
 // Small-M matrix-core kernel, 1 <= M <= 16, K % 128 == 0, block scales
 // (small_m.hip).  split == 1 writes BF16 y; split > 1 writes FP32 partials

@@ -42,7 +42,7 @@ def stats(got_bits, ref_bits):
     }
 
 
-def assert_parity(got_bits, ref_bits, what="", min_exact=0.9):
+def assert_parity(got_bits, ref_bits, what="", min_exact=0.9, elementwise=True):
     """min_exact: fraction of outputs that must be bit-identical to the oracle.
     Kernels that keep the reference rounding point bf16(decode*scale) differ
     from the FP64 oracle only where the FP32 sum lands next to a BF16 rounding
@@ -54,6 +54,8 @@ def assert_parity(got_bits, ref_bits, what="", min_exact=0.9):
     assert ok, f"{what}: parity failed {s}"
     if min_exact is not None:
         assert s["exact"] >= min_exact, f"{what}: only {s['exact']:.4f} bit-exact {s}"
+    if not elementwise:
+        return s
     g = bf16_to_f32(got_bits).astype(np.float64)
     r = bf16_to_f32(ref_bits).astype(np.float64)
     assert np.allclose(g, r, rtol=0.01, atol=0.001), f"{what}: allclose(.01,.001) failed {s}"

@@ -238,15 +238,17 @@ def test_linear_swiglu_fused_equals_unfused(fp8lin, gpu, oracle, m, n, k):
     c, s = up(codes, gpu), up(scales, gpu)
     fused = fp8lin.linear_swiglu(x, c, s)
     gate_up = fp8lin.fp8_linear(x, c, s)
-    if m <= 8:
-        # The decode GEMV and the GEMM sum in different orders; compare each
-        # with the oracle composition instead of bit for bit.
-        ref = oracle.swiglu(oracle.linear(bits(x), codes, scales))
-        assert_parity(bits(fused), ref, "fused swiglu (decode)")
-    else:
+    ref_gu = oracle.linear(bits(x), codes, scales)
+    assert_parity(bits(gate_up), ref_gu, "gate/up")
+    # SwiGLU of the device's own gate/up: only expf may differ (<= 1 ulp).
+    own = oracle.swiglu(bits(gate_up))
+    if m > 8:
+        # Same GEMM accumulation, different epilogue: bit-identical.
         assert torch.equal(fused, fp8lin.fused_swiglu(gate_up))
-        ref = oracle.swiglu(oracle.linear(bits(x), codes, scales))
-        assert ulp_distance(bits(fused), ref).max() <= 2
+        assert ulp_distance(bits(fused), own).max() <= 1
+    # Against the oracle composition a 1-ulp gate difference can move a tiny
+    # silu(a) (a << 0) by many ulps, so the tolerance clause applies.
+    assert_parity(bits(fused), oracle.swiglu(ref_gu), "fused swiglu", elementwise=False)
 
 
 # ---------------------------------------------------------- Engine::linear paths
@@ -338,6 +340,4 @@ def test_prefill_swiglu_shape(fp8lin, gpu, oracle, m):
     rows = np.unique(np.concatenate([rng.choice(m, 24, replace=False), [0, m - 1]]))
     xs = bits(x)[rows]
     ref = oracle.swiglu(oracle.linear(xs, codes.cpu().numpy(), scales.cpu().numpy()))
-    got = bits(y)[rows]
-    assert ulp_distance(got, ref).max() <= 2
-    assert (got == ref).mean() > 0.9
+    assert_parity(bits(y)[rows], ref, f"prefill swiglu M={m}", elementwise=False)
