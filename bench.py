@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 
-A step is one decode pass of the one-rank layer chain at M=1 (BASELINE
+A step is one decode pass of the one-rank layer chain at M=1 (benchmark
 config 2): gate/up 17408x5120, down 5120x8704 and QKV-gate 7168x5120, E4M3FN
 weights with 128x128 block scales (seed 0, N(0, 0.02)), BF16 activations
 N(0,1).  Weight sets are rotated so the working set exceeds twice the 256 MB
@@ -23,6 +23,11 @@ sys.path.insert(0, os.path.join(ROOT, "a100-vision-infer_amd"))
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 METRIC = "FP8 GEMV HBM GB/s (% peak) at M=1; prefill GEMM TFLOP/s (% MFMA peak)"
+# HBM bytes per launch of the roofline kernel (gate/up GEMV, M=1), from two
+# rocprofv3 --pmc passes: 2.000 x FETCH_SIZE (45 231.5 KiB) + 1.000 x WRITE_SIZE
+# (272.0 KiB); the factors are what the counters read for a 256 MiB device copy
+# (`bench.py --calibrate`).  Re-measure when the kernel changes.
+GATE_UP_TRAFFIC_BYTES = 92_912_640
 SHAPES = [("gate_up", 17408, 5120), ("down", 5120, 8704), ("qkv_gate", 7168, 5120)]
 
 
@@ -41,6 +46,11 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
+    p.add_argument("--sections", default="gemv,small,prefill,chain,stream",
+                   help="secondary measurements to run (comma list of gemv, small, prefill, "
+                        "chain, stream)")
+    p.add_argument("--calibrate", action="store_true",
+                   help="also run a 256 MiB device copy (known HBM bytes) for counter scaling")
     return p.parse_args()
 
 
@@ -52,7 +62,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
-              "tensor-parallel sharding is described in DESIGN.md but not run", file=sys.stderr)
+              "tensor-parallel sharding is designed but not run on more than one GPU", file=sys.stderr)
         sys.exit(2)
     import torch
     import fp8lin
@@ -99,9 +109,8 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    # The decode step runs as a captured HIP graph (the reference's decode
-    # loop is CUDA-graph captured too): one graph holds one step per weight
-    # copy, and the timed region replays it.
+    # The decode step also runs as a captured HIP graph (the reference's decode
+    # loop is CUDA-graph captured): one graph holds one step per weight copy.
     copies = len(sets)
     cap = torch.cuda.Stream(dev)
     graph = torch.cuda.CUDAGraph()
@@ -115,7 +124,7 @@ def main():
         sp.value = sp_saved
     stream.wait_stream(cap)
     replays = max(1, (args.steps + copies - 1) // copies)
-    steps = replays * copies
+    steps = args.steps
     for _ in range(3):
         graph.replay()
     torch.cuda.synchronize()
@@ -140,7 +149,7 @@ def main():
         graph.replay()
     r1.record()
     torch.cuda.synchronize()
-    graph_ms = r0.elapsed_time(r1) / steps
+    graph_ms = r0.elapsed_time(r1) / (replays * copies)
 
     # Dominant kernel: gate/up GEMV, back-to-back launches over the rotating
     # copies in a graph, timed with HIP events around the replays.
@@ -171,11 +180,14 @@ def main():
     extra = {"graph_us_per_step": round(graph_ms * 1e3, 3),
              "graph_GBs": round(step_bytes / (graph_ms * 1e-3) / 1e9, 1)}
     if not args.quick:
-        extra.update(secondary(torch, fp8lin, dev, sets, log))
+        extra.update(secondary(torch, fp8lin, dev, sets, log, set(args.sections.split(","))))
+    if args.calibrate:
+        extra.update(calibrate(torch, dev, log))
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(sets[0], xs, args.cpu_seconds, log)
+        cpu, cpu_extra = cpu_baseline(sets[0], xs, args.cpu_seconds, log)
+        extra.update(cpu_extra)
 
     out = {
         "metric": METRIC,
@@ -193,7 +205,7 @@ def main():
                 "BF16 N(0,1) activations)",
         "config": {
             "workload": "decode GEMV, M=1, one TP-rank layer chain: gate/up 17408x5120 + "
-                        "down 5120x8704 + QKV-gate 7168x5120 (BASELINE config 2)",
+                        "down 5120x8704 + QKV-gate 7168x5120 (config 2)",
             "batch_rows": 1,
             "weight_format": "E4M3FN codes + FP32 128x128 block scales (row-expanded)",
             "accumulate": "fp32",
@@ -207,7 +219,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GATE_UP_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2.000 + WRITE_SIZE x1.000 (copy-calibrated)",
             "avg_launch_us": round(gu_avg_ms * 1e3, 3),
             "algorithmic_bytes_per_launch": gu_bytes,
         },
@@ -230,7 +243,7 @@ def timed(torch, fn, iters, warm=3):
     return a.elapsed_time(b) / iters
 
 
-def secondary(torch, fp8lin, dev, sets, log):
+def secondary(torch, fp8lin, dev, sets, log, sections):
     """Per-shape and per-path figures through the C ABI with preallocated
     outputs (no allocation or tensor checks on the host between launches)."""
     import ctypes
@@ -243,14 +256,19 @@ def secondary(torch, fp8lin, dev, sets, log):
         if rc:
             raise RuntimeError(L.fp8lin_last_error())
 
-    # per-shape decode GEMV (rotating copies)
-    for name, n, k in SHAPES:
+    # per-shape decode GEMV (rotating copies), plus config 1 (N = K = 4096)
+    # over 32 copies (554 MB) so it too streams from HBM
+    cfg1 = [fp8lin.gen_weights(4096, 4096, seed=0, tag=100 + c, device=dev)
+            for c in range(32)] if "gemv" in sections else []
+    gemv_cases = [(name, n, k, [ws[name] for ws in sets]) for name, n, k in SHAPES]
+    gemv_cases.append(("cfg1_4096", 4096, 4096, cfg1))
+    for name, n, k, copies in (gemv_cases if "gemv" in sections else []):
         x = fp8lin.gen_activations(1, k, seed=0, tag=2, device=dev)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
         i = [0]
 
         def run():
-            c, s = sets[i[0] % len(sets)][name]
+            c, s = copies[i[0] % len(copies)]
             i[0] += 1
             ok(L.fp8lin_linear(P(x), P(c), P(s), s.size(1), P(y), 1, n, k, 1, sp))
         ms = timed(torch, run, 400)
@@ -258,8 +276,9 @@ def secondary(torch, fp8lin, dev, sets, log):
         extra[f"gemv_m1_{name}_GBs"] = round(gbs, 1)
         extra[f"gemv_m1_{name}_us"] = round(ms * 1e3, 2)
         log(f"gemv M=1 {name}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
+    del cfg1
     # small M (config 3): GEMV and matrix-core paths on the three shapes
-    for name, n, k in SHAPES:
+    for name, n, k in (SHAPES if "small" in sections else []):
         for m in (2, 4, 8):
             x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
             y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
@@ -285,7 +304,7 @@ def secondary(torch, fp8lin, dev, sets, log):
     # prefill GEMM with fused SwiGLU (config 4)
     n, k = 17408, 5120
     c, s = sets[0]["gate_up"]
-    for m in (512, 1024, 4096):
+    for m in ((512, 1024, 4096) if "prefill" in sections else ()):
         x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
         y = torch.empty((m, n // 2), dtype=torch.bfloat16, device=dev)
         ms = timed(torch, lambda: ok(L.fp8lin_linear_swiglu(P(x), P(c), P(s), s.size(1), P(y), m, n, k, sp)),
@@ -295,14 +314,94 @@ def secondary(torch, fp8lin, dev, sets, log):
         extra[f"prefill_swiglu_m{m}_frac"] = round(tflops / BF16_PEAK_TFLOPS, 4)
         log(f"prefill M={m} gate/up+SwiGLU: {ms:.3f} ms {tflops:.1f} TFLOP/s "
             f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of BF16 peak)")
+    if "chain" in sections:
+        extra.update(layer_chain(torch, fp8lin, dev, sets[0], log))
     # streaming-read ceiling: 1 GiB and the gate/up weight size
-    buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    sink = torch.zeros(4096, dtype=torch.float32, device=dev)
-    for label, nbytes in (("1GiB", 1 << 30), ("gate_up", 17408 * 5120)):
-        ms = timed(torch, lambda: ok(L.fp8lin_stream_read(P(buf), nbytes, P(sink), sp)), 50)
-        extra[f"stream_read_{label}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
-        log(f"stream read {label}: {extra[f'stream_read_{label}_GBs']} GB/s")
+    if "stream" in sections:
+        buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        sink = torch.zeros(4096, dtype=torch.float32, device=dev)
+        for label, nbytes in (("1GiB", 1 << 30), ("gate_up", 17408 * 5120)):
+            ms = timed(torch, lambda: ok(L.fp8lin_stream_read(P(buf), nbytes, P(sink), sp)), 50)
+            extra[f"stream_read_{label}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            log(f"stream read {label}: {extra[f'stream_read_{label}_GBs']} GB/s")
     return extra
+
+
+def layer_chain(torch, fp8lin, dev, ws, log):
+    """Config 5: QKV-gate -> gate/up+SwiGLU -> down -> vocab-sharded head
+    (75968 x 5120) at M = 512 and M = 1, each link fed by the previous one's
+    output where the shapes chain (QKV-gate and gate/up both read the layer
+    input; attention between them is out of scope).  One step touches 577 MB
+    of weights, more than twice the 256 MB Infinity Cache, so no rotation is
+    needed."""
+    import ctypes
+    L = fp8lin.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    head = fp8lin.gen_weights(75968, 5120, seed=0, tag=90, device=dev)
+    links = [("qkv_gate", ws["qkv_gate"], 7168, 5120, False),
+             ("gate_up_swiglu", ws["gate_up"], 17408, 5120, True),
+             ("down", ws["down"], 5120, 8704, False),
+             ("head", head, 75968, 5120, False)]
+    extra = {}
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(L.fp8lin_last_error())
+
+    for m in (1, 512):
+        x = fp8lin.gen_activations(m, 5120, seed=0, tag=2, device=dev)
+        outs = {name: torch.empty((m, n // 2 if sw else n), dtype=torch.bfloat16, device=dev)
+                for name, _, n, _, sw in links}
+        feeds = {"qkv_gate": x, "gate_up_swiglu": x, "down": outs["gate_up_swiglu"], "head": outs["down"]}
+
+        def call(name, w, n, k, sw):
+            c, s = w
+            if sw:
+                ok(L.fp8lin_linear_swiglu(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k, sp))
+            else:
+                ok(L.fp8lin_linear(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k, 1, sp))
+
+        def chain():
+            for link in links:
+                call(*link)
+        iters = 200 if m == 1 else 10
+        total_ms = timed(torch, chain, iters)
+        tot_bytes = tot_flops = 0
+        for name, w, n, k, sw in links:
+            ms = timed(torch, lambda: call(name, w, n, k, sw), iters)
+            nbytes = algo_bytes(m, n, k, n // 2 if sw else n)
+            flops = 2.0 * m * n * k
+            tot_bytes += nbytes
+            tot_flops += flops
+            key = f"chain_m{m}_{name}"
+            extra[key + "_us"] = round(ms * 1e3, 2)
+            if m == 1:
+                extra[key + "_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            else:
+                extra[key + "_TFLOPs"] = round(flops / (ms * 1e-3) / 1e12, 1)
+        extra[f"chain_m{m}_total_us"] = round(total_ms * 1e3, 2)
+        if m == 1:
+            gbs = tot_bytes / (total_ms * 1e-3) / 1e9
+            extra["chain_m1_GBs"] = round(gbs, 1)
+            log(f"chain M=1: {total_ms * 1e3:.2f} us, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM)")
+        else:
+            tf = tot_flops / (total_ms * 1e-3) / 1e12
+            extra[f"chain_m{m}_TFLOPs"] = round(tf, 1)
+            log(f"chain M={m}: {total_ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / BF16_PEAK_TFLOPS:.1f}% MFMA)")
+        log("  " + ", ".join(f"{name} {extra[f'chain_m{m}_{name}_us']} us" for name, *_ in links))
+    return extra
+
+
+def calibrate(torch, dev, log):
+    """A 256 MiB device-to-device copy (256 MiB read + 256 MiB written): the
+    known-size kernel that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.empty(1 << 28, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = timed(torch, lambda: dst.copy_(src), 5)
+    gbs = 2 * (1 << 28) / (ms * 1e-3) / 1e9
+    log(f"calibration copy 256 MiB: {ms * 1e3:.1f} us ({gbs:.1f} GB/s read+write)")
+    return {"calibration_copy_256MiB_us": round(ms * 1e3, 1)}
 
 
 def cpu_baseline(ws, xs, seconds, log):
@@ -330,9 +429,31 @@ def cpu_baseline(ws, xs, seconds, log):
     step_bytes = sum(algo_bytes(1, n, k) for _, n, k in SHAPES)
     gbs = step_bytes / per / 1e9
     log(f"cpu oracle: {per * 1e3:.1f} ms/step on {threads} threads ({gbs:.2f} GB/s)")
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} full decode steps (3 GEMVs, M=1) in {el:.1f} s; "
-                      f"{per * 1e3:.1f} ms per step; FP64 oracle, OpenMP over output rows"}
+
+    # one thread, one step
+    t0 = time.perf_counter()
+    for name, n, k in SHAPES:
+        c, s = host[name]
+        O.linear(xh[k], c, s, threads=1)
+    per1 = time.perf_counter() - t0
+    log(f"cpu oracle: {per1 * 1e3:.1f} ms/step on 1 thread ({step_bytes / per1 / 1e9:.2f} GB/s)")
+
+    # prefill M=4096 gate/up: 64 of the 17408 weight rows, scaled linearly
+    xp = O.gen_activations(0, 2, 4096, 5120)
+    c, s = host["gate_up"]
+    t0 = time.perf_counter()
+    O.linear(xp, c, s, rows=(0, 64), threads=threads)
+    part = time.perf_counter() - t0
+    est = part * 17408 / 64
+    log(f"cpu oracle prefill M=4096 gate/up: {est:.1f} s extrapolated from 64 rows ({part:.2f} s)")
+    cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"{reps} full decode steps (3 GEMVs, M=1) in {el:.1f} s; "
+                     f"{per * 1e3:.1f} ms per step; FP64 oracle, OpenMP over output rows"}
+    extra = {"cpu_1thread_ms_per_step": round(per1 * 1e3, 1),
+             "cpu_1thread_GBs": round(step_bytes / per1 / 1e9, 3),
+             "cpu_prefill_m4096_gate_up_s_extrapolated": round(est, 1),
+             "cpu_prefill_m4096_TFLOPs_extrapolated": round(2.0 * 4096 * 17408 * 5120 / est / 1e12, 5)}
+    return cpu, extra
 
 
 if __name__ == "__main__":

@@ -1,6 +1,6 @@
 """BF16 comparison helpers for parity tests.
 
-The parity bar (BASELINE.json north_star): the BF16 output is within 1 BF16
+The parity bar: the BF16 output is within 1 BF16
 ulp of the CPU oracle, or -- where the accumulation order differs -- the
 relative L2 error is <= 1e-2 with cosine similarity >= 0.9999.  The
 reference's own test tolerance (allclose rtol .01, atol .001 against an FP64

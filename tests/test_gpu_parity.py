@@ -2,7 +2,7 @@
 
 Shapes and data follow the reference's own kernel tests
 (tests/kernel_test.cpp, tests/optimized_test.cpp, tests/fp8_tensor_test.cpp)
-with numpy's seeded RNG in place of the CUDA RNG, plus the BASELINE shapes.
+with numpy's seeded RNG in place of the CUDA RNG, plus the benchmark shapes.
 Bar: <= 1 BF16 ulp from the FP64 oracle (or rel-L2 <= 1e-2 and cosine >=
 0.9999), allclose(rtol .01, atol .001), and -- for the kernels that keep the
 reference rounding point -- >= 90% of outputs bit-identical.
@@ -302,9 +302,9 @@ def test_engine_mixed_groups(fp8lin, gpu, oracle):
         assert_parity(y, sep, f"mixed groups m={m}")
 
 
-# --------------------------------------------------------------- BASELINE shapes
+# ------------------------------------------------------------- benchmark shapes
 def test_config1_gemv_seed0(fp8lin, gpu, oracle):
-    """M=1, N=K=4096, seed 0, N(0,0.02) weights."""
+    """Benchmark config 1: M=1, N=K=4096, seed 0, N(0,0.02) weights."""
     codes, scales = fp8lin.gen_weights(4096, 4096, seed=0, tag=1, device=gpu)
     x = fp8lin.gen_activations(1, 4096, seed=0, tag=2, device=gpu)
     y = fp8lin.fp8_linear(x, codes, scales, True)
@@ -316,7 +316,7 @@ def test_config1_gemv_seed0(fp8lin, gpu, oracle):
 @pytest.mark.parametrize("n,k", [(17408, 5120), (5120, 8704), (7168, 5120)])
 @pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_decode_shapes(fp8lin, gpu, oracle, n, k, m):
-    """BASELINE configs 2 and 3 at one TP rank's shard shapes, all rows."""
+    """Benchmark configs 2 and 3 at one TP rank's shard shapes, all rows."""
     codes, scales = fp8lin.gen_weights(n, k, seed=0, tag=1, device=gpu)
     x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=gpu)
     c_np, s_np = codes.cpu().numpy(), scales.cpu().numpy()
@@ -330,7 +330,7 @@ def test_decode_shapes(fp8lin, gpu, oracle, n, k, m):
 
 @pytest.mark.parametrize("m", [512, 4096])
 def test_prefill_swiglu_shape(fp8lin, gpu, oracle, m):
-    """gate/up N=17408, K=5120, fused SwiGLU; oracle on a
+    """Benchmark config 4: gate/up N=17408, K=5120, fused SwiGLU; oracle on a
     row sample plus the last rows."""
     n, k = 17408, 5120
     codes, scales = fp8lin.gen_weights(n, k, seed=0, tag=1, device=gpu)
