@@ -100,11 +100,12 @@ __device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t off) {
 
 namespace fp8lin {
 
-// SwiGLU of one (gate, up) pair of FP32 GEMM results, with the reference's
-// rounding points (src/optimized.cu:73): both inputs are first rounded to BF16
-// (they are BF16 tensors in the reference), g = bf16(a / (1 + exp(-a))),
-// y = bf16(g * u).  Shared by the standalone kernel and the GEMM epilogues so
-// the fused and unfused paths agree bit for bit.
+// SwiGLU of one (gate, up) pair, with the reference's rounding points
+// (src/optimized.cu:73): a and u are BF16 values (BF16 tensors in the
+// reference), g = bf16(a / (1 + exp(-a))), y = bf16(g * u), with an accurate
+// expf and an IEEE division so g stays within 1 BF16 ulp of the exact value.
+// Shared by the standalone kernel and every GEMM and GEMV epilogue, so the
+// fused and unfused paths agree bit for bit.
 __device__ __forceinline__ uint16_t swiglu_bf16_bits(uint16_t a_bits, uint16_t u_bits) {
     const float a = bf16_bits_to_f32(a_bits);
     const float u = bf16_bits_to_f32(u_bits);

@@ -1,0 +1,456 @@
+// Prefill FP8 GEMM for gfx950: y[M,N] = x[M,K] * W^T with W as E4M3FN codes
+// and FP32 block scales, BF16 MFMA with FP32 accumulation (the reference's
+// WMMA GEMM, src/optimized.cu:24-40, at the rounding point bf16(decode(c)*s)
+// of src/optimized.cu:32), optionally with the gate/up + SwiGLU epilogue
+// (src/engine.cpp:415).
+//
+// Workgroup: 4 waves, one per SIMD, 256 (M) x 256 (weight rows) tile.  Each
+// wave owns all 256 rows of M and 64 weight rows: 8 x 2 accumulators of
+// v_mfma_f32_32x32x16_bf16 held in AGPRs.  Owning the whole M extent makes the
+// dequantization cost per MFMA minimal (every code is converted once per
+// workgroup, 2 VALU per MFMA), and the 64-row width keeps the A-fragment LDS
+// reads at one 16-byte read per two MFMAs.
+//
+// Data movement (K advances 64 per step, so a 128-K scale block is 2 steps):
+//   A (BF16 activations): direct-to-LDS buffer loads (buffer_load_dwordx4 ...
+//     lds), coalesced 8 rows x 128 B per instruction, into a 3-stage ring of
+//     256 x 128 B; the 16-byte chunks of a row are XOR-swizzled (ga) so the
+//     16 rows read by a quarter-wave of a fragment load hit distinct banks.
+//     All 4 waves share it; one barrier per step, in the middle of the step.
+//   B (FP8 codes): each wave DMAs its own 64 rows x 64 B per step (16 rows x
+//     64 B per instruction) into a private 3-slot LDS ring (swizzle gb), reads
+//     them back in the MFMA B-operand layout and dequantizes them in registers
+//     one step ahead.  No B data crosses waves, so B needs no barrier.
+//   Scales: one dword per lane per 128-K block, loaded a step ahead.
+// The K index within a step is permuted identically for A and B (lane half h
+// of sub-step s covers k = 32*(s/2) + 16h + 8*(s%2) + [0,8)), which changes
+// only the FP32 summation order inside one MFMA.
+//
+// The steady state of a step is an explicit instruction sequence (one inline
+// asm statement per instruction): 64 MFMAs, each followed by two dequant
+// VALU instructions, with the next sub-step's LDS fragment reads, the DMAs and
+// the B reads placed in fixed MFMA slots and hand-counted s_waitcnt.  The
+// waits list the registers their loads filled as in/out operands, so the
+// compiler neither reads nor reuses a register before its data has arrived,
+// and every load into registers is retired before the loop's back edge.
+#pragma once
+#include <utility>
+
+#include "device.hpp"
+
+namespace fp8lin {
+namespace gemm_fp8 {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 256, WN = 64, BN = 256, BK = 64;
+constexpr int MT = 8, NT = 2;
+constexpr int THREADS = 256;
+constexpr int A_STAGE = BM * 128;               // 32 KiB: 256 rows x 64 BF16
+constexpr int A_BYTES = 3 * A_STAGE;
+constexpr int B_SLOT = WN * 64;                 // 4 KiB: 64 rows x 64 codes
+constexpr int B_WAVE = 3 * B_SLOT;
+constexpr int LDS_BYTES = A_BYTES + 4 * B_WAVE;  // 144 KiB of the 160 KiB
+
+// Chunk swizzles: A rows hold 8 chunks of 16 B (slot = chunk ^ ga(row)), B
+// rows 4 chunks (slot = chunk ^ gb(row)).  For any 16 consecutive rows read
+// at one chunk index both keep the 16-byte slots on distinct LDS banks.
+__device__ __forceinline__ int ga(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int gb(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// Raw buffer descriptor as four SGPRs (inline-asm operand form).
+__device__ __forceinline__ i32x4 make_desc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    i32x4 d;
+    d.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    d.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff);
+    d.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    d.w = 0x00020000;
+    return d;
+}
+
+// ---- one instruction each ----
+__device__ __forceinline__ void mfma(f32x16& acc, const u32x4& a, const u32x4& b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+template <int OFF>
+__device__ __forceinline__ void ds_read(u32x4& d, uint32_t addr) {
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "i"(OFF));
+}
+// 64 lanes x 16 B from global (voff + soff, bounds-checked) into LDS
+// [m0v, m0v + 1024), lane l at m0v + 16 l.
+__device__ __forceinline__ void dma16(uint32_t m0v, uint32_t voff, i32x4 desc, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 ::"s"(m0v), "v"(voff), "s"(desc), "s"(soff) : "memory", "m0");
+}
+__device__ __forceinline__ void buf_load1(float& d, uint32_t voff, i32x4 desc, int soff) {
+    asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(d) : "v"(voff), "s"(desc), "s"(soff));
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N) : "memory"); }
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Waits that also redefine the registers their loads filled (see header).
+template <int N>
+__device__ __forceinline__ void wait_lgkm8(u32x4 (&a)[MT]) {
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7])
+                 : "i"(N)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm12(u32x4 (&a)[MT], u32x4 (&b)[NT][2]) {
+    asm volatile("s_waitcnt lgkmcnt(%12)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                   "+v"(b[0][0]), "+v"(b[0][1]), "+v"(b[1][0]), "+v"(b[1][1])
+                 : "i"(N)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm_braw(u32x4 (&b)[2][NT][2]) {
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(b[0][0][0]), "+v"(b[0][0][1]), "+v"(b[0][1][0]), "+v"(b[0][1][1]), "+v"(b[1][0][0]),
+                   "+v"(b[1][0][1]), "+v"(b[1][1][0]), "+v"(b[1][1][1])
+                 : "i"(N)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm2(float (&v)[NT]) {
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(v[0]), "+v"(v[1]) : "i"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm4(float (&v)[NT], float (&u)[NT]) {
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(u[0]), "+v"(u[1]) : "i"(N) : "memory");
+}
+
+struct State {
+    f32x16 acc[MT][NT];
+    u32x4 af[2][MT];       // A fragments of two sub-steps
+    u32x4 bf[2][NT][4];    // dequantized B fragments [step parity][frag][sub-step]
+    u32x4 braw[2][NT][2];  // codes [step parity][frag][chunk pair]
+    float bsc[2][NT];      // scales [128-K block parity][frag]
+    f32x2 tp[2];           // dequant temporaries
+    float tm[4];
+};
+
+// Instruction K (0..127) of one step's dequantization: unit K/16 = (frag j,
+// sub-step ss), two code words of 4 each:
+//   v_cvt_pk_f32_fp8 lo, hi  ->  4 x v_mul_f32 by the scale  ->  2 x
+//   v_cvt_pk_bf16_f32 (round to nearest even): bf16(decode(c) * s).
+template <int K, int RB, int BD>
+__device__ __forceinline__ void dequant_op(State& st, const float (&sc)[NT]) {
+    constexpr int unit = K / 16, r = K % 16;
+    constexpr int j = unit / 4, ss = unit % 4;
+    constexpr int wi = r / 8, q = r % 8;
+    const u32x4& src = st.braw[RB][j][ss >> 1];
+    const uint32_t w = (ss & 1) ? (wi ? src.w : src.z) : (wi ? src.y : src.x);
+    if constexpr (q == 0) asm volatile("v_cvt_pk_f32_fp8 %0, %1" : "=v"(st.tp[0]) : "v"(w));
+    if constexpr (q == 1) asm volatile("v_cvt_pk_f32_fp8_sdwa %0, %1 src0_sel:WORD_1" : "=v"(st.tp[1]) : "v"(w));
+    if constexpr (q >= 2 && q <= 5) {
+        constexpr int e = q - 2;
+        asm volatile("v_mul_f32 %0, %1, %2" : "=v"(st.tm[e]) : "v"(st.tp[e >> 1][e & 1]), "v"(sc[j]));
+    }
+    if constexpr (q == 6 || q == 7) {
+        constexpr int e = (q - 6) * 2;
+        uint32_t o;
+        asm volatile("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(o) : "v"(st.tm[e]), "v"(st.tm[e + 1]));
+        st.bf[BD][j][ss][wi * 2 + (q - 6)] = o;
+    }
+}
+
+struct Ctx {
+    i32x4 dx, dw, ds;
+    uint32_t aoff[8];   // A DMA lane offsets (k = 0)
+    uint32_t boff[4];   // B DMA lane offsets (k = 0)
+    uint32_t soff[NT];  // scale row offsets
+    uint32_t ard[4];    // A fragment read address per sub-step, stage 0
+    uint32_t brd[2];    // B read address per chunk pair, slot 0
+    uint32_t m0a, m0b;  // this wave's DMA LDS bases, stage / slot 0
+    int scol;           // bytes per 128-K scale block in a scale row (4, or 0 for per-row scales)
+};
+
+// LDS positions of one step; the mod-3 rings are rotated at run time.
+struct Ring {
+    uint32_t ar, an, aw;  // A stages kt%3 (read), (kt+1)%3 (next), (kt+2)%3 (DMA)
+    uint32_t bw, br;      // B slots kt%3 (DMA), (kt+2)%3 (read)
+    __device__ __forceinline__ void advance() {
+        const uint32_t t = ar;
+        ar = an;
+        an = aw;
+        aw = t;
+        br = bw;
+        bw = bw == 2 * B_SLOT ? 0u : bw + B_SLOT;
+    }
+};
+
+// Step kt, T = kt % 4.
+//   A: read stage kt%3; after the mid-step barrier DMA A(kt+2) into stage
+//      (kt+2)%3; in sub-step 3 read step kt+1's first fragments.
+//   B: DMA B(kt+3) into slot kt%3; dequantize B(kt+1) from braw[(kt+1)&1];
+//      in sub-step 3 read B(kt+2) from slot (kt+2)%3 into braw[kt&1].
+//   Scales: odd steps load block (kt+3)/2 into bsc[block&1]; step kt
+//      dequantizes with block (kt+1)/2.
+template <int T>
+__device__ __forceinline__ void kstep(State& st, const Ctx& c, const Ring& rg, int kt) {
+    constexpr int RB_DQ = (T + 1) & 1, RB_RD = T & 1;
+    constexpr int BC = T & 1, BD = BC ^ 1;
+    constexpr int SB_DQ = ((T + 1) / 2) & 1;
+    constexpr bool SLOAD = T & 1;
+    constexpr int SB_LD = ((T + 3) / 2) & 1;
+    constexpr int NS = SLOAD ? 2 : 0;
+    constexpr bool PREV_SLOAD = !(T & 1);
+    constexpr int SB_PREV = ((T + 2) / 2) & 1;
+    const int kB = (kt + 3) * BK;
+    const int kA = (kt + 2) * BK * 2;
+    const int sS = ((kt + 3) >> 1) * c.scol;
+    uint32_t ard[4];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) ard[q] = c.ard[q] + rg.ar;
+    ard[0] = c.ard[0] + rg.an;
+    const uint32_t brd0 = c.brd[0] + rg.br, brd1 = c.brd[1] + rg.br;
+    const uint32_t m0b = c.m0b + rg.bw, m0a = c.m0a + rg.aw;
+
+    [&]<int... S>(std::integer_sequence<int, S...>) __attribute__((always_inline)) {
+        ([&]() __attribute__((always_inline)) {
+            constexpr int s = S;
+            if constexpr (s == 0)
+                wait_lgkm12<0>(st.af[0], st.braw[RB_DQ]);
+            else
+                wait_lgkm8<0>(st.af[s & 1]);
+            [&]<int... M>(std::integer_sequence<int, M...>) __attribute__((always_inline)) {
+                ([&]() __attribute__((always_inline)) {
+                    constexpr int m = M;
+                    constexpr int i = m >> 1, j = m & 1;
+                    mfma(st.acc[i][j], st.af[s & 1][i], st.bf[BC][j][s]);
+                    dequant_op<(s * 16 + m) * 2, RB_DQ, BD>(st, st.bsc[SB_DQ]);
+                    dequant_op<(s * 16 + m) * 2 + 1, RB_DQ, BD>(st, st.bsc[SB_DQ]);
+                    if constexpr (m < 8) {
+                        if constexpr (s < 3)
+                            ds_read<m * 4096>(st.af[(s + 1) & 1][m], ard[s + 1]);
+                        else
+                            ds_read<m * 4096>(st.af[0][m], ard[0]);
+                    }
+                    if constexpr (s == 0 && m >= 8 && (m & 1) == 0)
+                        dma16(m0b + ((m - 8) >> 1) * 1024, c.boff[(m - 8) >> 1], c.dw, kB);
+                    if constexpr (SLOAD && s == 0 && (m == 9 || m == 11))
+                        buf_load1(st.bsc[SB_LD][(m - 9) >> 1], c.soff[(m - 9) >> 1], c.ds, sS);
+                    if constexpr (s == 2 && m >= 8)
+                        dma16(m0a + (m - 8) * 1024, c.aoff[m - 8], c.dx, kA);
+                    if constexpr (s == 3 && m >= 8 && m < 12) {
+                        constexpr int jj = (m - 8) >> 1, cp = (m - 8) & 1;
+                        ds_read<jj * 2048>(st.braw[RB_RD][jj][cp], cp ? brd1 : brd0);
+                    }
+                }(), ...);
+            }(std::make_integer_sequence<int, 16>{});
+            if constexpr (s == 1) {
+                // A(kt+1), the previous step's last DMA, has landed (issued
+                // after it: this step's 4 B DMA and NS scale loads).
+                if constexpr (PREV_SLOAD)
+                    wait_vm2<4 + NS>(st.bsc[SB_PREV]);
+                else
+                    wait_vm<4 + NS>();
+                barrier();
+            }
+        }(), ...);
+    }(std::make_integer_sequence<int, 4>{});
+}
+
+// Grid: one workgroup per tile, dealt round-robin over the 8 XCDs by the
+// dispatcher; tile index L = (bid % 8) * per_xcd + bid / 8 gives each XCD a
+// contiguous tile range, walked GROUP_M tile rows at a time so concurrently
+// running workgroups of one XCD share A and B slices in its L2.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 8;
+__device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles, int& mt, int& nt) {
+    const int tiles = mtiles * ntiles;
+    const int per_xcd = (tiles + kXcds - 1) / kXcds;
+    const int L = (bid % kXcds) * per_xcd + bid / kXcds;
+    if (L >= tiles) return false;
+    const int per_group = kGroupM * ntiles;
+    const int g = L / per_group;
+    const int first_m = g * kGroupM;
+    const int gsize = min(kGroupM, mtiles - first_m);
+    const int r = L - g * per_group;
+    mt = first_m + r % gsize;
+    nt = r / gsize;
+    return true;
+}
+
+// Requirements (checked by the launcher): K % 256 == 0; x and w 16-byte
+// aligned; S == K/128 or S == 1; M*K*2, N*K, N*S*4 and (M + 256)*ldy*2
+// below 2^31.  When SWIGLU, N is the number of weight rows (gate rows
+// [0, N/2), up rows [N/2, N)) and y is [M, N/2].
+template <bool SWIGLU>
+__global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __restrict__ x,
+                                                          const uint8_t* __restrict__ w,
+                                                          const float* __restrict__ scales, int S,
+                                                          uint16_t* __restrict__ y, int ldy, int M, int N,
+                                                          int K, int mtiles, int ntiles) {
+    extern __shared__ __align__(16) uint16_t smem[];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+    int mtile, ntile;
+    if (!tile_of(blockIdx.x, mtiles, ntiles, mtile, ntile)) return;
+    const int m0 = mtile * BM;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+    const int KT = K / BK;
+
+    Ctx c;
+    c.dx = make_desc(x, (uint32_t)((int64_t)M * K * 2));
+    c.dw = make_desc(w, (uint32_t)((int64_t)N * K));
+    c.ds = make_desc(scales, (uint32_t)((int64_t)N * S * 4));
+    c.scol = S == 1 ? 0 : 4;
+    // A DMA instruction ii of wave w fills rows 8G..8G+7 (G = 8w + ii) of a
+    // stage: lane -> row 8G + lane/8, LDS slot lane%8 <- chunk slot ^ ga(row).
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) {
+        const int r = 8 * (8 * wave + ii) + (lane >> 3);
+        const int ch = (lane & 7) ^ ga(r);
+        const int m = m0 + r;
+        c.aoff[ii] = m < M ? (uint32_t)((int64_t)m * K * 2 + ch * 16) : kBufferOob;
+    }
+    c.m0a = __builtin_amdgcn_readfirstlane(lds0 + wave * 8 * 1024);
+    // This wave's 64 weight rows: local row rr -> weight row (or -1).
+    auto wrow = [&](int rr) -> int64_t {
+        if constexpr (SWIGLU) {
+            const int D = N >> 1;
+            const int o = ntile * (BN / 2) + wave * (WN / 2) + (rr & 31);
+            return o < D ? (rr < 32 ? (int64_t)o : (int64_t)D + o) : -1;
+        } else {
+            const int64_t n = (int64_t)ntile * BN + wave * WN + rr;
+            return n < N ? n : -1;
+        }
+    };
+    // B DMA instruction gi fills rows 16gi..16gi+15 of a slot: lane -> row
+    // 16gi + lane/4, LDS slot lane%4 <- chunk slot ^ gb(row).
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) {
+        const int rr = 16 * gi + (lane >> 2);
+        const int ch = (lane & 3) ^ gb(rr);
+        const int64_t n = wrow(rr);
+        c.boff[gi] = n >= 0 ? (uint32_t)(n * K + ch * 16) : kBufferOob;
+    }
+    c.m0b = __builtin_amdgcn_readfirstlane(lds0 + A_BYTES + wave * B_WAVE);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int64_t n = wrow(32 * j + l32);
+        c.soff[j] = n >= 0 ? (uint32_t)(n * S * 4) : kBufferOob;
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int ch = 4 * (s >> 1) + 2 * h + (s & 1);
+        c.ard[s] = lds0 + l32 * 128 + 16 * (ch ^ ga(l32));
+    }
+#pragma unroll
+    for (int cp = 0; cp < 2; ++cp)
+        c.brd[cp] = lds0 + A_BYTES + wave * B_WAVE + l32 * 64 + 16 * ((2 * cp + h) ^ gb(l32));
+
+    State st;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st.acc[i][j][r] = 0.0f;
+
+    // ---- prologue: A(0), A(1) into stages 0, 1; B(0..2) into slots 0..2;
+    // scale blocks 0, 1; B(0) dequantized; step 0's first fragments read.
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) dma16(c.m0a + ii * 1024, c.aoff[ii], c.dx, 0);
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) dma16(c.m0a + A_STAGE + ii * 1024, c.aoff[ii], c.dx, BK * 2);
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int gi = 0; gi < 4; ++gi) dma16(c.m0b + p * B_SLOT + gi * 1024, c.boff[gi], c.dw, p * BK);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        buf_load1(st.bsc[0][j], c.soff[j], c.ds, 0);
+        buf_load1(st.bsc[1][j], c.soff[j], c.ds, c.scol);
+    }
+    wait_vm4<0>(st.bsc[0], st.bsc[1]);
+    barrier();
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int cp = 0; cp < 2; ++cp) {
+            ds_read<0>(st.braw[0][j][cp], c.brd[cp] + j * 2048);
+            ds_read<B_SLOT>(st.braw[1][j][cp], c.brd[cp] + j * 2048);
+        }
+    wait_lgkm_braw<0>(st.braw);
+    [&]<int... K2>(std::integer_sequence<int, K2...>) __attribute__((always_inline)) {
+        (dequant_op<K2, 0, 0>(st, st.bsc[0]), ...);
+    }(std::make_integer_sequence<int, 128>{});
+#pragma unroll
+    for (int i = 0; i < MT; ++i) ds_read<0>(st.af[0][i], c.ard[0] + i * 4096);
+    wait_lgkm8<0>(st.af[0]);
+
+    // ---- K loop, 4 steps per iteration; only LDS DMA stays in flight
+    // across the back edge.
+    Ring rg{0u, (uint32_t)A_STAGE, (uint32_t)(2 * A_STAGE), 0u, (uint32_t)(2 * B_SLOT)};
+    for (int kt = 0; kt < KT; kt += 4) {
+        kstep<0>(st, c, rg, kt);
+        rg.advance();
+        kstep<1>(st, c, rg, kt + 1);
+        rg.advance();
+        kstep<2>(st, c, rg, kt + 2);
+        rg.advance();
+        kstep<3>(st, c, rg, kt + 3);
+        rg.advance();
+        // step kt+3 read step kt+4's fragments and B(kt+5) (LDS) and loaded
+        // scale block (kt+6)/2 into bsc[1], followed by 10 DMA.
+        wait_lgkm12<0>(st.af[0], st.braw[1]);
+        wait_vm2<10>(st.bsc[1]);
+    }
+    // The last steps prefetched past K (the next rows, or zeros past the
+    // buffers); their LDS DMA must land before the workgroup's LDS is freed.
+    wait_vm<0>();
+
+    // ---- epilogue: acc[i][j][r] = C[32i + 8(r/4) + 4h + r%4][wave col 32j + l32].
+    // Stores go through a buffer bounded to the M x ldy output: rows >= M fall
+    // outside it and columns past the end get an out-of-range lane offset.
+    const rsrc_t ry = make_rsrc(y, (uint32_t)((int64_t)M * ldy * 2));
+    const int row0 = m0 + 4 * h;
+    if constexpr (SWIGLU) {
+        const int D = N >> 1;
+        const int col = ntile * (BN / 2) + wave * (WN / 2) + l32;
+        const uint32_t voff = col < D ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+                const uint32_t p = pack_bf16x2(f32x2{st.acc[i][0][r], st.acc[i][1][r]});
+                const uint16_t v = swiglu_bf16_bits((uint16_t)(p & 0xffffu), (uint16_t)(p >> 16));
+                __builtin_amdgcn_raw_buffer_store_b16(v, ry, (int)voff, dr * ldy * 2, 0);
+            }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int col = ntile * BN + wave * WN + 32 * j + l32;
+            const uint32_t voff = col < N ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(st.acc[i][j][r]), ry, (int)voff,
+                                                          dr * ldy * 2, 0);
+                }
+        }
+    }
+}
+
+// True when the kernel's requirements hold (see gemm_fp8_kernel).
+inline bool supported(const uint16_t* x, const void* w, int S, int64_t ldy, int64_t M, int64_t N, int64_t K) {
+    const int64_t lim = (int64_t)1 << 31;
+    return K % 256 == 0 && K > 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(w) % 16 == 0 && (S == 1 || S == K / 128) && M * K * 2 < lim &&
+           N * K < lim && N * (int64_t)S * 4 < lim && (M + BM) * ldy * 2 < lim;
+}
+
+}  // namespace gemm_fp8
+}  // namespace fp8lin
