@@ -456,4 +456,12 @@ int fp8lin_stream_read(const void* src, size_t bytes, float* sink, fp8lin_stream
     });
 }
 
+int fp8lin_mfma_ceiling(int64_t iters, float* sink, uint64_t* clocks, fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(sink && clocks && iters > 0, FP8LIN_ERR_ARGUMENT, "mfma_ceiling: bad arguments");
+        ensure_device();
+        check_hip(fp8lin::launch_mfma_ceiling(iters, sink, clocks, as_stream(stream)), "mfma_ceiling launch");
+    });
+}
+
 }  // extern "C"

@@ -227,6 +227,40 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
     if ((threadIdx.x & 63) == 0 && acc == 0x7fc00001u) sink[blockIdx.x] = 1.0f;
 }
 
+// MFMA ceiling: 16 independent 32x32x16 BF16 accumulators per wave, operands
+// in registers, so the loop is bound by MFMA issue alone (32 cycles each).
+__global__ __launch_bounds__(256) void mfma_ceiling_kernel(int64_t iters, float* __restrict__ sink,
+                                                           uint64_t* __restrict__ clocks) {
+    typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+    f32x16 acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+    bf16x8_t a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (__bf16)(0.001f * (float)(threadIdx.x + i));
+        b[i] = (__bf16)(0.002f * (float)i);
+    }
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int64_t it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[i], 0, 0, 0);
+    }
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[i][r];
+    if (s == 1234.5f) sink[0] = s;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        clocks[0] = t1 - t0;
+        clocks[1] = r1 - r0;
+    }
+}
+
 int grid_for(int64_t items, int64_t per_block, int64_t cap) {
     int64_t g = (items + per_block - 1) / per_block;
     if (g < 1) g = 1;
@@ -276,6 +310,15 @@ hipError_t launch_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_
                              hipStream_t stream) {
     hipLaunchKernelGGL(gen_normal_kernel, dim3(grid_for(n, 256, 16384)), dim3(256), 0, stream, seed,
                        tag, first, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_mfma_ceiling(int64_t iters, float* sink, uint64_t* clocks, hipStream_t stream) {
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(mfma_ceiling_kernel, dim3(cus), dim3(256), 0, stream, iters, sink, clocks);
     return hipGetLastError();
 }
 

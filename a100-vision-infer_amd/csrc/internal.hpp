@@ -43,5 +43,6 @@ hipError_t launch_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_
 hipError_t launch_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n,
                              float* out, hipStream_t stream);
 hipError_t launch_stream_read(const void* src, size_t bytes, float* sink, hipStream_t stream);
+hipError_t launch_mfma_ceiling(int64_t iters, float* sink, uint64_t* clocks, hipStream_t stream);
 
 }  // namespace fp8lin

@@ -32,7 +32,7 @@ EXPORTED = [
     "fp8lin_tensor_small_workspace_bytes", "fp8lin_tensor_small", "fp8lin_gemm_bf16",
     "fp8lin_engine_linear_workspace_bytes", "fp8lin_engine_linear",
     "fp8lin_engine_linear_groups", "fp8lin_gen_weights", "fp8lin_gen_activations",
-    "fp8lin_gen_normal", "fp8lin_stream_read",
+    "fp8lin_gen_normal", "fp8lin_stream_read", "fp8lin_mfma_ceiling",
 ]
 
 
@@ -104,6 +104,7 @@ def lib():
         "fp8lin_gen_activations": (i32, [u64, u32, i64, i64, vp, vp]),
         "fp8lin_gen_normal": (i32, [u64, u32, u64, i64, vp, vp]),
         "fp8lin_stream_read": (i32, [vp, sz, vp, vp]),
+        "fp8lin_mfma_ceiling": (i32, [i64, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -205,3 +205,9 @@ def gen_normal(n, seed=0, tag=1, first=0, device="cuda"):
 def stream_read(src, sink):
     check(lib().fp8lin_stream_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink),
                                    _stream(src)))
+
+
+def mfma_ceiling(iters, sink, clocks):
+    """MFMA-ceiling probe: sink float32 [>=1], clocks int64 [2] (shader-clock
+    and 100 MHz ticks of workgroup 0), both on the device."""
+    check(lib().fp8lin_mfma_ceiling(int(iters), _ptr(sink), _ptr(clocks), _stream(sink)))

@@ -46,9 +46,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
-    p.add_argument("--sections", default="gemv,small,prefill,chain,stream",
+    p.add_argument("--sections", default="gemv,small,prefill,chain,stream,ceiling",
                    help="secondary measurements to run (comma list of gemv, small, prefill, "
-                        "chain, stream)")
+                        "chain, stream, ceiling)")
     p.add_argument("--calibrate", action="store_true",
                    help="also run a 256 MiB device copy (known HBM bytes) for counter scaling")
     return p.parse_args()
@@ -314,6 +314,18 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
         extra[f"prefill_swiglu_m{m}_frac"] = round(tflops / BF16_PEAK_TFLOPS, 4)
         log(f"prefill M={m} gate/up+SwiGLU: {ms:.3f} ms {tflops:.1f} TFLOP/s "
             f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of BF16 peak)")
+    # Practical-ceiling reference, not part of the library: the platform's
+    # BF16 GEMM (torch.mm -> hipBLASLt) on the same M=4096 shape with plain
+    # BF16 weights (no dequantization, no SwiGLU epilogue).
+    if "prefill" in sections:
+        m = 4096
+        xa = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
+        wb = torch.randn(k, n, device=dev, dtype=torch.bfloat16)
+        ms = timed(torch, lambda: torch.mm(xa, wb), 10)
+        tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        extra["reference_hipblaslt_bf16_m4096_TFLOPs"] = round(tflops, 1)
+        log(f"reference: torch.mm BF16 (hipBLASLt) M={m} N={n} K={k}: {ms:.3f} ms {tflops:.1f} TFLOP/s")
+        del xa, wb
     if "chain" in sections:
         extra.update(layer_chain(torch, fp8lin, dev, sets[0], log))
     # streaming-read ceiling: 1 GiB and the gate/up weight size
@@ -324,6 +336,25 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
             ms = timed(torch, lambda: ok(L.fp8lin_stream_read(P(buf), nbytes, P(sink), sp)), 50)
             extra[f"stream_read_{label}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
             log(f"stream read {label}: {extra[f'stream_read_{label}_GBs']} GB/s")
+    # MFMA ceiling: register-only BF16 MFMA on every CU for about a second
+    # (the clock settles), then the last launch's rate and shader clock.
+    if "ceiling" in sections:
+        sink = torch.zeros(1, dtype=torch.float32, device=dev)
+        clocks = torch.zeros(2, dtype=torch.int64, device=dev)
+        iters = 20000
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        flop = cus * 4 * iters * 16 * 32768
+        t_end = time.time() + 1.0
+        while True:
+            ms = timed(torch, lambda: ok(L.fp8lin_mfma_ceiling(iters, P(sink), P(clocks), sp)), 1, warm=0)
+            if time.time() > t_end:
+                break
+        c = clocks.cpu().tolist()
+        tflops = flop / (ms * 1e-3) / 1e12
+        extra["mfma_ceiling_TFLOPs"] = round(tflops, 1)
+        extra["mfma_ceiling_clock_MHz"] = round(c[0] / c[1] * 100.0, 0)
+        log(f"MFMA ceiling (register-only BF16 MFMA, {cus} CUs): {tflops:.1f} TFLOP/s "
+            f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of nominal peak) at {c[0] / c[1] * 100.0:.0f} MHz")
     return extra
 
 

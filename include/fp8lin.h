@@ -223,6 +223,15 @@ int fp8lin_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n, fl
  * (>= 4096 floats).  Used to measure the practical HBM read ceiling. */
 int fp8lin_stream_read(const void* src, size_t bytes, float* sink, fp8lin_stream_t stream);
 
+/* MFMA-ceiling probe (no reference counterpart): one workgroup of 4 waves per
+ * CU, each wave issuing iters x 16 independent v_mfma_f32_32x32x16_bf16 on
+ * register operands (no memory traffic).  clocks[0] and clocks[1] receive the
+ * shader-clock (s_memtime) and 100 MHz real-time (s_memrealtime) ticks that
+ * workgroup 0 spent in that loop; sink (1 float) keeps the work alive.  Flops
+ * per launch: CUs x 4 x iters x 16 x 32768.  Used to measure the practical
+ * BF16 MFMA ceiling and the clock it runs at. */
+int fp8lin_mfma_ceiling(int64_t iters, float* sink, uint64_t* clocks, fp8lin_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

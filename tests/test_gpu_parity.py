@@ -341,3 +341,23 @@ def test_prefill_swiglu_shape(fp8lin, gpu, oracle, m):
     xs = bits(x)[rows]
     ref = oracle.swiglu(oracle.linear(xs, codes.cpu().numpy(), scales.cpu().numpy()))
     assert_parity(bits(y)[rows], ref, f"prefill swiglu M={m}", elementwise=False)
+
+
+def test_ceiling_probes(fp8lin, gpu):
+    """The measurement probes run and report: the streaming read touches no
+    sink word for ordinary data, and the MFMA probe's shader-clock ticks match
+    16 MFMAs x 32 cycles per iteration (register-only, so nothing stalls)."""
+    src = torch.arange(1 << 20, dtype=torch.int32, device=gpu)
+    sink = torch.zeros(4096, dtype=torch.float32, device=gpu)
+    fp8lin.stream_read(src, sink)
+    clocks = torch.zeros(2, dtype=torch.int64, device=gpu)
+    one = torch.zeros(1, dtype=torch.float32, device=gpu)
+    iters = 200
+    fp8lin.mfma_ceiling(iters, one, clocks)
+    torch.cuda.synchronize()
+    assert float(sink.abs().sum()) == 0.0
+    assert float(one[0]) == 0.0
+    ticks, rt = clocks.cpu().tolist()
+    assert rt > 0
+    per_mfma = ticks / (iters * 16)
+    assert 31.0 <= per_mfma <= 40.0, per_mfma
