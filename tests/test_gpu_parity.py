@@ -361,3 +361,22 @@ def test_ceiling_probes(fp8lin, gpu):
     assert rt > 0
     per_mfma = ticks / (iters * 16)
     assert 31.0 <= per_mfma <= 40.0, per_mfma
+
+
+def test_swiglu_every_gate_value(fp8lin, gpu, oracle):
+    """All 65536 BF16 gate values a, with u = 1 (so y = g) and with a spread
+    of u: g = bf16(a/(1+exp(-a))) is a function of a's 16 bits, and
+    y = bf16(g*u) rounds an exact FP32 product, so agreeing with the oracle on
+    this set agrees on every input pair (src/optimized.cu:73)."""
+    a = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    rng = np.random.default_rng(7)
+    u_rand = rand_bf16(rng, (65536,), 2.0)
+    for u in (np.full(65536, 0x3F80, np.uint16), u_rand):
+        g = np.concatenate([a, u])[None, :]
+        y = bits(fp8lin.fused_swiglu(up(g, gpu)))[0]
+        ref = oracle.swiglu(g)[0]
+        yf, rf = bf16_to_f32(y), bf16_to_f32(ref)
+        both_nan = np.isnan(yf) & np.isnan(rf)
+        bad = (y != ref) & ~both_nan
+        assert not bad.any(), (f"{int(bad.sum())} of 65536 differ, e.g. a={a[bad][:8]} "
+                               f"got={y[bad][:8]} want={ref[bad][:8]}")
