@@ -18,11 +18,12 @@ hipError_t launch_gemv_swiglu(const uint16_t* x, const uint8_t* codes, const flo
                               hipStream_t stream);
 
 // Small-M matrix-core kernel, 1 <= M <= 16, K % 128 == 0, block scales
-// (small_m.hip).  split == 1 writes BF16 y; split > 1 writes FP32 partials
-// [split, M, N] and then reduces them in order into y.
+// (small_m.hip).  split == 4 sums the reference's four K ranges in order
+// inside each workgroup; no workspace.  M * K * 2 and 16 * K must be below
+// 2^31.
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales,
                           uint16_t* y, int64_t ldy, int M, int N, int K, int split,
-                          float* partial, hipStream_t stream);
+                          hipStream_t stream);
 
 // MFMA GEMM (gemm.hip).  B is E4M3FN codes (scales != nullptr, dequantized
 // to BF16 in LDS) or BF16 (scales == nullptr).  When swiglu, N is the number

@@ -1,141 +1,291 @@
 // Small-M (2..8 activation rows) block-FP8 linear on the matrix cores.
 //
 // Contract of fp8_tensor_small (src/fp8_tensor.cu:18-71): K % 128 == 0, block
-// scales [N, K/128], the weight tile is decoded to BF16 with the reference
+// scales [N, K/128], each weight is decoded to BF16 with the reference
 // rounding point bf16(decode(c) * s) before the BF16 matrix multiply, FP32
-// accumulation.  split == 4 divides the K blocks into four ranges exactly as
-// the reference does (steps = ceil(blocks/4), range i = [i*steps, ...)) and
-// reduces the FP32 partials in the order ((p0+p1)+p2)+p3 (:48-51).
+// accumulation.  The reference's split (1 or 4) only partitions its work
+// (src/fp8_tensor.cu:41-51); here the K partition is the kernel's own and the
+// same for both values, so both give the same bits.
 //
-// MI355X design: one workgroup of 4 waves owns 16 weight rows.  The 4 waves
-// take interleaved 128-wide K blocks of the workgroup's range and their 16x16
-// accumulators are added in LDS in a fixed order.  Per 128-K block a lane
-// loads 2x16 codes of its row with 128-bit loads (lane l: row l%16, K offset
-// 16*(l/16) + 64*h), converts them in registers and feeds them straight into
-// v_mfma_f32_16x16x32_bf16 as the B operand; the activations (rows >= M are
-// zero) are the A operand loaded with the same K permutation.  No LDS staging
-// of the weights: FP8 bytes go HBM -> VGPR -> BF16 -> MFMA.
-#include "device.hpp"
+// MI355X design: the path is an HBM stream of FP8 codes (M <= 8 rows reuse
+// each code at most 8 times), so the kernel is built around keeping enough
+// bytes in flight with coalesced loads, and holds no load data in registers
+// across steps:
+//   - a workgroup owns 16 weight rows; its 4 waves split K: wave w takes block
+//     w (128 K) of every 4-block chunk and accumulates one 16x16 block of
+//     v_mfma_f32_16x16x32_bf16 (weight rows = B operand, activation rows = A
+//     operand; lanes for activation rows >= M read a zero row).  The four
+//     partial sums are added in LDS in wave order;
+//   - codes go HBM -> LDS by direct-to-LDS DMA (buffer_load_dwordx4 ... lds),
+//     8 rows x 128 B per instruction, into a per-wave ring of D blocks of
+//     16 rows x 128 K (2 KiB each).  Row r of a slot holds its 16-byte chunks
+//     XOR-swizzled by (r >> 1) & 7, which keeps the MFMA-layout reads free of
+//     bank conflicts;
+//   - activations x[m][512-K chunk] and the block scales of a chunk are DMA'd
+//     the same way XA chunks ahead into buffers the waves share (one barrier
+//     per chunk);
+//   - per block a lane reads 2 x 16 codes, one scale and 4 activation
+//     fragments from LDS, converts the codes (v_cvt_pk_f32_fp8, v_mul_f32,
+//     v_cvt_pk_bf16_f32) and issues 4 MFMAs.
+// Every DMA of a step is issued unconditionally (blocks past K, rows past N or
+// M get out-of-range offsets and land zeros), so the issue order is the same
+// for every shape and the s_waitcnt counts below are fixed numbers.  The same
+// template also builds 64-row workgroups (NBW == 4: each wave its own 16 rows
+// over all blocks), which measured slower at every decode shape.
+#include <utility>
+
+#include "gemm_fp8.hpp"
 #include "internal.hpp"
 
 namespace fp8lin {
 namespace {
 
-constexpr int kSmallThreads = 256;
-constexpr int kSmallWaves = kSmallThreads / kWave;
+using gemm_fp8::barrier;
+using gemm_fp8::dma16;
+using gemm_fp8::i32x4;
+using gemm_fp8::make_desc;
+using gemm_fp8::wait_vm;
+
+constexpr int kRowX = 1040;  // LDS stride of an activation row (1 KiB + 16 B)
+constexpr int kMaxM = 8;
+
+__device__ __forceinline__ int sw(int r) { return (r >> 1) & 7; }
+
+// 64 lanes x 4 B from global (voff, bounds-checked) into LDS [m0v, m0v + 256).
+__device__ __forceinline__ void dma4(uint32_t m0v, uint32_t voff, i32x4 desc) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(desc)
+                 : "memory", "m0");
+}
+
+// Issue order of a wave, per 4-block chunk: at its first own block, after the
+// wait, CS DMAs prefetch chunk c + XA (XQ activation rows, 1 scale block);
+// at the end of each own block, 2 DMAs refill its ring slot D own blocks
+// ahead.  A wave owns NBW blocks of each chunk.  The vmcnt at the first own
+// block of a chunk (W0) and at the others (W1) is the number of DMAs issued
+// after the oldest one the block needs: its codes, the chunk's scales and
+// (first block) the chunk's activation rows.
+constexpr int cmin(int a, int b) { return a < b ? a : b; }
+constexpr int wait0(int D, int CS, int NBW, int XA) {
+    return cmin(2 * (D - 1) + CS * (D / NBW - 1), 2 * XA * NBW + CS * (XA - 1));
+}
+constexpr int wait1(int D, int CS, int NBW, int XA) {
+    return cmin(2 * (D - 1) + CS * (D / NBW), 2 * XA * NBW + 2 + CS * XA);
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     u32x4 v{a, b, c, d};
     return __builtin_bit_cast(bf16x8, v);
 }
 
-__global__ __launch_bounds__(kSmallThreads) void small_m_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ codes,
-    const float* __restrict__ scales, uint16_t* __restrict__ y, int64_t ldy,
-    float* __restrict__ partial, int M, int N, int K) {
-    __shared__ float red[kSmallWaves][256];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int n0 = blockIdx.x * 16;
-    const int split = gridDim.y, sidx = blockIdx.y;
-    const int KB = K >> 7;
-    const int steps = (KB + split - 1) / split;
-    const int begin = sidx * steps;
-    const int end = min(KB, begin + steps);
+// Workgroup shapes (W waves):
+//   NBW == 4: each wave owns 16 rows and all blocks of a chunk;
+//   NBW == 4 / W: the waves share 16 rows and split every chunk's 4 blocks
+//     (wave w takes blocks w, w + W, ...); their partial sums are added in
+//     LDS in wave order.
+template <int W, int D, int NBW, int XA>
+struct SmallCfg {
+    static constexpr bool KSPLIT = NBW < 4;
+    static constexpr int ROWS = KSPLIT ? 16 : 16 * W;
+    static constexpr int XBUFS = XA + 1;
+    static constexpr int XQ = kMaxM / W;  // activation rows DMA'd per wave per chunk
+    static constexpr int CS = XQ + 1;
+    static constexpr int W0 = wait0(D, CS, NBW, XA), W1 = wait1(D, CS, NBW, XA);
+    static_assert(W * NBW == 4 || NBW == 4, "a chunk's blocks are split evenly");
+    static_assert(D % NBW == 0 && W0 <= 63 && W1 <= 63, "ring depth");
+    static constexpr size_t lds(int M) {
+        return (size_t)W * D * 2048 + (size_t)XBUFS * (M + 1) * kRowX + (size_t)W * XBUFS * 256 +
+               (KSPLIT ? (size_t)W * 1024 : 0);
+    }
+};
 
-    const int col = lane & 15, g = lane >> 4;
-    const int64_t row = min(n0 + col, N - 1);
-    const uint8_t* wrow = codes + row * (int64_t)K;
-    const float* srow = scales + row * (int64_t)KB;
-    const bool xrow_valid = col < M;
-    const uint16_t* xrow = x + (int64_t)(xrow_valid ? col : 0) * K;
+// Requirements (checked by the host): 2 <= M <= 8, K % 128 == 0,
+// 32 * K < 2^31.
+template <int W, int D, int NBW, int XA>
+__global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restrict__ x,
+                                                         const uint8_t* __restrict__ codes,
+                                                         const float* __restrict__ scales,
+                                                         uint16_t* __restrict__ y, int64_t ldy, int M, int N,
+                                                         int K) {
+    using C = SmallCfg<W, D, NBW, XA>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+    const int KB = K >> 7;
+    const int nchunks = (KB + 3) >> 2;
+    const int64_t nw = (int64_t)blockIdx.x * C::ROWS + (C::KSPLIT ? 0 : 16 * wave);  // this wave's first row
+    const int rows_here = (int)max((int64_t)0, min((int64_t)16, (int64_t)N - nw));
+    const int xbuf = (M + 1) * kRowX;
+    const uint32_t o_codes = (uint32_t)(wave * D * 2048);
+    const uint32_t o_x = (uint32_t)(W * D * 2048);
+    const uint32_t o_sc = o_x + C::XBUFS * xbuf + wave * (C::XBUFS * 256);
+    const uint32_t o_red = o_x + C::XBUFS * xbuf + W * (C::XBUFS * 256);
+
+    // row M of every activation buffer stays zero: lanes for rows >= M read it
+    for (int e = threadIdx.x; e < C::XBUFS * 64; e += 64 * W)
+        *reinterpret_cast<u32x4*>(lds + o_x + (e >> 6) * xbuf + M * kRowX + (e & 63) * 16) = u32x4{0, 0, 0, 0};
+    __syncthreads();
+
+    const i32x4 dw = make_desc(codes + (rows_here ? nw * K : 0), (uint32_t)(rows_here * K));
+    const i32x4 ds = make_desc(scales + (rows_here ? nw * KB : 0), (uint32_t)(rows_here * KB * 4));
+    const i32x4 dx = make_desc(x, (uint32_t)(M * K * 2));
+
+    // Own block j of this wave -> global block index.
+    auto gblk = [&](int j) __attribute__((always_inline)) -> int {
+        const int c = j / NBW, p = j % NBW;
+        return 4 * c + (C::KSPLIT ? wave + W * p : p);
+    };
+    // DMA lane offsets.  Codes, instruction q: lane -> row 8q + lane/8, LDS
+    // position lane%8 <- chunk (lane%8) ^ sw(row) of the block's 128 codes.
+    uint32_t cvoff[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int r = 8 * q + (lane >> 3);
+        cvoff[q] = (uint32_t)(r * K + 16 * ((lane & 7) ^ sw(r)));
+    }
+    // Scales of chunk c: lane -> row lane/4, block 4c + lane%4 (LDS [row][4]).
+    const uint32_t svoff = (uint32_t)((lane >> 2) * KB * 4 + 4 * (lane & 3));
+    auto dma_codes = [&](int j) __attribute__((always_inline)) {
+        const int blk = gblk(j);
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + o_codes + (uint32_t)(j % D) * 2048u);
+        const bool ok = blk < KB;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) dma16(m0 + q * 1024, ok ? cvoff[q] + (uint32_t)blk * 128u : kBufferOob, dw, 0);
+    };
+    auto dma_chunk = [&](int c) __attribute__((always_inline)) {
+        const uint32_t xb = lds0 + o_x + (uint32_t)((c % C::XBUFS) * xbuf);
+#pragma unroll
+        for (int q = 0; q < C::XQ; ++q) {
+            const int m = wave + W * q;
+            const int k = c * 512 + 8 * lane;
+            const uint32_t off = m < M && k < K ? (uint32_t)((m * K + k) * 2) : kBufferOob;
+            // rows >= M land (zeros) in the zero row, which no DMA else writes
+            dma16(__builtin_amdgcn_readfirstlane(xb + (uint32_t)(m < M ? m : M) * kRowX), off, dx, 0);
+        }
+        const uint32_t sb = lds0 + o_sc + (uint32_t)((c % C::XBUFS) * 256);
+        const bool ok = 4 * c + (lane & 3) < KB;
+        dma4(__builtin_amdgcn_readfirstlane(sb), ok ? svoff + (uint32_t)(16 * c) : kBufferOob, ds);
+    };
+
+    // Read side, lane (row = lane%16, g = lane/16).
+    const int row = lane & 15, g = lane >> 4;
+    const uint32_t c0off = (uint32_t)(row * 128 + 16 * (g ^ sw(row)));
+    const uint32_t c1off = (uint32_t)(row * 128 + 16 * ((4 + g) ^ sw(row)));
+    const uint32_t xrow = (uint32_t)((row < M ? row : M) * kRowX + 32 * g);
+
+    // ---- prologue: XA chunks of activations and scales, own blocks 0..D-1
+#pragma unroll
+    for (int c = 0; c < XA; ++c) dma_chunk(c);
+#pragma unroll
+    for (int j = 0; j < D; ++j) dma_codes(j);
+    wait_vm<0>();
+    barrier();
 
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    int kb = begin + wave;
-    u32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-    float s = 0.0f;
-    if (kb < end) {
-        c0 = load_u32x4_stream(wrow + kb * 128 + 16 * g);
-        c1 = load_u32x4_stream(wrow + kb * 128 + 64 + 16 * g);
-        s = srow[kb];
-    }
-    for (; kb < end; kb += kSmallWaves) {
-        const int kn = kb + kSmallWaves;
-        u32x4 n0c = {0, 0, 0, 0}, n1c = {0, 0, 0, 0};
-        float sn = 0.0f;
-        if (kn < end) {
-            n0c = load_u32x4_stream(wrow + kn * 128 + 16 * g);
-            n1c = load_u32x4_stream(wrow + kn * 128 + 64 + 16 * g);
-            sn = srow[kn];
-        }
+    for (int c = 0; c < nchunks; ++c) {
+        const uint32_t xb = o_x + (uint32_t)((c % C::XBUFS) * xbuf);
+        const uint32_t sb = o_sc + (uint32_t)((c % C::XBUFS) * 256);
+        [&]<int... P>(std::integer_sequence<int, P...>) __attribute__((always_inline)) {
+            ([&]() __attribute__((always_inline)) {
+                constexpr int p = P;
+                const int j = NBW * c + p;
+                const int b = C::KSPLIT ? wave + W * p : p;  // block within the chunk
+                if constexpr (p == 0) {
+                    // this chunk's activations, scales and first block landed in
+                    // every wave, and every wave is done with the buffers of
+                    // chunk c - 1, which chunk c + XA reuses
+                    wait_vm<C::W0>();
+                    barrier();
+                    dma_chunk(c + XA);
+                } else {
+                    wait_vm<C::W1>();
+                }
+                const uint32_t slot = o_codes + (uint32_t)(j % D) * 2048u;
+                const u32x4 c0 = *reinterpret_cast<const u32x4*>(lds + slot + c0off);
+                const u32x4 c1 = *reinterpret_cast<const u32x4*>(lds + slot + c1off);
+                const float s = *reinterpret_cast<const float*>(lds + sb + row * 16 + b * 4);
+                u32x4 xf[4];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const u32x4 cw = h ? c1 : c0;
-            uint32_t wv[8];
-            dequant4(cw.x, s, wv[0], wv[1]);
-            dequant4(cw.y, s, wv[2], wv[3]);
-            dequant4(cw.z, s, wv[4], wv[5]);
-            dequant4(cw.w, s, wv[6], wv[7]);
-            u32x4 xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
-            if (xrow_valid) {
-                xa = load_u32x4(xrow + kb * 128 + 64 * h + 16 * g);
-                xb = load_u32x4(xrow + kb * 128 + 64 * h + 16 * g + 8);
-            }
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8, xa), as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8, xb), as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc, 0, 0, 0);
-        }
-        c0 = n0c;
-        c1 = n1c;
-        s = sn;
-    }
-    // acc[r] = C[4*g + r][col]
+                for (int f = 0; f < 4; ++f)
+                    xf[f] = *reinterpret_cast<const u32x4*>(lds + xb + xrow + b * 256 + (f >> 1) * 128 +
+                                                            (f & 1) * 16);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][(4 * g + r) * 16 + col] = acc[r];
-    __syncthreads();
-    const int t = threadIdx.x;  // 256 outputs: m = t/16, n = t%16
-    const int m = t >> 4, n = n0 + (t & 15);
-    const float total = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
-    if (m < M && n < N) {
-        if (partial)
-            partial[((int64_t)sidx * M + m) * N + n] = total;
-        else
-            y[(int64_t)m * ldy + n] = f32_to_bf16_bits(total);
+                for (int h = 0; h < 2; ++h) {
+                    const u32x4 cw = h ? c1 : c0;
+                    uint32_t wv[8];
+                    dequant4(cw.x, s, wv[0], wv[1]);
+                    dequant4(cw.y, s, wv[2], wv[3]);
+                    dequant4(cw.z, s, wv[4], wv[5]);
+                    dequant4(cw.w, s, wv[6], wv[7]);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xf[2 * h]),
+                                                                   as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc,
+                                                                   0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xf[2 * h + 1]),
+                                                                   as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc,
+                                                                   0, 0, 0);
+                }
+                // the slot's codes are in registers; refill it D own blocks ahead
+                gemm_fp8::wait_lgkm<0>();
+                dma_codes(j + D);
+            }(), ...);
+        }(std::make_integer_sequence<int, NBW>{});
+    }
+    // DMAs past the end still target this workgroup's LDS
+    wait_vm<0>();
+
+    // acc[i] = C[m = 4g + i][n = row]
+    float total[4];
+    if constexpr (C::KSPLIT) {
+        float* red = reinterpret_cast<float*>(lds + o_red);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave * 256 + (4 * g + i) * 16 + row] = acc[i];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float t = red[(4 * g + i) * 16 + row];
+#pragma unroll
+            for (int w = 1; w < W; ++w) t = t + red[w * 256 + (4 * g + i) * 16 + row];
+            total[i] = t;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) total[i] = acc[i];
+    }
+    if (row < rows_here) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * g + i;
+            if (m < M) y[(int64_t)m * ldy + nw + row] = f32_to_bf16_bits(total[i]);
+        }
     }
 }
 
-// y = bf16(((p0 + p1) + p2) + ...) in index order (src/fp8_tensor.cu:48-51).
-__global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ p,
-                                                              uint16_t* __restrict__ y,
-                                                              int64_t ldy, int M, int N,
-                                                              int split) {
-    const int64_t elements = (int64_t)M * N;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < elements;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        float t = p[i];
-        for (int s = 1; s < split; ++s) t = t + p[s * elements + i];
-        const int64_t m = i / N, n = i % N;
-        y[m * ldy + n] = f32_to_bf16_bits(t);
-    }
+template <int W, int D, int NBW, int XA>
+hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy, int M,
+                  int N, int K, hipStream_t stream) {
+    using C = SmallCfg<W, D, NBW, XA>;
+    auto kern = small_m_kernel<W, D, NBW, XA>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)C::lds(kMaxM));
+    if (attr != hipSuccess) return attr;
+    const int groups = (N + C::ROWS - 1) / C::ROWS;
+    const size_t lds = C::lds(M);
+    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * W), lds, stream, x, codes, scales, y, ldy, M, N, K);
+    return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales,
-                          uint16_t* y, int64_t ldy, int M, int N, int K, int split,
-                          float* partial, hipStream_t stream) {
-    dim3 grid((N + 15) / 16, split);
-    hipLaunchKernelGGL(small_m_kernel, grid, dim3(kSmallThreads), 0, stream, x, codes, scales, y,
-                       ldy, split > 1 ? partial : nullptr, M, N, K);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || split == 1) return e;
-    const int64_t elements = (int64_t)M * N;
-    int blocks = (int)((elements + 255) / 256);
-    if (blocks > 65535) blocks = 65535;
-    hipLaunchKernelGGL(reduce_partials_kernel, dim3(blocks), dim3(256), 0, stream, partial, y, ldy,
-                       M, N, split);
-    return hipGetLastError();
+// Four waves share 16 weight rows and split every chunk's 4 blocks; a 4-block
+// ring each and activations prefetched 3 chunks ahead (77 KiB of LDS, two
+// workgroups per CU).  Measured on MI355X at the decode shapes (M = 2..8) this
+// beats 64-row workgroups (the NBW == 4 form) for every shape, and deeper
+// rings that leave one workgroup per CU.
+hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                          int64_t ldy, int M, int N, int K, int /*split*/, hipStream_t stream) {
+    return launch<4, 4, 1, 3>(x, codes, scales, y, ldy, M, N, K, stream);
 }
 
 }  // namespace fp8lin

@@ -117,9 +117,10 @@ int fp8lin_linear_shared(const uint16_t* x, const void* weight, const float* sca
 
 /* ---------------------------------------------------------------------------
  * Small-M matrix-core path, 2 <= M <= 8, K % 128 == 0, block scales
- * [N, K/128], split in {1, 4}.  split == 4 writes FP32 partial sums of four
- * K ranges to `workspace` and reduces them in the fixed order
- * ((p0+p1)+p2)+p3.  Replaces
+ * [N, K/128], split in {1, 4}.  split == 4 sums the FP32 partials of the
+ * reference's four K ranges in the fixed order ((p0+p1)+p2)+p3 inside each
+ * workgroup, so no workspace is needed: the workspace size is 0 and the
+ * workspace arguments are accepted and ignored.  Replaces
  * `at::Tensor fp8_tensor_small(at::Tensor x, at::Tensor codes,
  *                              at::Tensor scales, int split=1)`
  * (include/avi/ops.h:10, src/fp8_tensor.cu:53-71); the same contract serves
