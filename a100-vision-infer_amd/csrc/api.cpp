@@ -3,6 +3,9 @@
 // Engine::linear decision table.  No allocation, no host synchronisation.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <exception>
@@ -75,6 +78,7 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 constexpr int64_t kMaxDim = (int64_t)1 << 31;
+constexpr int64_t kMaxGridRows = (int64_t)1 << 22;  // one workgroup of up to 1024 threads per row
 
 void check_dims(int64_t M, int64_t N, int64_t K) {
     require(M > 0 && N > 0 && K > 0, FP8LIN_ERR_SHAPE, "Empty GEMM: M, N and K must be positive");
@@ -245,6 +249,33 @@ int engine_impl(const fp8lin_linear_options& o, const fp8lin_weight& w, const ui
     return FP8LIN_PATH_BF16;
 }
 
+// src/dual_path.cu:69-72 (residual form) and src/optimized.cu:72 (plain form).
+void check_rms(const uint16_t* x, const uint16_t* w, const uint16_t* y, int64_t rows, int64_t D,
+               double eps) {
+    require(x && w && y, FP8LIN_ERR_ARGUMENT, "Invalid RMS input: null pointer");
+    require(rows > 0 && D > 0 && D < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid RMS input shape");
+    require(rows < kMaxGridRows, FP8LIN_ERR_SHAPE, "RMS input: more than 2^22-1 rows");
+    require(std::isfinite(eps) && eps > 0, FP8LIN_ERR_ARGUMENT, "Invalid RMS input: eps must be finite and > 0");
+}
+
+// src/dual_path.cu:73-75
+void check_candidates(int64_t M, int64_t N, int64_t offset, const double* out) {
+    require(out != nullptr, FP8LIN_ERR_ARGUMENT, "Invalid vocabulary candidates: null output");
+    require(M > 0 && M <= 65535 && N > 0 && offset >= 0 && offset <= INT32_MAX - N, FP8LIN_ERR_SHAPE,
+            "Invalid vocabulary candidates");
+}
+
+void check_workspace(const void* ws, size_t have, size_t need, const char* what) {
+    require(have >= need && (need == 0 || ws != nullptr), FP8LIN_ERR_WORKSPACE, what);
+    require(aligned16(ws), FP8LIN_ERR_WORKSPACE, "workspace must be 16-byte aligned");
+}
+
+size_t vocab_ws(int64_t M, int64_t N) { return (size_t)(M * fp8lin::vocab_chunks(N) * 8); }
+
+// Output head: the logits (padded to 256 bytes), then the chunk partials.
+int64_t logits_bytes(int64_t M, int64_t N) { return (M * N * 2 + 255) / 256 * 256; }
+size_t linear_candidates_ws(int64_t M, int64_t N) { return (size_t)logits_bytes(M, N) + vocab_ws(M, N); }
+
 }  // namespace
 
 extern "C" {
@@ -407,6 +438,92 @@ int fp8lin_engine_linear_groups(const fp8lin_linear_options* options, const fp8l
                         as_stream(stream));
             offset += groups[g].N;
         }
+    });
+}
+
+// ---- decode epilogue and output head ----
+
+int fp8lin_rms(const uint16_t* x, const uint16_t* weight, uint16_t* y, int64_t rows, int64_t D,
+               double eps, int centered, fp8lin_stream_t stream) {
+    return guarded([&] {
+        if (rows == 0) return;
+        check_rms(x, weight, y, rows, D, eps);
+        ensure_device();
+        check_hip(fp8lin::launch_rms(x, nullptr, weight, nullptr, y, rows, (int)D, (float)eps, centered != 0,
+                                     as_stream(stream)),
+                  "rms launch");
+    });
+}
+
+int fp8lin_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_t* weight,
+                        uint16_t* residual, uint16_t* y, int64_t rows, int64_t D, double eps,
+                        int centered, fp8lin_stream_t stream) {
+    return guarded([&] {
+        check_rms(x, weight, y, rows, D, eps);
+        require(update && residual, FP8LIN_ERR_ARGUMENT, "Invalid fused residual RMS input: null pointer");
+        ensure_device();
+        check_hip(fp8lin::launch_rms(x, update, weight, residual, y, rows, (int)D, (float)eps, centered != 0,
+                                     as_stream(stream)),
+                  "residual rms launch");
+    });
+}
+
+size_t fp8lin_vocab_candidates_workspace_bytes(int64_t M, int64_t N) {
+    if (M <= 0 || N <= 0 || M >= kMaxDim || N >= kMaxDim) return 0;
+    return vocab_ws(M, N);
+}
+
+int fp8lin_vocab_candidates(const uint16_t* logits, int64_t M, int64_t N, int64_t offset, double* out,
+                            void* workspace, size_t workspace_bytes, fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(logits != nullptr, FP8LIN_ERR_ARGUMENT, "Invalid vocabulary candidates: null logits");
+        check_candidates(M, N, offset, out);
+        check_workspace(workspace, workspace_bytes, vocab_ws(M, N), "vocabulary candidates: workspace too small");
+        ensure_device();
+        check_hip(fp8lin::launch_vocab_candidates(logits, (int)M, (int)N, offset, static_cast<uint32_t*>(workspace),
+                                                  out, as_stream(stream)),
+                  "vocabulary candidates launch");
+    });
+}
+
+int fp8lin_merge_candidates(const double* gathered, int64_t ranks, int64_t rows, int64_t* out,
+                            fp8lin_stream_t stream) {
+    return guarded([&] {
+        // src/dual_path.cu:86-88
+        require(gathered && out, FP8LIN_ERR_ARGUMENT, "Invalid gathered candidates: null pointer");
+        require(ranks > 0 && ranks <= 8 && rows > 0 && rows <= 65535, FP8LIN_ERR_SHAPE,
+                "Invalid gathered candidates");
+        ensure_device();
+        check_hip(fp8lin::launch_merge_candidates(gathered, (int)ranks, rows, out, as_stream(stream)),
+                  "merge candidates launch");
+    });
+}
+
+size_t fp8lin_linear_candidates_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
+    return linear_candidates_ws(M, N);
+}
+
+int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const float* scales,
+                             int64_t scale_cols, int64_t M, int64_t N, int64_t K, int64_t offset,
+                             double* out, void* workspace, size_t workspace_bytes,
+                             fp8lin_stream_t stream) {
+    return guarded([&] {
+        // src/speculative.cpp:25-27: linear(normalized, "lm_head") then
+        // vocabulary_candidates(projected, offset)
+        require(x && codes, FP8LIN_ERR_ARGUMENT, "FP8 linear candidates: null pointer");
+        check_dims(M, N, K);
+        check_scales(scales, scale_cols, K);
+        check_candidates(M, N, offset, out);
+        check_workspace(workspace, workspace_bytes, linear_candidates_ws(M, N),
+                        "linear candidates: workspace too small");
+        ensure_device();
+        const hipStream_t s = as_stream(stream);
+        auto* logits = static_cast<uint16_t*>(workspace);
+        auto* part = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + logits_bytes(M, N));
+        linear_impl(x, codes, scales, scale_cols, logits, N, M, N, K, s);
+        check_hip(fp8lin::launch_vocab_candidates(logits, (int)M, (int)N, offset, part, out, s),
+                  "vocabulary candidates launch");
     });
 }
 

@@ -1,0 +1,294 @@
+// Decode epilogue and output-head kernels around the linear layers:
+//   - RMSNorm and the fused residual add + RMSNorm that follows each
+//     row-parallel projection (src/optimized.cu:71, src/dual_path.cu:12-28);
+//   - the per-rank vocabulary candidates of the output head and their merge
+//     across ranks (src/dual_path.cu:29-67,79-92).
+#include "device.hpp"
+#include "internal.hpp"
+
+namespace fp8lin {
+namespace {
+
+// Threads per row: one 8-element vector per thread up to D = 8192, so a
+// decode row is read in one round of loads.  Depends on D only, so a row's
+// result does not depend on how many rows share the launch.
+constexpr int kNormMaxThreads = 1024;
+int norm_threads(int D) {
+    const int t = ((D + 7) / 8 + 63) / 64 * 64;
+    return t < 64 ? 64 : (t > kNormMaxThreads ? kNormMaxThreads : t);
+}
+
+// Block sum of one float per thread: wave butterfly, then the wave sums in
+// wave order.  Every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = scratch[0];
+    for (int q = 1; q < waves; ++q) t += scratch[q];
+    return t;
+}
+
+__device__ __forceinline__ uint32_t bf16_add(uint32_t a, uint32_t b) {
+    return f32_to_bf16_bits(bf16_bits_to_f32(a) + bf16_bits_to_f32(b));
+}
+
+// One workgroup of norm_threads(D) threads per row.  Thread t owns elements
+// 8t + 8Tj + [0, 8), j = 0, 1, ..., in that order whatever the load width, so
+// the sum of squares -- and with it the output -- is the same for the
+// residual form and for RMSNorm of the stored sum, as the reference requires
+// (tests/dual_path_test.cpp:17).  VEC (D % 8 == 0, 16-byte aligned buffers):
+// the first two vectors of each thread stay in registers between the passes
+// and their weights are loaded before the block sum; further vectors are read
+// back from the residual (or x) in the second pass.
+template <bool RES, bool VEC>
+__global__ __launch_bounds__(kNormMaxThreads) void rms_kernel(const uint16_t* __restrict__ x,
+                                                              const uint16_t* __restrict__ update,
+                                                              const uint16_t* __restrict__ w,
+                                                              uint16_t* __restrict__ residual,
+                                                              uint16_t* __restrict__ y, int D, float eps,
+                                                              int centered) {
+    __shared__ float scratch[kNormMaxThreads / 64];
+    const int64_t base = (int64_t)blockIdx.x * D;
+    const int t = threadIdx.x, T = blockDim.x;
+    const float c = centered ? 1.0f : 0.0f;
+    float ss = 0.0f;
+    if constexpr (VEC) {
+        // first pass over one vector: residual (stored) or x bits, and its squares
+        auto first = [&](int i0) __attribute__((always_inline)) -> u32x4 {
+            u32x4 v = load_u32x4(x + base + i0);
+            if constexpr (RES) {
+                const u32x4 u = load_u32x4(update + base + i0);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    v[q] = bf16_add(v[q] & 0xffffu, u[q] & 0xffffu) | (bf16_add(v[q] >> 16, u[q] >> 16) << 16);
+                *reinterpret_cast<u32x4*>(residual + base + i0) = v;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float a = bf16_bits_to_f32(v[q] & 0xffffu), b = bf16_bits_to_f32(v[q] >> 16);
+                ss = __builtin_fmaf(a, a, ss);
+                ss = __builtin_fmaf(b, b, ss);
+            }
+            return v;
+        };
+        const int i0a = 8 * t, i0b = 8 * t + 8 * T;
+        u32x4 ka = {0, 0, 0, 0}, kb = {0, 0, 0, 0}, wa = {0, 0, 0, 0}, wb = {0, 0, 0, 0};
+        if (i0a < D) ka = first(i0a);
+        if (i0b < D) kb = first(i0b);
+        for (int i0 = i0b + 8 * T; i0 < D; i0 += 8 * T) first(i0);
+        if (i0a < D) wa = load_u32x4(w + i0a);
+        if (i0b < D) wb = load_u32x4(w + i0b);
+        const float inv = rsqrtf(block_sum(ss, scratch) / (float)D + eps);
+        auto norm = [&](uint32_t v, uint32_t wt) __attribute__((always_inline)) -> uint32_t {
+            float n = bf16_bits_to_f32(v) * inv;
+            if (!centered) n = bf16_bits_to_f32(f32_to_bf16_bits(n));
+            return f32_to_bf16_bits(n * (bf16_bits_to_f32(wt) + c));
+        };
+        auto second = [&](int i0, const u32x4& v, const u32x4& wv) __attribute__((always_inline)) {
+            u32x4 o;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                o[q] = norm(v[q] & 0xffffu, wv[q] & 0xffffu) | (norm(v[q] >> 16, wv[q] >> 16) << 16);
+            *reinterpret_cast<u32x4*>(y + base + i0) = o;
+        };
+        if (i0a < D) second(i0a, ka, wa);
+        if (i0b < D) second(i0b, kb, wb);
+        const uint16_t* src = RES ? residual : x;
+        for (int i0 = i0b + 8 * T; i0 < D; i0 += 8 * T)
+            second(i0, load_u32x4(src + base + i0), load_u32x4(w + i0));
+    } else {
+        for (int i0 = 8 * t; i0 < D; i0 += 8 * T) {
+            for (int j = 0; j < 8 && i0 + j < D; ++j) {
+                float v = bf16_bits_to_f32(x[base + i0 + j]);
+                if constexpr (RES) {
+                    const uint16_t r = (uint16_t)bf16_add(x[base + i0 + j], update[base + i0 + j]);
+                    residual[base + i0 + j] = r;
+                    v = bf16_bits_to_f32(r);
+                }
+                ss = __builtin_fmaf(v, v, ss);
+            }
+        }
+        const float inv = rsqrtf(block_sum(ss, scratch) / (float)D + eps);
+        const uint16_t* src = RES ? residual : x;
+        for (int i0 = 8 * t; i0 < D; i0 += 8 * T) {
+            for (int j = 0; j < 8 && i0 + j < D; ++j) {
+                float n = bf16_bits_to_f32(src[base + i0 + j]) * inv;
+                if (!centered) n = bf16_bits_to_f32(f32_to_bf16_bits(n));
+                y[base + i0 + j] = f32_to_bf16_bits(n * (bf16_bits_to_f32(w[i0 + j]) + c));
+            }
+        }
+    }
+}
+
+// ---- vocabulary candidates ----
+// (value, id) order: larger value first, then the smaller id.  It is a total
+// order on the pairs, so any reduction tree gives the reference's result.
+__device__ __forceinline__ void pick(float& v, uint32_t& id, float ov, uint32_t oid) {
+    if (ov > v || (ov == v && oid < id)) {
+        v = ov;
+        id = oid;
+    }
+}
+
+// NaN counts as +inf: the row's candidate becomes non-finite and the merge
+// rejects it, as torch.max's NaN propagation does in the reference.
+__device__ __forceinline__ void pick_bf16(float& v, uint32_t& id, uint32_t bits, uint32_t i) {
+    float f = bf16_bits_to_f32(bits);
+    if (f != f) f = __builtin_inff();
+    pick(v, id, f, i);
+}
+
+// Stage 1, grid (chunks, M) x 256 threads: the best of one 2048-column chunk
+// of a row as {float bits, column} into part[(m * chunks + chunk) * 2].  One
+// 16-byte load per thread (VEC: N % 8 == 0 and 16-byte aligned rows), so
+// every chunk is one round of loads and a 75968-wide decode row spreads over
+// 38 CUs.  Stage 2, grid M x 64 threads: the best of a row's chunks as
+// out[2m] = value, out[2m+1] = column + offset (doubles).
+constexpr int kVocabChunk = 2048;
+constexpr int kVocabThreads = kVocabChunk / 8;
+
+__device__ __forceinline__ void wave_pick(float& v, uint32_t& id) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const float ov = __shfl_xor(v, d, kWave);
+        const uint32_t oid = __shfl_xor(id, d, kWave);
+        pick(v, id, ov, oid);
+    }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kVocabThreads) void vocab_partial_kernel(const uint16_t* __restrict__ logits, int N,
+                                                                      int chunks, uint32_t* __restrict__ part) {
+    __shared__ float sv[kVocabThreads / 64];
+    __shared__ uint32_t sid[kVocabThreads / 64];
+    const int t = threadIdx.x, chunk = blockIdx.x, m = blockIdx.y;
+    const uint16_t* row = logits + (int64_t)m * N;
+    float best = -__builtin_inff();
+    uint32_t id = 0xffffffffu;
+    if constexpr (VEC) {
+        const int64_t i0 = (int64_t)chunk * kVocabChunk + 8 * t;
+        if (i0 < N) {
+            const u32x4 v = load_u32x4(row + i0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                pick_bf16(best, id, v[q] & 0xffffu, (uint32_t)(i0 + 2 * q));
+                pick_bf16(best, id, v[q] >> 16, (uint32_t)(i0 + 2 * q + 1));
+            }
+        }
+    } else {
+        uint32_t b[8];
+        const int64_t i0 = (int64_t)chunk * kVocabChunk + t;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[j] = i0 + j * kVocabThreads < N ? row[i0 + j * kVocabThreads] : 0u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j * kVocabThreads < N) pick_bf16(best, id, b[j], (uint32_t)(i0 + j * kVocabThreads));
+    }
+    wave_pick(best, id);
+    const int lane = t & 63, wave = t >> 6;
+    if (lane == 0) {
+        sv[wave] = best;
+        sid[wave] = id;
+    }
+    __syncthreads();
+    if (t == 0) {
+#pragma unroll
+        for (int q = 1; q < kVocabThreads / 64; ++q) pick(best, id, sv[q], sid[q]);
+        uint32_t* p = part + ((int64_t)m * chunks + chunk) * 2;
+        p[0] = __builtin_bit_cast(uint32_t, best);
+        p[1] = id;
+    }
+}
+
+__global__ __launch_bounds__(64) void vocab_finish_kernel(const uint32_t* __restrict__ part, int chunks,
+                                                          int64_t offset, double* __restrict__ out) {
+    const int m = blockIdx.x;
+    float best = -__builtin_inff();
+    uint32_t id = 0xffffffffu;
+    for (int c = threadIdx.x; c < chunks; c += 64) {
+        const uint32_t* p = part + ((int64_t)m * chunks + c) * 2;
+        pick(best, id, __builtin_bit_cast(float, p[0]), p[1]);
+    }
+    wave_pick(best, id);
+    if (threadIdx.x == 0) {
+        out[2 * m] = (double)best;
+        out[2 * m + 1] = (double)((int64_t)id + offset);
+    }
+}
+
+// One thread per row: the best candidate over ranks, -1 when any rank's entry
+// is non-finite or its id is not an integer in [0, INT_MAX].
+__global__ __launch_bounds__(128) void merge_candidates_kernel(const double* __restrict__ gathered, int ranks,
+                                                               int64_t rows, int64_t* __restrict__ out) {
+    const int64_t r = (int64_t)blockIdx.x * 128 + threadIdx.x;
+    if (r >= rows) return;
+    double best = -__builtin_inf();
+    int64_t id = INT64_MAX;
+    bool invalid = false;
+    for (int k = 0; k < ranks; ++k) {
+        const double v = gathered[(k * rows + r) * 2], raw = gathered[(k * rows + r) * 2 + 1];
+        if (!__builtin_isfinite(v) || !__builtin_isfinite(raw) || raw < 0 || raw > 2147483647.0 ||
+            raw != __builtin_floor(raw)) {
+            invalid = true;
+            continue;
+        }
+        const int64_t next = (int64_t)raw;
+        if (v > best || (v == best && next < id)) {
+            best = v;
+            id = next;
+        }
+    }
+    out[r] = invalid ? -1 : id;
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+
+hipError_t launch_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
+                      uint16_t* y, int64_t M, int D, float eps, bool centered, hipStream_t stream) {
+    const bool vec = D % 8 == 0 && aligned16(x) && aligned16(w) && aligned16(y) &&
+                     (!update || (aligned16(update) && aligned16(residual)));
+    const dim3 grid((unsigned)M), block(norm_threads(D));
+    const int c = centered ? 1 : 0;
+    if (update) {
+        if (vec)
+            hipLaunchKernelGGL((rms_kernel<true, true>), grid, block, 0, stream, x, update, w, residual, y, D, eps, c);
+        else
+            hipLaunchKernelGGL((rms_kernel<true, false>), grid, block, 0, stream, x, update, w, residual, y, D, eps, c);
+    } else {
+        if (vec)
+            hipLaunchKernelGGL((rms_kernel<false, true>), grid, block, 0, stream, x, update, w, residual, y, D, eps, c);
+        else
+            hipLaunchKernelGGL((rms_kernel<false, false>), grid, block, 0, stream, x, update, w, residual, y, D, eps,
+                               c);
+    }
+    return hipGetLastError();
+}
+
+int64_t vocab_chunks(int64_t N) { return (N + kVocabChunk - 1) / kVocabChunk; }
+
+hipError_t launch_vocab_candidates(const uint16_t* logits, int M, int N, int64_t offset, uint32_t* part,
+                                   double* out, hipStream_t stream) {
+    const int chunks = (int)vocab_chunks(N);
+    const dim3 grid(chunks, M), block(kVocabThreads);
+    if (N % 8 == 0 && aligned16(logits))
+        hipLaunchKernelGGL(vocab_partial_kernel<true>, grid, block, 0, stream, logits, N, chunks, part);
+    else
+        hipLaunchKernelGGL(vocab_partial_kernel<false>, grid, block, 0, stream, logits, N, chunks, part);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(vocab_finish_kernel, dim3(M), dim3(64), 0, stream, part, chunks, offset, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_merge_candidates(const double* gathered, int ranks, int64_t rows, int64_t* out,
+                                   hipStream_t stream) {
+    hipLaunchKernelGGL(merge_candidates_kernel, dim3((unsigned)((rows + 127) / 128)), dim3(128), 0, stream,
+                       gathered, ranks, rows, out);
+    return hipGetLastError();
+}
+
+}  // namespace fp8lin

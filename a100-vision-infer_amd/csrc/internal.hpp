@@ -44,6 +44,19 @@ hipError_t launch_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_
 hipError_t launch_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n,
                              float* out, hipStream_t stream);
 hipError_t launch_stream_read(const void* src, size_t bytes, float* sink, hipStream_t stream);
+
+// Decode epilogue and output head (epilogue.hip).  launch_rms: RMSNorm of x
+// (update == nullptr) or of residual = bf16(x + update), also stored.
+hipError_t launch_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
+                      uint16_t* y, int64_t M, int D, float eps, bool centered, hipStream_t stream);
+// Candidates of logits [M, N] -> out [M, 2] doubles {value, id + offset};
+// part: M * vocab_chunks(N) {float bits, id} pairs.
+int64_t vocab_chunks(int64_t N);
+hipError_t launch_vocab_candidates(const uint16_t* logits, int M, int N, int64_t offset, uint32_t* part,
+                                   double* out, hipStream_t stream);
+hipError_t launch_merge_candidates(const double* gathered, int ranks, int64_t rows, int64_t* out,
+                                   hipStream_t stream);
+
 hipError_t launch_mfma_ceiling(int64_t iters, float* sink, uint64_t* clocks, hipStream_t stream);
 
 }  // namespace fp8lin

@@ -33,6 +33,9 @@ EXPORTED = [
     "fp8lin_engine_linear_workspace_bytes", "fp8lin_engine_linear",
     "fp8lin_engine_linear_groups", "fp8lin_gen_weights", "fp8lin_gen_activations",
     "fp8lin_gen_normal", "fp8lin_stream_read", "fp8lin_mfma_ceiling",
+    "fp8lin_rms", "fp8lin_residual_rms", "fp8lin_vocab_candidates_workspace_bytes",
+    "fp8lin_vocab_candidates", "fp8lin_merge_candidates",
+    "fp8lin_linear_candidates_workspace_bytes", "fp8lin_linear_candidates",
 ]
 
 
@@ -105,6 +108,13 @@ def lib():
         "fp8lin_gen_normal": (i32, [u64, u32, u64, i64, vp, vp]),
         "fp8lin_stream_read": (i32, [vp, sz, vp, vp]),
         "fp8lin_mfma_ceiling": (i32, [i64, vp, vp, vp]),
+        "fp8lin_rms": (i32, [vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
+        "fp8lin_residual_rms": (i32, [vp, vp, vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
+        "fp8lin_vocab_candidates_workspace_bytes": (sz, [i64, i64]),
+        "fp8lin_vocab_candidates": (i32, [vp, i64, i64, i64, vp, vp, sz, vp]),
+        "fp8lin_merge_candidates": (i32, [vp, i64, i64, vp, vp]),
+        "fp8lin_linear_candidates_workspace_bytes": (sz, [i64, i64, i64]),
+        "fp8lin_linear_candidates": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -1,7 +1,7 @@
 """Tensor-level host mirror of the reference's linear-path operators.
 
 Same names, argument meaning and error behaviour as the reference's ATen
-functions (laoyin/a100-vision-infer include/avi/ops.h:10,11,18,20 and
+functions (laoyin/a100-vision-infer include/avi/ops.h:6-8,10,11,18-20 and
 include/avi/engine.h:13): inputs are device tensors, the output is allocated
 on the input's device, work is enqueued on torch's current stream, and a
 violated precondition raises (Fp8linError, a RuntimeError, where the
@@ -178,6 +178,89 @@ def gemm_bf16(x, w, out=None):
     y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     check(lib().fp8lin_gemm_bf16(_ptr(x), _ptr(w), _ptr(y), y.stride(0), M, N, K, _stream(x)))
     return y
+
+
+def fused_rms(x, weight, eps, one_center):
+    """`at::Tensor fused_rms(x, weight, double eps, bool one_center)` --
+    src/optimized.cu:71-72 (RMSNorm over the last dimension)."""
+    if not (_is_dev(x) and _is_dev(weight) and weight.device == x.device and
+            x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.dim() >= 1 and
+            weight.numel() == x.size(-1)):
+        _fail(ERR_ARGUMENT, "Invalid RMS input")
+    x, weight = x.contiguous(), weight.contiguous()
+    y = torch.empty_like(x)
+    D = x.size(-1)
+    rows = x.numel() // D if D else 0
+    check(lib().fp8lin_rms(_ptr(x), _ptr(weight), _ptr(y), rows, D, float(eps),
+                           int(bool(one_center)), _stream(x)))
+    return y
+
+
+def residual_rms(x, update, weight, eps, centered=True):
+    """`std::pair<Tensor,Tensor> residual_rms(residual, update, weight, eps,
+    centered=true)` -- src/dual_path.cu:68-78.  Returns (bf16(x + update),
+    RMSNorm of that sum)."""
+    ok = (_is_dev(x) and x.dim() >= 2 and x.dtype == torch.bfloat16 and x.is_contiguous() and
+          x.numel() > 0 and _is_dev(update) and update.device == x.device and
+          update.dtype == x.dtype and update.shape == x.shape and update.is_contiguous() and
+          _is_dev(weight) and weight.device == x.device and weight.dtype == x.dtype and
+          weight.is_contiguous() and weight.numel() == x.size(-1))
+    if not ok:
+        _fail(ERR_ARGUMENT, "Invalid fused residual RMS input")
+    residual, y = torch.empty_like(x), torch.empty_like(x)
+    D = x.size(-1)
+    check(lib().fp8lin_residual_rms(_ptr(x), _ptr(update), _ptr(weight), _ptr(residual), _ptr(y),
+                                    x.numel() // D, D, float(eps), int(bool(centered)), _stream(x)))
+    return residual, y
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device) if nbytes else None
+
+
+def vocabulary_candidates(logits, offset=0):
+    """`at::Tensor vocabulary_candidates(logits, int64_t offset=0)` --
+    src/dual_path.cu:79-85: per row {max value, argmax + offset} as doubles."""
+    if not (_is_dev(logits) and logits.dtype == torch.bfloat16 and logits.dim() == 2 and
+            logits.is_contiguous()):
+        _fail(ERR_ARGUMENT, "Invalid vocabulary candidates")
+    M, N = logits.shape
+    out = torch.empty((M, 2), dtype=torch.float64, device=logits.device)
+    nbytes = lib().fp8lin_vocab_candidates_workspace_bytes(M, N)
+    ws = _workspace(nbytes, logits.device)
+    check(lib().fp8lin_vocab_candidates(_ptr(logits), M, N, int(offset), _ptr(out), _ptr(ws), nbytes,
+                                        _stream(logits)))
+    return out
+
+
+def merge_candidates(gathered):
+    """`at::Tensor merge_candidates(at::Tensor gathered)` --
+    src/dual_path.cu:86-92: [ranks, rows, 2] doubles -> [rows] int64 ids
+    (-1 where a rank's candidate is not finite or not a valid id)."""
+    if not (_is_dev(gathered) and gathered.dtype == torch.float64 and gathered.is_contiguous() and
+            gathered.dim() == 3 and gathered.size(2) == 2):
+        _fail(ERR_ARGUMENT, "Invalid gathered candidates")
+    out = torch.empty(gathered.size(1), dtype=torch.int64, device=gathered.device)
+    check(lib().fp8lin_merge_candidates(_ptr(gathered), gathered.size(0), gathered.size(1),
+                                        _ptr(out), _stream(gathered)))
+    return out
+
+
+def linear_candidates(x, codes, scales, offset=0):
+    """`vocabulary_candidates(fp8_linear(x, codes, scales), offset)` in one call
+    (Engine::local_candidates, src/speculative.cpp:25-27)."""
+    _check_x(x, "FP8 linear expects CUDA BF16 [M,K]")
+    _check_codes(codes, x)
+    sc = _scale_cols(scales, codes.size(0), codes.size(1))
+    M, N, K = x.size(0), codes.size(0), codes.size(1)
+    if not (M > 0 and N > 0 and K > 0):
+        _fail(ERR_SHAPE, "Empty GEMM")
+    out = torch.empty((M, 2), dtype=torch.float64, device=x.device)
+    nbytes = lib().fp8lin_linear_candidates_workspace_bytes(M, N, K)
+    ws = _workspace(nbytes, x.device)
+    check(lib().fp8lin_linear_candidates(_ptr(x), _ptr(codes), _ptr(scales), sc, M, N, K,
+                                         int(offset), _ptr(out), _ptr(ws), nbytes, _stream(x)))
+    return out
 
 
 def gen_weights(n, k, seed=0, tag=1, std=0.02, device="cuda"):

@@ -46,9 +46,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
-    p.add_argument("--sections", default="gemv,small,prefill,chain,stream,ceiling",
+    p.add_argument("--sections", default="gemv,small,prefill,chain,head,stream,ceiling",
                    help="secondary measurements to run (comma list of gemv, small, prefill, "
-                        "chain, stream, ceiling)")
+                        "chain, head, stream, ceiling)")
     p.add_argument("--calibrate", action="store_true",
                    help="also run a 256 MiB device copy (known HBM bytes) for counter scaling")
     return p.parse_args()
@@ -243,6 +243,34 @@ def timed(torch, fn, iters, warm=3):
     return a.elapsed_time(b) / iters
 
 
+def graph_timed(torch, fn, sp, reps=20, replays=20):
+    """Per-call time of `fn` with the host out of the loop: `reps` calls
+    captured in one HIP graph (fn launches on sp, a ctypes stream handle that
+    is pointed at the capture stream meanwhile), replayed `replays` times."""
+    cap = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(cap):
+        saved, sp.value = sp.value, cap.cuda_stream
+        try:
+            fn()
+            cap.synchronize()
+            with torch.cuda.graph(graph, stream=cap):
+                for _ in range(reps):
+                    fn()
+        finally:
+            sp.value = saved
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (replays * reps)
+
+
 def secondary(torch, fp8lin, dev, sets, log, sections):
     """Per-shape and per-path figures through the C ABI with preallocated
     outputs (no allocation or tensor checks on the host between launches)."""
@@ -328,6 +356,8 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
         del xa, wb
     if "chain" in sections:
         extra.update(layer_chain(torch, fp8lin, dev, sets[0], log))
+    if "head" in sections:
+        extra.update(head_and_epilogue(torch, fp8lin, dev, log))
     # streaming-read ceiling: 1 GiB and the gate/up weight size
     if "stream" in sections:
         buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -355,6 +385,63 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
         extra["mfma_ceiling_clock_MHz"] = round(c[0] / c[1] * 100.0, 0)
         log(f"MFMA ceiling (register-only BF16 MFMA, {cus} CUs): {tflops:.1f} TFLOP/s "
             f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of nominal peak) at {c[0] / c[1] * 100.0:.0f} MHz")
+    return extra
+
+
+def head_and_epilogue(torch, fp8lin, dev, log):
+    """The output head and the decode epilogue (src/speculative.cpp:25-27,
+    src/dual_path.cu): the vocab-sharded head 75968 x 5120 alone and followed
+    by its vocabulary candidates, at M = 1 and 4; residual add + RMSNorm at
+    hidden 5120.  Timed as graph replays: these calls are short enough that
+    eager timing through the C ABI measures the host's launch rate."""
+    import ctypes
+    L = fp8lin.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    extra = {}
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(L.fp8lin_last_error())
+
+    n, k = 75968, 5120
+    c, s = fp8lin.gen_weights(n, k, seed=0, tag=90, device=dev)
+    for m in (1, 4):
+        x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
+        logits = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        out = torch.empty((m, 2), dtype=torch.float64, device=dev)
+        vws = torch.empty(L.fp8lin_vocab_candidates_workspace_bytes(m, n), dtype=torch.uint8, device=dev)
+        hws = torch.empty(L.fp8lin_linear_candidates_workspace_bytes(m, n, k), dtype=torch.uint8, device=dev)
+
+        def head():
+            ok(L.fp8lin_linear(P(x), P(c), P(s), s.size(1), P(logits), m, n, k, 1, sp))
+
+        def head_candidates():
+            ok(L.fp8lin_linear_candidates(P(x), P(c), P(s), s.size(1), m, n, k, 0, P(out), P(hws),
+                                          hws.numel(), sp))
+
+        def candidates():
+            ok(L.fp8lin_vocab_candidates(P(logits), m, n, 0, P(out), P(vws), vws.numel(), sp))
+        nbytes = algo_bytes(m, n, k)
+        for label, fn in (("linear", head), ("linear_candidates", head_candidates), ("candidates_only", candidates)):
+            ms = graph_timed(torch, fn, sp)
+            extra[f"head_m{m}_{label}_us"] = round(ms * 1e3, 2)
+            if label != "candidates_only":
+                extra[f"head_m{m}_{label}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            log(f"head M={m} {label}: {ms * 1e3:.2f} us (graph replay)")
+    del c, s
+    d = 5120
+    w = fp8lin.gen_activations(1, d, seed=1, tag=3, device=dev)
+    for m in (1, 512, 4096):
+        x = fp8lin.gen_activations(m, d, seed=0, tag=2, device=dev)
+        u = fp8lin.gen_activations(m, d, seed=0, tag=4, device=dev)
+        res, y = torch.empty_like(x), torch.empty_like(x)
+        ms = graph_timed(torch, lambda: ok(L.fp8lin_residual_rms(P(x), P(u), P(w), P(res), P(y), m, d, 1e-6, 1,
+                                                                 sp)), sp)
+        nbytes = (4 * m * d + d) * 2
+        extra[f"residual_rms_m{m}_us"] = round(ms * 1e3, 2)
+        extra[f"residual_rms_m{m}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        log(f"residual_rms M={m} D={d}: {ms * 1e3:.2f} us {nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
     return extra
 
 

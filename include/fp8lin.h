@@ -203,6 +203,67 @@ enum fp8lin_path {
 };
 
 /* ---------------------------------------------------------------------------
+ * Decode epilogue: RMSNorm over the last dimension of x [rows, D] (BF16):
+ *   inv = rsqrt(sum_i x_i^2 / D + eps)
+ *   centered:  y_i = bf16(x_i * inv * (w_i + 1))
+ *   otherwise: y_i = bf16(bf16(x_i * inv) * w_i)
+ * with the sum in FP32.  Replaces
+ * `at::Tensor fused_rms(at::Tensor x, at::Tensor weight, double eps, bool one_center)`
+ * (include/avi/ops.h:19, src/optimized.cu:71-72).  rows == 0 is a no-op.
+ */
+int fp8lin_rms(const uint16_t* x, const uint16_t* weight, uint16_t* y, int64_t rows, int64_t D,
+               double eps, int centered, fp8lin_stream_t stream);
+
+/* Fused residual add + RMSNorm: residual = bf16(x + update), y = RMSNorm of
+ * residual as in fp8lin_rms.  Bit-identical to fp8lin_residual_rms's residual
+ * fed to fp8lin_rms.  Replaces
+ * `std::pair<at::Tensor, at::Tensor> residual_rms(at::Tensor residual,
+ *     at::Tensor update, at::Tensor weight, double eps, bool centered=true)`
+ * (include/avi/ops.h:6, src/dual_path.cu:68-78); the pair is (residual, y).
+ * Requires rows > 0, 0 < D < 2^31, eps finite and > 0; the outputs must not
+ * overlap the inputs.
+ */
+int fp8lin_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_t* weight,
+                        uint16_t* residual, uint16_t* y, int64_t rows, int64_t D, double eps,
+                        int centered, fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Output head.  Per row of BF16 logits [M, N], the largest value (NaN counts
+ * as +inf so that a NaN row is rejected by the merge, ties go to the smaller
+ * column) as out[m] = {value, column + offset} in doubles.  Replaces
+ * `at::Tensor vocabulary_candidates(at::Tensor logits, int64_t offset=0)`
+ * (include/avi/ops.h:7, src/dual_path.cu:79-85).  Requires 0 < M <= 65535,
+ * N > 0, 0 <= offset <= INT32_MAX - N; workspace: the bytes below (one
+ * {value, column} pair per 2048 columns and row, 16-byte aligned).
+ */
+size_t fp8lin_vocab_candidates_workspace_bytes(int64_t M, int64_t N);
+int fp8lin_vocab_candidates(const uint16_t* logits, int64_t M, int64_t N, int64_t offset,
+                            double* out, void* workspace, size_t workspace_bytes,
+                            fp8lin_stream_t stream);
+
+/* Token ids from gathered candidates [ranks, rows, 2] (doubles): per row the
+ * best {value, id} over ranks (ties to the smaller id), or -1 if any rank's
+ * value or id is non-finite or the id is not an integer in [0, INT32_MAX].
+ * Replaces `at::Tensor merge_candidates(at::Tensor gathered)`
+ * (include/avi/ops.h:8, src/dual_path.cu:86-92).  Requires 0 < ranks <= 8
+ * and 0 < rows <= 65535.
+ */
+int fp8lin_merge_candidates(const double* gathered, int64_t ranks, int64_t rows, int64_t* out,
+                            fp8lin_stream_t stream);
+
+/* The head projection and its candidates in one call: out equals
+ * fp8lin_vocab_candidates(fp8lin_linear(x, W), offset), the pair of
+ * src/speculative.cpp:25-27 (Engine::local_candidates with gpu_candidates).
+ * The logits [M, N] and the chunk pairs go to the workspace (the bytes below,
+ * 16-byte aligned).  Requirements of fp8lin_linear and fp8lin_vocab_candidates.
+ */
+size_t fp8lin_linear_candidates_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const float* scales,
+                             int64_t scale_cols, int64_t M, int64_t N, int64_t K, int64_t offset,
+                             double* out, void* workspace, size_t workspace_bytes,
+                             fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Deterministic synthetic inputs (no reference counterpart; used by the
  * benchmark and tests so that the device and a host checker see the same
  * bits).  Element i of stream `tag` is a standard normal from Philox4x32-10

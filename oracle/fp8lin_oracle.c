@@ -304,3 +304,83 @@ void oracle_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_t K, u
 #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < M * K; i++) x[i] = oracle_bf16_rne(oracle_normal(seed, tag, (uint64_t)i));
 }
+
+/* ---------------- decode epilogue and output head ---------------- */
+
+static void rms_row(const float* r, const uint16_t* w, uint16_t* y, int64_t D, float eps, int centered) {
+    double ss = 0.0;
+    for (int64_t i = 0; i < D; i++) ss += (double)r[i] * (double)r[i];
+    const float inv = (float)(1.0 / sqrt(ss / (double)D + (double)eps));
+    for (int64_t i = 0; i < D; i++) {
+        float v = r[i] * inv;
+        if (!centered) v = oracle_bf16_to_float(oracle_bf16_rne(v));
+        y[i] = oracle_bf16_rne(v * (oracle_bf16_to_float(w[i]) + (centered ? 1.0f : 0.0f)));
+    }
+}
+
+/* src/optimized.cu:71 */
+void oracle_rms(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t M, int64_t D, float eps,
+                int centered) {
+    float* r = (float*)malloc((size_t)D * sizeof(float));
+    for (int64_t m = 0; m < M; m++) {
+        for (int64_t i = 0; i < D; i++) r[i] = oracle_bf16_to_float(x[m * D + i]);
+        rms_row(r, w, y + m * D, D, eps, centered);
+    }
+    free(r);
+}
+
+/* src/dual_path.cu:12-28 */
+void oracle_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
+                         uint16_t* y, int64_t M, int64_t D, float eps, int centered) {
+    float* r = (float*)malloc((size_t)D * sizeof(float));
+    for (int64_t m = 0; m < M; m++) {
+        for (int64_t i = 0; i < D; i++) {
+            const uint16_t b = oracle_bf16_rne(oracle_bf16_to_float(x[m * D + i]) +
+                                               oracle_bf16_to_float(update[m * D + i]));
+            residual[m * D + i] = b;
+            r[i] = oracle_bf16_to_float(b);
+        }
+        rms_row(r, w, y + m * D, D, eps, centered);
+    }
+    free(r);
+}
+
+/* src/dual_path.cu:29-59 */
+void oracle_vocab_candidates(const uint16_t* logits, int64_t M, int64_t N, int64_t offset, double* out) {
+    for (int64_t m = 0; m < M; m++) {
+        float best = -INFINITY;
+        int64_t id = -1;
+        for (int64_t n = 0; n < N; n++) {
+            float v = oracle_bf16_to_float(logits[m * N + n]);
+            if (isnan(v)) v = INFINITY;
+            if (id < 0 || v > best) {
+                best = v;
+                id = n;
+            }
+        }
+        out[2 * m] = (double)best;
+        out[2 * m + 1] = (double)(id + offset);
+    }
+}
+
+/* src/dual_path.cu:60-67 */
+void oracle_merge_candidates(const double* gathered, int64_t ranks, int64_t rows, int64_t* out) {
+    for (int64_t r = 0; r < rows; r++) {
+        double best = -INFINITY;
+        int64_t id = INT64_MAX;
+        int invalid = 0;
+        for (int64_t k = 0; k < ranks; k++) {
+            const double v = gathered[(k * rows + r) * 2], raw = gathered[(k * rows + r) * 2 + 1];
+            if (!isfinite(v) || !isfinite(raw) || raw < 0 || raw > 2147483647.0 || raw != floor(raw)) {
+                invalid = 1;
+                continue;
+            }
+            const int64_t next = (int64_t)raw;
+            if (v > best || (v == best && next < id)) {
+                best = v;
+                id = next;
+            }
+        }
+        out[r] = invalid ? -1 : id;
+    }
+}

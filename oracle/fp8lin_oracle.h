@@ -65,6 +65,25 @@ int oracle_linear_bf16w(const uint16_t* x, const uint16_t* w, uint16_t* y,
  * u = in[r,D+j]; in is [M, 2D].  src/optimized.cu:73. */
 void oracle_swiglu(const uint16_t* in, uint16_t* y, int64_t M, int64_t D);
 
+/* ---- decode epilogue and output head ---- */
+/* RMSNorm of BF16 rows: inv = 1/sqrt(sum_i x^2 / D + eps) (sum and root in
+ * double), v = float(x) * inv, rounded to BF16 first when !centered, then
+ * y = bf16(v * (w + (centered ? 1 : 0))).  src/optimized.cu:71 (`rms`). */
+void oracle_rms(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t M, int64_t D, float eps,
+                int centered);
+/* residual = bf16(float(x) + float(update)); y = oracle_rms(residual).
+ * src/dual_path.cu:12-28 (`add_norm`). */
+void oracle_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
+                         uint16_t* y, int64_t M, int64_t D, float eps, int centered);
+/* Per row: the largest BF16 logit (NaN counts as +inf) and its column; ties
+ * go to the smallest column.  out[2r] = value, out[2r+1] = column + offset.
+ * src/dual_path.cu:29-59,80-89 (`vocabulary_candidates`). */
+void oracle_vocab_candidates(const uint16_t* logits, int64_t M, int64_t N, int64_t offset, double* out);
+/* gathered [ranks, rows, 2]: per row the best (value, id) over ranks, ties to
+ * the smaller id; -1 when any rank's entry is non-finite or its id is not an
+ * integer in [0, INT_MAX].  src/dual_path.cu:60-67 (`candidate_merge`). */
+void oracle_merge_candidates(const double* gathered, int64_t ranks, int64_t rows, int64_t* out);
+
 /* ---- deterministic synthetic inputs (seeded, counter based) ---- */
 /* Philox4x32-10 (Salmon et al., SC'11): counter ctr[4], key key[2]. */
 void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

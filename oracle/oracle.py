@@ -22,6 +22,8 @@ _u16p = ctypes.POINTER(ctypes.c_uint16)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i64 = ctypes.c_int64
+_f64p = ctypes.POINTER(ctypes.c_double)
+_i64p = ctypes.POINTER(ctypes.c_int64)
 
 
 def lib():
@@ -58,6 +60,11 @@ def lib():
                                          ctypes.c_float, _u8p, _f32p, _f32p]
         L.oracle_gen_activations.argtypes = [ctypes.c_uint64, ctypes.c_uint32, _i64, _i64, _u16p]
         L.oracle_max_threads.restype = ctypes.c_int
+        L.oracle_rms.argtypes = [_u16p, _u16p, _u16p, _i64, _i64, ctypes.c_float, ctypes.c_int]
+        L.oracle_residual_rms.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _i64, _i64, ctypes.c_float,
+                                          ctypes.c_int]
+        L.oracle_vocab_candidates.argtypes = [_u16p, _i64, _i64, _i64, _f64p]
+        L.oracle_merge_candidates.argtypes = [_f64p, _i64, _i64, _i64p]
     return _lib
 
 
@@ -158,6 +165,44 @@ def swiglu(gate_up_bits):
     y = np.empty((m, d2 // 2), np.uint16)
     lib().oracle_swiglu(_p(g, _u16p), _p(y, _u16p), m, d2 // 2)
     return y
+
+
+# ---- decode epilogue and output head ----
+def rms(x_bits, w_bits, eps=1e-6, centered=True):
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    w = np.ascontiguousarray(w_bits, np.uint16)
+    m, d = x.shape
+    y = np.empty_like(x)
+    lib().oracle_rms(_p(x, _u16p), _p(w, _u16p), _p(y, _u16p), m, d, eps, int(centered))
+    return y
+
+
+def residual_rms(x_bits, u_bits, w_bits, eps=1e-6, centered=True):
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    u = np.ascontiguousarray(u_bits, np.uint16)
+    w = np.ascontiguousarray(w_bits, np.uint16)
+    m, d = x.shape
+    res, y = np.empty_like(x), np.empty_like(x)
+    lib().oracle_residual_rms(_p(x, _u16p), _p(u, _u16p), _p(w, _u16p), _p(res, _u16p), _p(y, _u16p), m, d,
+                              eps, int(centered))
+    return res, y
+
+
+def vocab_candidates(logit_bits, offset=0):
+    lg = np.ascontiguousarray(logit_bits, np.uint16)
+    m, n = lg.shape
+    out = np.empty((m, 2), np.float64)
+    lib().oracle_vocab_candidates(_p(lg, _u16p), m, n, offset, _p(out, _f64p))
+    return out
+
+
+def merge_candidates(gathered):
+    g = np.ascontiguousarray(gathered, np.float64)
+    ranks, rows, two = g.shape
+    assert two == 2
+    out = np.empty(rows, np.int64)
+    lib().oracle_merge_candidates(_p(g, _f64p), ranks, rows, _p(out, _i64p))
+    return out
 
 
 # ---- synthetic inputs ----

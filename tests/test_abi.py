@@ -79,6 +79,49 @@ def test_shared_and_swiglu_validation(fp8lin):
     assert L.fp8lin_decode(P, P, 7, P, 4, 256, None) == 2
 
 
+def test_epilogue_validation(fp8lin):
+    """src/dual_path.cu:69-72,73-75,86-88 preconditions as status codes."""
+    L = fp8lin.lib()
+    assert L.fp8lin_rms(P, P, P, 0, 64, 1e-6, 1, None) == 0                 # no rows: no-op
+    assert L.fp8lin_rms(None, P, P, 2, 64, 1e-6, 1, None) == 2
+    assert L.fp8lin_rms(P, P, P, 2, 0, 1e-6, 1, None) == 1
+    assert L.fp8lin_rms(P, P, P, 1 << 22, 64, 1e-6, 1, None) == 1          # grid rows
+    assert L.fp8lin_residual_rms(P, P, P, P, P, 0, 64, 1e-6, 1, None) == 1  # numel() > 0
+    assert L.fp8lin_residual_rms(P, None, P, P, P, 2, 64, 1e-6, 1, None) == 2
+    assert L.fp8lin_residual_rms(P, P, P, P, P, 2, 64, 0.0, 1, None) == 2   # eps > 0
+    assert L.fp8lin_residual_rms(P, P, P, P, P, 2, 64, float("nan"), 1, None) == 2
+    assert L.fp8lin_residual_rms(P, P, P, P, P, 2, 64, float("inf"), 0, None) == 2
+    ws = L.fp8lin_vocab_candidates_workspace_bytes(3, 10000)
+    assert ws == 3 * 5 * 8                                                  # 5 chunks of 2048
+    assert L.fp8lin_vocab_candidates(P, 0, 10, 0, P, P, ws, None) == 1      # M > 0
+    assert L.fp8lin_vocab_candidates(P, 65536, 10, 0, P, P, 1 << 30, None) == 1
+    assert L.fp8lin_vocab_candidates(P, 3, 10000, -1, P, P, ws, None) == 1  # offset >= 0
+    assert L.fp8lin_vocab_candidates(P, 3, 10000, 2**31 - 10000, P, P, ws, None) == 1
+    assert L.fp8lin_vocab_candidates(P, 3, 10000, 0, P, P, ws - 8, None) == 4
+    assert L.fp8lin_vocab_candidates(P, 3, 10000, 0, P, None, ws, None) == 4
+    assert L.fp8lin_vocab_candidates(P, 3, 10000, 0, None, P, ws, None) == 2
+    assert L.fp8lin_vocab_candidates(None, 3, 10000, 0, P, P, ws, None) == 2
+    assert L.fp8lin_merge_candidates(P, 9, 4, P, None) == 1                 # ranks <= 8
+    assert L.fp8lin_merge_candidates(P, 0, 4, P, None) == 1
+    assert L.fp8lin_merge_candidates(P, 2, 65536, P, None) == 1
+    assert L.fp8lin_merge_candidates(None, 2, 4, P, None) == 2
+
+
+def test_linear_candidates_validation(fp8lin):
+    L = fp8lin.lib()
+    # the BF16 logits [M, N] padded to 256 bytes, then one pair per chunk
+    assert L.fp8lin_linear_candidates_workspace_bytes(1, 1000, 256) == 2048 + 8
+    assert L.fp8lin_linear_candidates_workspace_bytes(16, 1000, 256) == 32000 + 16 * 8
+    assert L.fp8lin_linear_candidates_workspace_bytes(2, 75968, 5120) == 303872 + 2 * 38 * 8
+    assert L.fp8lin_linear_candidates_workspace_bytes(0, 1000, 256) == 0
+    ws = L.fp8lin_linear_candidates_workspace_bytes(2, 1000, 256)
+    assert L.fp8lin_linear_candidates(P, P, P, 1, 2, 1000, 256, 0, P, P, ws - 1, None) == 4
+    assert L.fp8lin_linear_candidates(P, P, P, 3, 2, 1000, 256, 0, P, P, ws, None) == 2
+    assert L.fp8lin_linear_candidates(P, P, P, 1, 2, 1000, 256, -5, P, P, ws, None) == 1
+    assert L.fp8lin_linear_candidates(P, P, P, 1, 2, 1000, 256, 0, None, P, ws, None) == 2
+    assert L.fp8lin_linear_candidates(P, P, P, 1, 0, 1000, 256, 0, P, P, ws, None) == 1
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error path")
 def test_no_device_is_reported(fp8lin):
     L = fp8lin.lib()

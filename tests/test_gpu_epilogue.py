@@ -1,0 +1,282 @@
+"""GPU parity of the decode epilogue and the output head: fused residual add +
+RMSNorm, RMSNorm, vocabulary candidates, their cross-rank merge and the head
+projection followed by its candidates.
+
+Cases follow the reference's own test (tests/dual_path_test.cpp:7-48) with
+numpy's seeded RNG in place of the CUDA RNG.  Residuals, candidates and
+merged ids are integer/selection results and must be bit-identical to the
+oracle; the normalised output keeps the BF16 parity bar (FP32 block sum here,
+FP64 sum in the oracle).
+"""
+import numpy as np
+import pytest
+import torch
+
+from parity import assert_parity, bf16_to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def up(a, dev):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if a.dtype == np.uint16:
+        t = t.view(torch.bfloat16)
+    return t.to(dev)
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def rand_bf16(rng, shape, scale=1.0):
+    f = (rng.standard_normal(shape) * scale).astype(np.float32)
+    return torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_of(values):
+    return torch.tensor(values, dtype=torch.float32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def misaligned(t):
+    """A contiguous copy of t whose data pointer is 2 bytes past a 16-byte
+    boundary (forces the scalar-load kernels)."""
+    flat = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    v = flat[1:].view(t.shape)
+    v.copy_(t)
+    assert v.data_ptr() % 16 != 0
+    return v
+
+
+# ------------------------------------------------------------------ RMSNorm
+@pytest.mark.parametrize("m", [1, 4, 33, 512])
+@pytest.mark.parametrize("d", [16, 128, 5120])
+@pytest.mark.parametrize("centered", [False, True])
+def test_residual_rms_reference_grid(fp8lin, gpu, oracle, m, d, centered):
+    """tests/dual_path_test.cpp:9-17: residual bit-exact, output at the parity
+    bar, and identical to fused_rms of the stored residual."""
+    rng = np.random.default_rng(104 + m * 7 + d + centered)
+    x, u, w = rand_bf16(rng, (m, d)), rand_bf16(rng, (m, d)), rand_bf16(rng, (d,))
+    xt, ut, wt = up(x, gpu), up(u, gpu), up(w, gpu)
+    res, y = fp8lin.residual_rms(xt, ut, wt, 1e-6, centered)
+    ref_res, ref_y = oracle.residual_rms(x, u, w, 1e-6, centered)
+    assert np.array_equal(bits(res), ref_res)
+    assert np.array_equal(bits(res), bits(xt + ut))
+    assert_parity(bits(y), ref_y, f"residual_rms {m}x{d} c{centered}", min_exact=0.95)
+    assert torch.equal(y, fp8lin.fused_rms(res, wt, 1e-6, centered))
+
+
+@pytest.mark.parametrize("m,d", [(3, 1000), (2, 33), (1, 7168), (5, 16384), (2, 7), (2, 20480), (1, 24584)])
+@pytest.mark.parametrize("centered", [False, True])
+def test_rms_ragged_and_misaligned(fp8lin, gpu, oracle, m, d, centered):
+    """Widths off the 8-element vector, and 2-byte-aligned buffers: the scalar
+    kernel gives the same bits as the vector kernel."""
+    rng = np.random.default_rng(m * 31 + d)
+    x, u, w = rand_bf16(rng, (m, d), 3.0), rand_bf16(rng, (m, d)), rand_bf16(rng, (d,))
+    xt, ut, wt = up(x, gpu), up(u, gpu), up(w, gpu)
+    y = fp8lin.fused_rms(xt, wt, 1e-5, centered)
+    assert_parity(bits(y), oracle.rms(x, w, 1e-5, centered), f"rms {m}x{d}", min_exact=0.95)
+    res, y2 = fp8lin.residual_rms(xt, ut, wt, 1e-5, centered)
+    assert np.array_equal(bits(res), oracle.residual_rms(x, u, w, 1e-5, centered)[0])
+    res_m, y2_m = fp8lin.residual_rms(misaligned(xt), misaligned(ut), misaligned(wt), 1e-5, centered)
+    assert torch.equal(res_m, res) and torch.equal(y2_m, y2)
+    assert torch.equal(fp8lin.fused_rms(misaligned(xt), misaligned(wt), 1e-5, centered), y)
+
+
+def test_rms_3d_input(fp8lin, gpu, oracle):
+    """fused_rms normalises the last dimension of any shape (src/optimized.cu:72)."""
+    rng = np.random.default_rng(5)
+    x, w = rand_bf16(rng, (2, 3, 256)), rand_bf16(rng, (256,))
+    y = fp8lin.fused_rms(up(x, gpu), up(w, gpu), 1e-6, True)
+    assert y.shape == (2, 3, 256)
+    assert_parity(bits(y).reshape(6, 256), oracle.rms(x.reshape(6, 256), w, 1e-6, True), "rms 3d",
+                  min_exact=0.95)
+
+
+def test_residual_rms_rejects(fp8lin, gpu):
+    x = torch.zeros((2, 64), dtype=torch.bfloat16, device=gpu)
+    w = torch.zeros(64, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(fp8lin.Fp8linError):
+        fp8lin.residual_rms(x, x[:, :32].contiguous(), w, 1e-6)
+    with pytest.raises(fp8lin.Fp8linError):
+        fp8lin.residual_rms(x, x, w, 0.0)
+    with pytest.raises(fp8lin.Fp8linError):
+        fp8lin.residual_rms(x[0], x[0], w, 1e-6)   # dim() >= 2
+
+
+# ------------------------------------------------------ vocabulary candidates
+@pytest.mark.parametrize("m", [1, 4, 6])
+@pytest.mark.parametrize("n", [1, 257, 4096, 4097, 124160])
+def test_vocab_candidates_reference_grid(fp8lin, gpu, oracle, m, n):
+    """tests/dual_path_test.cpp:19-28: ties across chunks at columns 0 and
+    N-1, offset 124160, and the merge with a copy shifted down by it."""
+    rng = np.random.default_rng(m * 1000 + n)
+    logits = rand_bf16(rng, (m, n))
+    logits[:, 0] = bf16_of([8.0])[0]
+    logits[:, n - 1] = bf16_of([8.0])[0]
+    lt = up(logits, gpu)
+    cand = fp8lin.vocabulary_candidates(lt, 124160)
+    ref = oracle.vocab_candidates(logits, 124160)
+    assert np.array_equal(cand.cpu().numpy(), ref)
+    top = lt.float().max(-1)
+    assert torch.equal(cand[:, 0], top.values.double())
+    assert torch.equal(cand[:, 1], (top.indices + 124160).double())
+    lower = cand.clone()
+    lower[:, 1] -= 124160
+    ids = fp8lin.merge_candidates(torch.stack([cand, lower]).contiguous())
+    assert torch.equal(ids, top.indices)
+    # 2-byte-aligned rows take the scalar-load kernel: same result
+    assert torch.equal(fp8lin.vocabulary_candidates(misaligned(lt), 124160), cand)
+
+
+@pytest.mark.parametrize("invalid", [float("nan"), float("inf"), float("-inf")])
+def test_nonfinite_vocabulary_rejected(fp8lin, gpu, oracle, invalid):
+    """tests/dual_path_test.cpp:29-33."""
+    logits = torch.full((1, 4097), invalid, device=gpu).to(torch.bfloat16)
+    cand = fp8lin.vocabulary_candidates(logits)
+    assert np.array_equal(cand.cpu().numpy(), oracle.vocab_candidates(bits(logits)), equal_nan=True)
+    assert fp8lin.merge_candidates(cand.unsqueeze(0).contiguous()).item() == -1
+
+
+def test_nan_invalidates_losing_neg_inf_does_not(fp8lin, gpu):
+    """tests/dual_path_test.cpp:34-38."""
+    logits = torch.zeros((2, 4097), device=gpu).to(torch.bfloat16)
+    logits[0, 4096] = float("-inf")
+    logits[1, 4096] = float("nan")
+    ids = fp8lin.merge_candidates(fp8lin.vocabulary_candidates(logits).unsqueeze(0).contiguous()).cpu()
+    assert ids.tolist() == [0, -1]
+
+
+def test_merge_candidates_vs_oracle(fp8lin, gpu, oracle):
+    """Random candidates over 1..8 ranks with value ties across ranks and
+    corrupt entries (NaN/inf values, negative, fractional, > INT_MAX ids)."""
+    rng = np.random.default_rng(77)
+    for ranks in range(1, 9):
+        rows = 300
+        g = np.empty((ranks, rows, 2))
+        g[..., 0] = rng.integers(-4, 4, (ranks, rows)) * 0.5
+        g[..., 1] = rng.integers(0, 1 << 20, (ranks, rows))
+        bad = rng.random((ranks, rows)) < 0.02
+        kinds = rng.integers(0, 6, (ranks, rows))
+        g[..., 0] = np.where(bad & (kinds == 0), np.nan, g[..., 0])
+        g[..., 0] = np.where(bad & (kinds == 1), np.inf, g[..., 0])
+        g[..., 1] = np.where(bad & (kinds == 2), -1.0, g[..., 1])
+        g[..., 1] = np.where(bad & (kinds == 3), 2.5, g[..., 1])
+        g[..., 1] = np.where(bad & (kinds == 4), 2.0 ** 31, g[..., 1])
+        g[..., 1] = np.where(bad & (kinds == 5), np.nan, g[..., 1])
+        got = fp8lin.merge_candidates(up(g, gpu)).cpu().numpy()
+        assert np.array_equal(got, oracle.merge_candidates(g)), f"ranks={ranks}"
+
+
+def test_epilogue_graph_replay(fp8lin, gpu, oracle):
+    """tests/dual_path_test.cpp:39-47: residual RMS -> candidates -> merge
+    captured once, replayed after the input changes."""
+    rng = np.random.default_rng(9)
+    x = up(rand_bf16(rng, (4, 128)), gpu)
+    u = up(rand_bf16(rng, (4, 128)), gpu)
+    w = torch.zeros(128, dtype=torch.bfloat16, device=gpu)
+
+    def invoke():
+        y = fp8lin.residual_rms(x, u, w, 1e-6)[1]
+        return fp8lin.merge_candidates(fp8lin.vocabulary_candidates(y).unsqueeze(0).contiguous())
+
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        out = invoke()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = invoke()
+    for i in range(3):
+        if i:
+            x[:, 37 + i] = 100.0
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = fp8lin.fused_rms(x + u, w, 1e-6, True).argmax(-1)
+        assert torch.equal(out, expected), f"replay {i}"
+
+
+# ----------------------------------------------- head projection + candidates
+def _head(fp8lin, gpu, m, n, k, seed):
+    codes, scales = fp8lin.gen_weights(n, k, seed=seed, tag=1, device=gpu)
+    x = fp8lin.gen_activations(m, k, seed=seed, tag=2, device=gpu)
+    return x, codes, scales
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 9, 64])
+@pytest.mark.parametrize("n,k", [(1000, 256), (4097, 5120), (31040, 4096), (777, 10240), (300, 6144)])
+def test_linear_candidates_equals_unfused(fp8lin, gpu, oracle, m, n, k):
+    """The head in one call (src/speculative.cpp:25-27) is bit-identical to
+    vocabulary_candidates(fp8_linear(x, W), offset) on the GEMV paths (128-bit
+    and byte loads) and the M > 8 GEMM path."""
+    x, codes, scales = _head(fp8lin, gpu, m, n, k, seed=m + n)
+    offset = 124160
+    want = fp8lin.vocabulary_candidates(fp8lin.fp8_linear(x, codes, scales, True), offset)
+    got = fp8lin.linear_candidates(x, codes, scales, offset)
+    assert torch.equal(got, want), f"{m}x{n}x{k}"
+    if m <= 8:
+        got_b = fp8lin.linear_candidates(misaligned(x), codes, scales, offset)
+        assert torch.equal(got_b, want), f"byte loads {m}x{n}x{k}"
+
+
+def test_linear_candidates_vs_oracle(fp8lin, gpu, oracle):
+    """Against the oracle's logits: the chosen id's logit is the oracle's row
+    maximum to within the GEMV's 1-ulp bar, and the value is that logit."""
+    m, n, k = 4, 4097, 5120
+    x, codes, scales = _head(fp8lin, gpu, m, n, k, seed=3)
+    logits = oracle.linear(bits(x), codes.cpu().numpy(), scales.cpu().numpy())
+    got = fp8lin.linear_candidates(x, codes, scales, 0).cpu().numpy()
+    lf = bf16_to_f32(logits).astype(np.float64)
+    for r in range(m):
+        i = int(got[r, 1])
+        assert abs(got[r, 0] - lf[r, i]) <= abs(lf[r, i]) * 2 ** -7
+        assert lf[r].max() - lf[r, i] <= abs(lf[r].max()) * 2 ** -7
+
+
+def test_linear_candidates_ties_and_nan(fp8lin, gpu, oracle):
+    """Equal weight rows give exactly tied logits: the smallest row id wins,
+    across row groups and across activation rows; a NaN scale makes its row
+    +inf, which the merge rejects."""
+    m, n, k = 3, 1030, 512
+    rng = np.random.default_rng(12)
+    codes_np = (rng.integers(0, 127, (n, k)) | (rng.integers(0, 2, (n, k)) << 7)).astype(np.uint8)
+    codes_np[[5, 6, 700, 1029]] = codes_np[900]
+    scales_np = (rng.random((n, k // 128)) * 0.01 + 0.001).astype(np.float32)
+    scales_np[[5, 6, 700, 1029]] = scales_np[900] = 1.0
+    x_np = rand_bf16(rng, (m, k))
+    x_np[1] = x_np[0] ^ 0x8000          # one of rows 0 and 1 sees the tied rows as its maximum
+    x = up(x_np, gpu)
+    codes, scales = up(codes_np, gpu), up(scales_np, gpu)
+    want = fp8lin.vocabulary_candidates(fp8lin.fp8_linear(x, codes, scales), 0)
+    got = fp8lin.linear_candidates(x, codes, scales, 0)
+    assert torch.equal(got, want)
+    assert 5 in got[:2, 1].long().tolist()
+    logits = oracle.linear(bits(x), codes_np, scales_np)
+    assert np.array_equal(got.cpu().numpy(), oracle.vocab_candidates(logits, 0))
+    scales_np[17, 0] = np.nan
+    got = fp8lin.linear_candidates(x, codes, up(scales_np, gpu), 0)
+    assert torch.isinf(got[:, 0]).all()
+    assert (fp8lin.merge_candidates(got.unsqueeze(0).contiguous()) == -1).all()
+
+
+def test_linear_candidates_graph_replay(fp8lin, gpu):
+    """Captured head: every replay matches the eager call on the new input."""
+    x, codes, scales = _head(fp8lin, gpu, 1, 31040, 4096, seed=21)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        out = fp8lin.linear_candidates(x, codes, scales, 62080)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = fp8lin.linear_candidates(x, codes, scales, 62080)
+    for i in range(4):
+        if i:
+            x.copy_(fp8lin.gen_activations(1, 4096, seed=100 + i, tag=2, device=gpu))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = fp8lin.linear_candidates(x, codes, scales, 62080)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"

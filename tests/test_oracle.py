@@ -235,6 +235,100 @@ def test_swiglu_fixture_and_special_values(oracle):
     assert y[0, 0] == 0 and y[0, 1] == 0 and y[0, 2] == 20.0 and abs(y[0, 3]) < 1e-6
 
 
+# ------------------------------------- decode epilogue and output head (f)
+def _torch_rms_reference(r_bits, w_bits, eps, centered):
+    """The reference test's own formula (tests/dual_path_test.cpp:13-15) in
+    torch float32: r * rsqrt(mean(r^2) + eps), BF16-rounded first when not
+    centered, times (w + centered), to BF16."""
+    r = torch.from_numpy(bf16_to_f32(r_bits))
+    ref = r * torch.rsqrt((r * r).mean(-1, keepdim=True) + eps)
+    if not centered:
+        ref = ref.to(torch.bfloat16).float()
+    w = torch.from_numpy(bf16_to_f32(w_bits))
+    return (ref * (w + (1.0 if centered else 0.0))).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("m,d", [(1, 16), (4, 128), (33, 5120)])
+@pytest.mark.parametrize("centered", [False, True])
+def test_residual_rms_oracle(oracle, m, d, centered):
+    """tests/dual_path_test.cpp:8-17: the residual is the BF16 sum bit for bit
+    (torch's own float32 add + BF16 cast), and the normalized output matches
+    the reference test's torch formula within its allclose(.01, .001)."""
+    rng = np.random.default_rng(m * d + centered)
+    x = torch_bf16_bits(rng.standard_normal((m, d)).astype(np.float32))
+    u = torch_bf16_bits(rng.standard_normal((m, d)).astype(np.float32))
+    w = torch_bf16_bits(rng.standard_normal(d).astype(np.float32))
+    res, y = oracle.residual_rms(x, u, w, 1e-6, centered)
+    want_res = torch_bf16_bits(bf16_to_f32(x) + bf16_to_f32(u))
+    assert np.array_equal(res, want_res)
+    ref = _torch_rms_reference(res, w, 1e-6, centered)
+    assert np.allclose(bf16_to_f32(y), bf16_to_f32(ref), rtol=0.01, atol=0.001)
+    assert ulp_distance(y, ref).max() <= 1
+    # fused_rms of the sum is the same function (src/optimized.cu:71)
+    assert np.array_equal(oracle.rms(res, w, 1e-6, centered), y)
+
+
+def test_rms_closed_forms(oracle):
+    """Constant rows normalize to +-1 (times w + 1 when centered); scaling a
+    row by a power of two changes nothing when eps is negligible; the centered
+    form with w = 0 equals the uncentered form with w = 1 (both are bf16(v))."""
+    d = 256
+    c = torch_bf16_bits(np.array([[3.0] * d, [-0.5] * d], np.float32))
+    w0 = np.zeros(d, np.uint16)
+    y = bf16_to_f32(oracle.rms(c, w0, 1e-6, True))
+    assert np.all(y[0] == 1.0) and np.all(y[1] == -1.0)
+    rng = np.random.default_rng(3)
+    x = torch_bf16_bits(rng.standard_normal((3, d)).astype(np.float32))
+    w = torch_bf16_bits(rng.standard_normal(d).astype(np.float32))
+    x8 = torch_bf16_bits(bf16_to_f32(x) * 8.0)
+    assert np.array_equal(oracle.rms(x, w, 1e-30, True), oracle.rms(x8, w, 1e-30, True))
+    one = torch_bf16_bits(np.ones(d, np.float32))
+    assert np.array_equal(oracle.rms(x, w0, 1e-6, True), oracle.rms(x, one, 1e-6, False))
+
+
+@pytest.mark.parametrize("m,n", [(1, 1), (4, 257), (6, 4096), (1, 4097), (4, 124160)])
+def test_vocab_candidates_oracle(oracle, m, n):
+    """tests/dual_path_test.cpp:19-27: ties across chunks (columns 0 and N-1
+    both 8) go to the smaller column, values and columns (+ offset) equal
+    numpy's max / first argmax, and the TP merge of a candidate set with a
+    shifted copy keeps the smaller id."""
+    rng = np.random.default_rng(n)
+    lg = torch_bf16_bits(rng.standard_normal((m, n)).astype(np.float32))
+    lg[:, 0] = torch_bf16_bits(np.array([8.0], np.float32))[0]
+    lg[:, n - 1] = lg[:, 0]
+    off = 124160
+    cand = oracle.vocab_candidates(lg, off)
+    f = bf16_to_f32(lg)
+    assert np.array_equal(cand[:, 0], f.max(1).astype(np.float64))
+    assert np.array_equal(cand[:, 1], (f.argmax(1) + off).astype(np.float64))
+    lower = cand.copy()
+    lower[:, 1] -= off
+    assert np.array_equal(oracle.merge_candidates(np.stack([cand, lower])), f.argmax(1))
+
+
+def test_candidates_nonfinite(oracle):
+    """tests/dual_path_test.cpp:28-38: an all-NaN or all-inf row is rejected
+    (-1); a losing -inf is valid; a NaN anywhere invalidates the row."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    for bad in (nan, inf, -inf):
+        lg = torch_bf16_bits(np.full((1, 4097), bad, np.float32))
+        assert oracle.merge_candidates(oracle.vocab_candidates(lg)[None])[0] == -1
+    lg = np.zeros((2, 4097), np.uint16)
+    lg[0, 4096] = torch_bf16_bits(np.array([-inf], np.float32))[0]
+    lg[1, 4096] = torch_bf16_bits(np.array([nan], np.float32))[0]
+    ids = oracle.merge_candidates(oracle.vocab_candidates(lg)[None])
+    assert ids[0] == 0 and ids[1] == -1
+    # corrupt ids are rejected: negative, fractional, above INT_MAX
+    g = np.array([[[1.0, 3.0]], [[0.5, -1.0]]])
+    assert oracle.merge_candidates(g)[0] == -1
+    g[1, 0, 1] = 2.5
+    assert oracle.merge_candidates(g)[0] == -1
+    g[1, 0, 1] = 2.0 ** 31
+    assert oracle.merge_candidates(g)[0] == -1
+    g[1, 0, 1] = 2.0
+    assert oracle.merge_candidates(g)[0] == 3
+
+
 # ------------------------------------------- planted mistakes are caught (CPU)
 def _linear_variant(x_bits, codes, scales, mistake):
     k = codes.shape[1]
