@@ -14,3 +14,4 @@ from .ops import (fp8_decode, fp8_linear, fp8_tensor_small, fused_rms, fused_swi
                   linear_swiglu, merge_candidates, mfma_ceiling, residual_rms,
                   small_linear_shared, stream_read, tilelang_fp8_small, vocabulary_candidates)
 from .engine import LinearEngine, StoredWeight  # noqa: F401
+from .artifact import load_linear_engine, read_manifest, read_tensor  # noqa: F401
