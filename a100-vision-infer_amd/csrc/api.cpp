@@ -168,11 +168,22 @@ bool tensor_small_eligible(const fp8lin_linear_options& o, const fp8lin_weight& 
            w.K % 128 == 0 && w.scale_cols == w.K / 128 && (!o.tilelang_fp8 || w.N % 16 == 0);
 }
 
+// Split-K partials of the FP8 GEMM branch: outputs with few 256x256 tiles
+// (prefill QKV and down projections at M <= 1024) split K over more CUs.
+int engine_splits(const fp8lin_weight& w, int64_t rows, int64_t ldy) {
+    if (rows <= 8 || rows >= kMaxDim) return 1;
+    return fp8lin::gemm_splits((int)w.scale_cols, ldy, (int)rows, (int)w.N, (int)w.K, false);
+}
+size_t split_ws(const fp8lin_weight& w, int64_t rows, int splits) {
+    return splits > 1 ? (size_t)splits * (size_t)rows * (size_t)w.N * 4 : 0;
+}
+
 size_t engine_ws(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t rows) {
     if (tensor_small_eligible(o, w, rows)) return tensor_small_ws(rows, w.N, o.fp8_tensor_split);
     if (o.multi_token_gemv && rows > 1 && rows <= 8) return 0;
     if (w.cached_bf16 && rows > 1) return 0;
-    if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) return 0;
+    // (the split count for ldy = N: a wider ldy never adds splits)
+    if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) return split_ws(w, rows, engine_splits(w, rows, w.N));
     if (w.scales) return dequant_gemm_ws(w.N, w.K);
     return 0;
 }
@@ -225,7 +236,17 @@ int engine_impl(const fp8lin_linear_options& o, const fp8lin_weight& w, const ui
     }
     // :222-224
     if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) {
-        linear_impl(x, codes, w.scales, w.scale_cols, y, ldy, rows, w.N, w.K, stream);
+        const int splits = engine_splits(w, rows, ldy);
+        if (splits > 1) {
+            const size_t need = split_ws(w, rows, splits);
+            require(ws != nullptr && ws_bytes >= need && aligned16(ws), FP8LIN_ERR_WORKSPACE,
+                    "split-K partial workspace missing, too small or unaligned");
+            check_hip(fp8lin::launch_gemm_split(x, codes, w.scales, (int)w.scale_cols, y, ldy, (int)rows,
+                                                (int)w.N, (int)w.K, false, static_cast<float*>(ws), splits, stream),
+                      "fp8 split-K gemm launch");
+        } else {
+            linear_impl(x, codes, w.scales, w.scale_cols, y, ldy, rows, w.N, w.K, stream);
+        }
         return rows <= 8 ? FP8LIN_PATH_FP8_GEMV : FP8LIN_PATH_FP8_GEMM;
     }
     // :225-233, 2048-row BF16 slabs, each GEMM writing its column slice of y.

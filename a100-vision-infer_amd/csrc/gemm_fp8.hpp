@@ -278,16 +278,30 @@ __device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles, int& mt
     return true;
 }
 
+// K range of split s of `splits`: whole 256-K chunks, spread evenly.
+__device__ __forceinline__ void split_range(int K, int s, int splits, int& kbeg, int& klen) {
+    const int chunks = K / 256;
+    const int c0 = (int)((int64_t)s * chunks / splits), c1 = (int)((int64_t)(s + 1) * chunks / splits);
+    kbeg = 256 * c0;
+    klen = 256 * (c1 - c0);
+}
+
 // Requirements (checked by the launcher): K % 256 == 0; x and w 16-byte
 // aligned; S == K/128 or S == 1; M*K*2, N*K, N*S*4 and (M + 256)*ldy*2
 // below 2^31.  When SWIGLU, N is the number of weight rows (gate rows
 // [0, N/2), up rows [N/2, N)) and y is [M, N/2].
-template <bool SWIGLU>
+//
+// PARTIAL (split-K): y is the FP32 partial buffer.  blockIdx.y = s takes
+// split s of `splits` K ranges and writes its sums to (float*)y + s*M*N as
+// [M, N] in weight-row columns (gate and up columns unpaired when SWIGLU);
+// splitk_reduce_kernel adds the splits in order and applies the BF16
+// rounding and the epilogue.  (M + 256)*N*4 < 2^31.
+template <bool SWIGLU, bool PARTIAL = false>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __restrict__ x,
                                                           const uint8_t* __restrict__ w,
                                                           const float* __restrict__ scales, int S,
                                                           uint16_t* __restrict__ y, int ldy, int M, int N,
-                                                          int K, int mtiles, int ntiles) {
+                                                          int K, int mtiles, int ntiles, int splits = 1) {
     extern __shared__ __align__(16) uint16_t smem[];
     const int t = threadIdx.x;
     const int lane = t & 63;
@@ -298,12 +312,17 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
     if (!tile_of(blockIdx.x, mtiles, ntiles, mtile, ntile)) return;
     const int m0 = mtile * BM;
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-    const int KT = K / BK;
+    // This workgroup's K range: the buffers start at kbeg (rows keep the
+    // stride K), so the step offsets below are relative to it.
+    int kbeg = 0, klen = K;
+    if constexpr (PARTIAL) split_range(K, blockIdx.y, splits, kbeg, klen);
+    const int KT = klen / BK;
+    const int sbeg = S == 1 ? 0 : kbeg / 128;
 
     Ctx c;
-    c.dx = make_desc(x, (uint32_t)((int64_t)M * K * 2));
-    c.dw = make_desc(w, (uint32_t)((int64_t)N * K));
-    c.ds = make_desc(scales, (uint32_t)((int64_t)N * S * 4));
+    c.dx = make_desc(x + kbeg, (uint32_t)((int64_t)M * K * 2 - (int64_t)kbeg * 2));
+    c.dw = make_desc(w + kbeg, (uint32_t)((int64_t)N * K - kbeg));
+    c.ds = make_desc(scales + sbeg, (uint32_t)((int64_t)N * S * 4 - (int64_t)sbeg * 4));
     c.scol = S == 1 ? 0 : 4;
     // A DMA instruction ii of wave w fills rows 8G..8G+7 (G = 8w + ii) of a
     // stage: lane -> row 8G + lane/8, LDS slot lane%8 <- chunk slot ^ ga(row).
@@ -414,8 +433,33 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
     // ---- epilogue: acc[i][j][r] = C[32i + 8(r/4) + 4h + r%4][wave col 32j + l32].
     // Stores go through a buffer bounded to the M x ldy output: rows >= M fall
     // outside it and columns past the end get an out-of-range lane offset.
-    const rsrc_t ry = make_rsrc(y, (uint32_t)((int64_t)M * ldy * 2));
     const int row0 = m0 + 4 * h;
+    if constexpr (PARTIAL) {
+        const rsrc_t rp = make_rsrc(reinterpret_cast<float*>(y) + (int64_t)blockIdx.y * M * N,
+                                    (uint32_t)((int64_t)M * N * 4));
+        uint32_t voff[NT];
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const int64_t n = wrow(32 * j + l32);
+            voff[j] = n >= 0 ? (uint32_t)(((int64_t)row0 * N + n) * 4) : kBufferOob;
+        }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    // copy the element first: __builtin_bit_cast of a vector
+                    // element reads element 0 with hipcc (ROCm 7.2)
+                    const float a = st.acc[i][j][r];
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, a), rp, (int)voff[j],
+                                                          dr * N * 4, 0);
+                }
+            }
+        return;
+    }
+    const rsrc_t ry = make_rsrc(y, (uint32_t)((int64_t)M * ldy * 2));
     if constexpr (SWIGLU) {
         const int D = N >> 1;
         const int col = ntile * (BN / 2) + wave * (WN / 2) + l32;
@@ -430,19 +474,23 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
                 __builtin_amdgcn_raw_buffer_store_b16(v, ry, (int)voff, dr * ldy * 2, 0);
             }
     } else {
+        // both accumulator columns of a row at once, in the order the SwiGLU
+        // epilogue reads them (fewer accumulators live at a time)
+        uint32_t voff[NT];
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             const int col = ntile * BN + wave * WN + 32 * j + l32;
-            const uint32_t voff = col < N ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
-                    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(st.acc[i][j][r]), ry, (int)voff,
-                                                          dr * ldy * 2, 0);
-                }
+            voff[j] = col < N ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
         }
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+                const uint32_t p = pack_bf16x2(f32x2{st.acc[i][0][r], st.acc[i][1][r]});
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(p & 0xffffu), ry, (int)voff[0], dr * ldy * 2, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(p >> 16), ry, (int)voff[1], dr * ldy * 2, 0);
+            }
     }
 }
 

@@ -31,6 +31,14 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
 hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, int S,
                        uint16_t* y, int64_t ldy, int M, int N, int K, bool swiglu,
                        hipStream_t stream);
+// Split-K form of the FP8 GEMM for outputs with few tiles: gemm_splits()
+// K ranges (1 = no split) whose FP32 sums go to part (splits * M * N floats,
+// 16-byte aligned), then one reduction launch writes y.  Unaligned x or w
+// run the unsplit GEMM (part unused).
+int gemm_splits(int S, int64_t ldy, int M, int N, int K, bool swiglu);
+hipError_t launch_gemm_split(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
+                             int64_t ldy, int M, int N, int K, bool swiglu, float* part, int splits,
+                             hipStream_t stream);
 
 // Elementwise kernels (elementwise.hip).
 hipError_t launch_dequant(const uint8_t* codes, const float* scales, int64_t S, uint16_t* y,

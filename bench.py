@@ -473,12 +473,25 @@ def layer_chain(torch, fp8lin, dev, ws, log):
                 for name, _, n, _, sw in links}
         feeds = {"qkv_gate": x, "gate_up_swiglu": x, "down": outs["gate_up_swiglu"], "head": outs["down"]}
 
+        # Non-SwiGLU links go through Engine::linear's dispatch (split-K for
+        # the few-tile prefill projections); gate/up through the fused kernel.
+        opt = fp8lin.LinearOptions()
+        recs, wss = {}, {}
+        for name, (c, s), n, k, sw in links:
+            r = fp8lin.Weight()
+            r.data, r.scales, r.scale_cols, r.cached_bf16, r.N, r.K = c.data_ptr(), s.data_ptr(), s.size(1), None, n, k
+            recs[name] = r
+            need = L.fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(r), m)
+            wss[name] = (torch.empty(need, dtype=torch.uint8, device=dev) if need else None, need)
+
         def call(name, w, n, k, sw):
             c, s = w
             if sw:
                 ok(L.fp8lin_linear_swiglu(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k, sp))
             else:
-                ok(L.fp8lin_linear(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k, 1, sp))
+                ws, need = wss[name]
+                ok(L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(recs[name]), P(feeds[name]), m,
+                                          P(outs[name]), n, P(ws) if ws is not None else None, need, None, sp))
 
         def chain():
             for link in links:

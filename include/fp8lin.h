@@ -169,8 +169,10 @@ typedef struct fp8lin_linear_options {
     int shared_gemv_fp8;  /* shared GEMV reads FP8 codes even if a cache exists */
 } fp8lin_linear_options;
 
-/* Workspace needed by fp8lin_engine_linear for this weight and row count
- * (split-K partials or a 2048-row BF16 slab); 0 if none. */
+/* Workspace needed by fp8lin_engine_linear for this weight and row count;
+ * 0 if none.  The FP8 GEMM branch (rows > 8) splits K when the output has at
+ * most 128 tiles of 256x256 and then needs splits * rows * N FP32 partials;
+ * the dequant-then-GEMM branch needs a 2048-row BF16 slab. */
 size_t fp8lin_engine_linear_workspace_bytes(const fp8lin_linear_options* options,
                                             const fp8lin_weight* weight, int64_t rows);
 /* Id of the branch fp8lin_engine_linear takes for this weight, options and

@@ -302,6 +302,75 @@ def test_engine_mixed_groups(fp8lin, gpu, oracle):
         assert_parity(y, sep, f"mixed groups m={m}")
 
 
+# ------------------------------------------------------------ split-K GEMM
+@pytest.mark.parametrize("m,n,k", [(300, 1040, 1024), (33, 520, 2560), (17, 256, 8704), (600, 7168, 512)])
+def test_engine_splitk_gemm(fp8lin, gpu, oracle, m, n, k):
+    """Engine::linear's FP8 GEMM branch (src/engine.cpp:222-224) with few
+    output tiles splits K over more CUs: FP32 partials per K range, added in
+    order by a second launch.  Parity with the oracle, and with the unsplit
+    kernel: only the FP32 summation order differs, so all but outputs next
+    to a rounding boundary (or near zero, where an ulp is tiny) match."""
+    F = fp8lin
+    rng = np.random.default_rng(m + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    eng = F.LinearEngine()
+    eng.add("w.weight", up(codes, gpu), up(scales, gpu))
+    rec = eng._record("w")
+    import ctypes
+    need = F.lib().fp8lin_engine_linear_workspace_bytes(ctypes.byref(eng.options), ctypes.byref(rec), m)
+    tiles = -(-m // 256) * -(-n // 256)
+    splits = 1 if 2 * tiles > 256 else min(256 // tiles, k // 256, 8)
+    assert need == (splits * m * n * 4 if splits > 1 else 0)
+    x = rand_bf16(rng, (m, k))
+    y, path = eng.linear(up(x, gpu), "w", return_path=True)
+    assert path == F.PATH_FP8_GEMM
+    cols = (0, min(n, 600))
+    ref = oracle.linear(x, codes, scales, rows=cols)
+    got = bits(y)
+    assert_parity(got[:, cols[0]:cols[1]], ref[:, cols[0]:cols[1]], f"split-K {m}x{n}x{k}")
+    plain = bits(F.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu)))
+    assert_parity(got, plain, f"split-K vs unsplit {m}x{n}x{k}", min_exact=0.99)
+    assert (ulp_distance(got, plain) <= 1).mean() >= 0.9999
+    # too small a workspace is an error, not a silent fallback
+    if need:
+        y2 = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+        ws = torch.empty(need, dtype=torch.uint8, device=gpu)
+        rc = F.lib().fp8lin_engine_linear(ctypes.byref(eng.options), ctypes.byref(rec),
+                                          ctypes.c_void_p(up(x, gpu).data_ptr()), m, ctypes.c_void_p(y2.data_ptr()),
+                                          n, ctypes.c_void_p(ws.data_ptr()), need - 16, None, stream)
+        assert rc == F.ERR_WORKSPACE
+
+
+def test_engine_splitk_graph_replay(fp8lin, gpu, oracle):
+    """A captured split-K GEMM (two launches) matches eager on every replay."""
+    F = fp8lin
+    rng = np.random.default_rng(5)
+    m, n, k = 64, 768, 2048
+    codes, scales = rand_codes(rng, n, k), (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    eng = F.LinearEngine()
+    eng.add("w.weight", up(codes, gpu), up(scales, gpu))
+    x = up(rand_bf16(rng, (m, k)), gpu)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        out = eng.linear(x, "w")
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = eng.linear(x, "w")
+    for i in range(4):
+        if i:
+            x.copy_(up(rand_bf16(rng, (m, k)), gpu))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = eng.linear(x, "w")
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+
+
 # ------------------------------------------------------------- benchmark shapes
 def test_config1_gemv_seed0(fp8lin, gpu, oracle):
     """Benchmark config 1: M=1, N=K=4096, seed 0, N(0,0.02) weights."""
