@@ -167,6 +167,24 @@ def test_engine_decision_table(fp8lin):
     assert _path(F, O(), _weight(F, scales=False), 4) == F.PATH_BF16
 
 
+def test_engine_splitk_workspace(fp8lin):
+    """FP8 GEMM branch: split-K partials when the output has <= 128 tiles of
+    256x256; splits = min(256 / tiles, K / 256, 8)."""
+    F, O = fp8lin, fp8lin.LinearOptions
+
+    def ws(n, k, rows, **kw):
+        w = _weight(F, n=n, k=k, **kw)
+        return F.lib().fp8lin_engine_linear_workspace_bytes(ctypes.byref(O()), ctypes.byref(w), rows)
+    assert ws(7168, 5120, 512) == 4 * 512 * 7168 * 4      # QKV-gate, 56 tiles
+    assert ws(5120, 8704, 512) == 6 * 512 * 5120 * 4      # down, 40 tiles
+    assert ws(7168, 5120, 1024) == 2 * 1024 * 7168 * 4    # 112 tiles
+    assert ws(17408, 5120, 512) == 0                      # 136 tiles: no split
+    assert ws(256, 512, 20) == 2 * 20 * 256 * 4           # K / 256 = 2 caps the splits
+    assert ws(256, 256, 20) == 0                          # one 256-K chunk
+    assert ws(256, 640, 20) == 0                          # K % 256 != 0: general GEMM
+    assert ws(7168, 5120, 8) == 0                         # GEMV rows
+
+
 def test_engine_validation(fp8lin):
     F = fp8lin
     L = F.lib()
