@@ -17,10 +17,9 @@ hipError_t launch_gemv_swiglu(const uint16_t* x, const uint8_t* codes, const flo
                               uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
                               hipStream_t stream);
 
-// Small-M matrix-core kernel, 1 <= M <= 16, K % 128 == 0, block scales
-// (small_m.hip).  split == 4 sums the reference's four K ranges in order
-// inside each workgroup; no workspace.  M * K * 2 and 16 * K must be below
-// 2^31.
+// Small-M matrix-core kernel, 2 <= M <= 8, K % 128 == 0, block scales
+// (small_m.hip).  The K partition is the kernel's own, so split 1 and 4 give
+// the same bits; no workspace.  M * K * 2 and 16 * K must be below 2^31.
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales,
                           uint16_t* y, int64_t ldy, int M, int N, int K, int split,
                           hipStream_t stream);
