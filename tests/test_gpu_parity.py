@@ -303,7 +303,8 @@ def test_engine_mixed_groups(fp8lin, gpu, oracle):
 
 
 # ------------------------------------------------------------ split-K GEMM
-@pytest.mark.parametrize("m,n,k", [(300, 1040, 1024), (33, 520, 2560), (17, 256, 8704), (600, 7168, 512)])
+@pytest.mark.parametrize("m,n,k", [(300, 1040, 1024), (33, 520, 2560), (17, 256, 8704), (600, 7168, 512),
+                                   (512, 7168, 5120), (512, 5120, 8704)])
 def test_engine_splitk_gemm(fp8lin, gpu, oracle, m, n, k):
     """Engine::linear's FP8 GEMM branch (src/engine.cpp:222-224) with few
     output tiles splits K over more CUs: FP32 partials per K range, added in
