@@ -1,6 +1,7 @@
 """Build the fp8lin HIP library for gfx950 in-tree.
 
-    python a100-vision-infer_amd/build.py        # -> a100-vision-infer_amd/lib/libfp8lin.so
+    python a100-vision-infer_amd/build.py          # -> a100-vision-infer_amd/lib/libfp8lin.so
+    python a100-vision-infer_amd/build.py --aten   # also lib/avi_aten.so (LibTorch shim)
 
 Each source is compiled with hipcc in parallel, then linked into one shared
 library exporting the C ABI of include/fp8lin.h.  Packed FP32 instructions are
@@ -71,5 +72,38 @@ def build(verbose=False, jobs=None):
     return LIB
 
 
+ATEN_SRC = os.path.join(HERE, "aten", "avi_ops.cpp")
+ATEN_LIB = os.path.join(LIBDIR, "avi_aten.so")
+
+
+def build_aten(verbose=False):
+    """The reference's avi:: operators on ROCm LibTorch over the C ABI
+    (aten/avi_ops.cpp), as a Python extension module.  Its fp8lin_* symbols
+    resolve against libfp8lin.so, which fp8lin.aten loads first (global)."""
+    import ctypes
+
+    import torch
+    from torch.utils import cpp_extension
+
+    if not os.path.exists(LIB):
+        raise RuntimeError("build the fp8lin library first")
+    ctypes.CDLL(LIB, mode=ctypes.RTLD_GLOBAL)
+    bdir = os.path.join(OBJ, "aten")
+    shutil.rmtree(bdir, ignore_errors=True)
+    os.makedirs(bdir)
+    tlib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cpp_extension.load(
+        name="avi_aten", sources=[ATEN_SRC], build_directory=bdir, with_cuda=False, verbose=verbose,
+        extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-I{rocm}/include"],
+        extra_ldflags=[f"-L{rocm}/lib", "-lamdhip64", f"-L{tlib}", "-lc10_hip"])
+    tmp = ATEN_LIB + ".tmp"
+    shutil.copyfile(os.path.join(bdir, "avi_aten.so"), tmp)
+    os.replace(tmp, ATEN_LIB)
+    return ATEN_LIB
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    if "--aten" in sys.argv:
+        print(build_aten(verbose="-v" in sys.argv))
