@@ -95,6 +95,22 @@ class LinearEngine:
                 self.decoded_weights[name] = fp8_decode(w.data, w.scale)
                 self.decoded_bytes += nbytes
 
+    @staticmethod
+    def qkv_gate_views(projected, heads, kv_heads, head_dim):
+        """The fused QKV-gate output [T, H*2D + 2*HK*D] split as the reference
+        slices it (src/engine.cpp:279-282): q [T,H,D] and gate [T,H*D] from the
+        per-head [q | gate] rows, k and v [T,HK,D].  q, k and v are views; gate
+        is a reshape of a strided view, which copies, as in the reference."""
+        T, D, H, HK = projected.size(0), head_dim, heads, kv_heads
+        if projected.size(-1) != H * 2 * D + 2 * HK * D:
+            raise Fp8linError(ERR_ARGUMENT, "QKV-gate output width does not match the head layout")
+        qg = projected.narrow(-1, 0, H * 2 * D).reshape(T, H, 2 * D)
+        q = qg.narrow(-1, 0, D)
+        gate = qg.narrow(-1, D, D).reshape(T, H * D)
+        k = projected.narrow(-1, H * 2 * D, HK * D).reshape(T, HK, D)
+        v = projected.narrow(-1, H * 2 * D + HK * D, HK * D).reshape(T, HK, D)
+        return q, gate, k, v
+
     # -- dispatch --------------------------------------------------------------
     def _record(self, name):
         w = self.weights.get(name + ".weight")

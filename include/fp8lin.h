@@ -13,6 +13,10 @@
  *  - BF16 data is passed as uint16_t bit patterns;
  *  - `stream` is a hipStream_t (NULL = the null stream); work is enqueued
  *    on it and is capturable into a HIP graph;
+ *  - a workspace (16-byte aligned device memory of at least the size the
+ *    matching *_workspace_bytes function reports) belongs to the call's
+ *    launches until they complete on `stream`: calls that may run at the same
+ *    time (other streams) need their own workspaces;
  *  - the return value is FP8LIN_OK or one of the FP8LIN_ERR_* codes below;
  *    fp8lin_last_error() gives a message for the calling thread's last
  *    failure.  No C++ exception crosses this boundary.

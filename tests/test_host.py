@@ -60,3 +60,22 @@ def test_operator_checks_raise(fp8lin):
         fp8lin.fused_swiglu(torch.zeros(2, 3, dtype=torch.bfloat16))
     with pytest.raises(fp8lin.Fp8linError):
         fp8lin.fp8_tensor_small(x, codes, scales, split=4)
+
+
+def test_qkv_gate_views(fp8lin):
+    """src/engine.cpp:279-282: q_proj rows are per head [q(D) | gate(D)], then
+    k_proj and v_proj; the fused output splits back into the four parts."""
+    import torch
+    T, H, HK, D = 3, 2, 1, 4
+    q_proj = torch.arange(T * H * 2 * D, dtype=torch.float32).reshape(T, H * 2 * D)
+    k_proj = 1000 + torch.arange(T * HK * D, dtype=torch.float32).reshape(T, HK * D)
+    v_proj = 2000 + torch.arange(T * HK * D, dtype=torch.float32).reshape(T, HK * D)
+    fused = torch.cat([q_proj, k_proj, v_proj], 1)
+    q, gate, k, v = fp8lin.LinearEngine.qkv_gate_views(fused, H, HK, D)
+    per_head = q_proj.reshape(T, H, 2 * D)
+    assert torch.equal(q, per_head[..., :D]) and torch.equal(gate, per_head[..., D:].reshape(T, H * D))
+    assert torch.equal(k, k_proj.reshape(T, HK, D)) and torch.equal(v, v_proj.reshape(T, HK, D))
+    assert q.data_ptr() == fused.data_ptr()
+    import pytest
+    with pytest.raises(fp8lin.Fp8linError):
+        fp8lin.LinearEngine.qkv_gate_views(fused[:, 1:], H, HK, D)
