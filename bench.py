@@ -359,12 +359,23 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
         extra.update(layer_chain(torch, fp8lin, dev, sets[0], log))
     if "head" in sections:
         extra.update(head_and_epilogue(torch, fp8lin, dev, log))
-    # streaming-read ceiling: 1 GiB and the gate/up weight size
+    # streaming-read ceiling: 1 GiB and each decode weight size.  Each launch
+    # reads the next region of a 1 GiB buffer (as the GEMV benchmarks rotate
+    # weight copies), so the reads come from HBM, not the 256 MB Infinity Cache.
     if "stream" in sections:
         buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         sink = torch.zeros(4096, dtype=torch.float32, device=dev)
-        for label, nbytes in (("1GiB", 1 << 30), ("gate_up", 17408 * 5120)):
-            ms = timed(torch, lambda: ok(L.fp8lin_stream_read(P(buf), nbytes, P(sink), sp)), 50)
+        for label, nbytes in (("1GiB", 1 << 30), ("gate_up", 17408 * 5120), ("down", 5120 * 8704),
+                              ("qkv_gate", 7168 * 5120), ("cfg1", 4096 * 4096)):
+            regions = max(1, (1 << 30) // ((nbytes + 4095) // 4096 * 4096))
+            step = (1 << 30) // regions // 4096 * 4096
+            i = [0]
+
+            def read():
+                src = ctypes.c_void_p(buf.data_ptr() + (i[0] % regions) * step)
+                i[0] += 1
+                ok(L.fp8lin_stream_read(src, nbytes, P(sink), sp))
+            ms = graph_timed(torch, read, sp, reps=max(4, 2 * regions), replays=5)
             extra[f"stream_read_{label}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
             log(f"stream read {label}: {extra[f'stream_read_{label}_GBs']} GB/s")
     # MFMA ceiling: register-only BF16 MFMA on every CU for about a second
