@@ -302,6 +302,27 @@ def test_engine_mixed_groups(fp8lin, gpu, oracle):
         assert_parity(y, sep, f"mixed groups m={m}")
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("k", [9344, 10240, 12288])
+def test_gemv_long_k(fp8lin, gpu, oracle, m, k):
+    """K > 9216: the decode GEMV's four-wave step split (and its byte-load
+    form on an unaligned view) against the oracle."""
+    rng = np.random.default_rng(m * 7 + k)
+    n = 300
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s = up(codes, gpu), up(scales, gpu)
+    xg = up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"gemv K={k} m={m}")
+    flat = torch.empty(m * k + 1, dtype=torch.bfloat16, device=gpu)
+    xu = flat[1:].view(m, k)
+    xu.copy_(xg)
+    assert torch.equal(fp8lin.fp8_linear(xu, c, s, True), y)
+
+
 # ------------------------------------------------------------ split-K GEMM
 @pytest.mark.parametrize("m,n,k", [(300, 1040, 1024), (33, 520, 2560), (17, 256, 8704), (600, 7168, 512),
                                    (512, 7168, 5120), (512, 5120, 8704)])
