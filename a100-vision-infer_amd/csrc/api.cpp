@@ -271,12 +271,15 @@ int engine_impl(const fp8lin_linear_options& o, const fp8lin_weight& w, const ui
 }
 
 // src/dual_path.cu:69-72 (residual form) and src/optimized.cu:72 (plain form).
+// Only the residual form checks eps (src/dual_path.cu:72); the plain form
+// takes it as given (src/optimized.cu:72).
 void check_rms(const uint16_t* x, const uint16_t* w, const uint16_t* y, int64_t rows, int64_t D,
-               double eps) {
+               double eps, bool check_eps) {
     require(x && w && y, FP8LIN_ERR_ARGUMENT, "Invalid RMS input: null pointer");
     require(rows > 0 && D > 0 && D < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid RMS input shape");
     require(rows < kMaxGridRows, FP8LIN_ERR_SHAPE, "RMS input: more than 2^22-1 rows");
-    require(std::isfinite(eps) && eps > 0, FP8LIN_ERR_ARGUMENT, "Invalid RMS input: eps must be finite and > 0");
+    require(!check_eps || (std::isfinite(eps) && eps > 0), FP8LIN_ERR_ARGUMENT,
+            "Invalid fused residual RMS input: eps must be finite and > 0");
 }
 
 // src/dual_path.cu:73-75
@@ -468,7 +471,7 @@ int fp8lin_rms(const uint16_t* x, const uint16_t* weight, uint16_t* y, int64_t r
                double eps, int centered, fp8lin_stream_t stream) {
     return guarded([&] {
         if (rows == 0) return;
-        check_rms(x, weight, y, rows, D, eps);
+        check_rms(x, weight, y, rows, D, eps, false);
         ensure_device();
         check_hip(fp8lin::launch_rms(x, nullptr, weight, nullptr, y, rows, (int)D, (float)eps, centered != 0,
                                      as_stream(stream)),
@@ -480,7 +483,7 @@ int fp8lin_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_
                         uint16_t* residual, uint16_t* y, int64_t rows, int64_t D, double eps,
                         int centered, fp8lin_stream_t stream) {
     return guarded([&] {
-        check_rms(x, weight, y, rows, D, eps);
+        check_rms(x, weight, y, rows, D, eps, true);
         require(update && residual, FP8LIN_ERR_ARGUMENT, "Invalid fused residual RMS input: null pointer");
         ensure_device();
         check_hip(fp8lin::launch_rms(x, update, weight, residual, y, rows, (int)D, (float)eps, centered != 0,

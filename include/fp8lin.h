@@ -215,7 +215,8 @@ enum fp8lin_path {
  *   otherwise: y_i = bf16(bf16(x_i * inv) * w_i)
  * with the sum in FP32.  Replaces
  * `at::Tensor fused_rms(at::Tensor x, at::Tensor weight, double eps, bool one_center)`
- * (include/avi/ops.h:19, src/optimized.cu:71-72).  rows == 0 is a no-op.
+ * (include/avi/ops.h:19, src/optimized.cu:71-72).  rows == 0 is a no-op;
+ * eps is used as given (the reference checks it only in the residual form).
  */
 int fp8lin_rms(const uint16_t* x, const uint16_t* weight, uint16_t* y, int64_t rows, int64_t D,
                double eps, int centered, fp8lin_stream_t stream);
