@@ -86,7 +86,7 @@ def test_epilogue_validation(fp8lin):
     assert L.fp8lin_rms(None, P, P, 2, 64, 1e-6, 1, None) == 2
     assert L.fp8lin_rms(P, P, P, 2, 0, 1e-6, 1, None) == 1
     assert L.fp8lin_rms(P, P, P, 1 << 22, 64, 1e-6, 1, None) == 1          # grid rows
-    assert L.fp8lin_rms(P, P, P, 0, 64, 0.0, 1, None) == 0                  # eps unchecked here
+    assert L.fp8lin_rms(P, P, P, 0, 64, 0.0, 1, None) == 0                  # no rows: no-op, any eps
     assert L.fp8lin_residual_rms(P, P, P, P, P, 0, 64, 1e-6, 1, None) == 1  # numel() > 0
     assert L.fp8lin_residual_rms(P, None, P, P, P, 2, 64, 1e-6, 1, None) == 2
     assert L.fp8lin_residual_rms(P, P, P, P, P, 2, 64, 0.0, 1, None) == 2   # eps > 0
