@@ -551,6 +551,44 @@ int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const floa
     });
 }
 
+size_t engine_candidates_ws(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t rows) {
+    const size_t head = (size_t)logits_bytes(rows, w.N) + (vocab_ws(rows, w.N) + 255) / 256 * 256;
+    return head + engine_ws(o, w, rows);
+}
+
+size_t fp8lin_engine_linear_candidates_workspace_bytes(const fp8lin_linear_options* options,
+                                                       const fp8lin_weight* weight, int64_t rows) {
+    if (!options || !weight || rows <= 0 || weight->N <= 0 || rows >= kMaxDim || weight->N >= kMaxDim) return 0;
+    return engine_candidates_ws(*options, *weight, rows);
+}
+
+int fp8lin_engine_linear_candidates(const fp8lin_linear_options* options, const fp8lin_weight* weight,
+                                    const uint16_t* x, int64_t rows, int64_t offset, double* out,
+                                    void* workspace, size_t workspace_bytes, int* path_out,
+                                    fp8lin_stream_t stream) {
+    return guarded([&] {
+        // src/speculative.cpp:25-27 with gpu_candidates: Engine::linear(normalized,
+        // "lm_head"), then vocabulary_candidates(projected, offset)
+        require(options && weight, FP8LIN_ERR_ARGUMENT, "Engine linear candidates: null options or weight");
+        require(x != nullptr, FP8LIN_ERR_ARGUMENT, "Engine linear: null pointer");
+        check_dims(rows, weight->N, weight->K);
+        check_candidates(rows, weight->N, offset, out);
+        check_workspace(workspace, workspace_bytes, engine_candidates_ws(*options, *weight, rows),
+                        "engine linear candidates: workspace too small");
+        char* base = static_cast<char*>(workspace);
+        auto* logits = reinterpret_cast<uint16_t*>(base);
+        auto* part = reinterpret_cast<uint32_t*>(base + logits_bytes(rows, weight->N));
+        const size_t head = (size_t)logits_bytes(rows, weight->N) + (vocab_ws(rows, weight->N) + 255) / 256 * 256;
+        validate_engine(*options, *weight, x, rows, logits, weight->N);
+        ensure_device();
+        const hipStream_t s = as_stream(stream);
+        const int path = engine_impl(*options, *weight, x, rows, logits, weight->N, base + head, workspace_bytes - head, s);
+        check_hip(fp8lin::launch_vocab_candidates(logits, (int)rows, (int)weight->N, offset, part, out, s),
+                  "vocabulary candidates launch");
+        if (path_out) *path_out = path;
+    });
+}
+
 int fp8lin_gen_weights(uint64_t seed, uint32_t tag, int64_t N, int64_t K, float std_dev,
                        uint8_t* codes, float* scales, fp8lin_stream_t stream) {
     return guarded([&] {

@@ -36,6 +36,7 @@ EXPORTED = [
     "fp8lin_rms", "fp8lin_residual_rms", "fp8lin_vocab_candidates_workspace_bytes",
     "fp8lin_vocab_candidates", "fp8lin_merge_candidates",
     "fp8lin_linear_candidates_workspace_bytes", "fp8lin_linear_candidates",
+    "fp8lin_engine_linear_candidates_workspace_bytes", "fp8lin_engine_linear_candidates",
 ]
 
 
@@ -115,6 +116,10 @@ def lib():
         "fp8lin_merge_candidates": (i32, [vp, i64, i64, vp, vp]),
         "fp8lin_linear_candidates_workspace_bytes": (sz, [i64, i64, i64]),
         "fp8lin_linear_candidates": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, sz, vp]),
+        "fp8lin_engine_linear_candidates_workspace_bytes": (sz, [ctypes.POINTER(LinearOptions),
+                                                                 ctypes.POINTER(Weight), i64]),
+        "fp8lin_engine_linear_candidates": (i32, [ctypes.POINTER(LinearOptions), ctypes.POINTER(Weight), vp,
+                                                  i64, i64, vp, vp, sz, ctypes.POINTER(ctypes.c_int), vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

@@ -132,6 +132,25 @@ class LinearEngine:
             self._workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
         return self._workspace
 
+    def local_candidates(self, x, name="lm_head", offset=0, return_path=False):
+        """`Engine::local_candidates` with gpu_candidates (src/speculative.cpp:25-27):
+        the projection through this engine's dispatch, then per row the
+        {max value, argmax + offset} pair as doubles [rows, 2]."""
+        rows = x.numel() // x.size(-1)
+        x2 = x.reshape(rows, x.size(-1)).contiguous()
+        rec = self._record(name)
+        opt = self.options
+        out = torch.empty((rows, 2), dtype=torch.float64, device=x.device)
+        need = lib().fp8lin_engine_linear_candidates_workspace_bytes(ctypes.byref(opt), ctypes.byref(rec), rows)
+        ws = self._ws(need, x.device)
+        path = ctypes.c_int(0)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        check(lib().fp8lin_engine_linear_candidates(
+            ctypes.byref(opt), ctypes.byref(rec), ctypes.c_void_p(x2.data_ptr()), rows, int(offset),
+            ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()) if ws is not None else None, need,
+            ctypes.byref(path), stream))
+        return (out, path.value) if return_path else out
+
     def linear(self, x, name, return_path=False):
         """`Engine::linear(x, name)` without reduce/bias (src/engine.cpp:196-242)."""
         rows = x.numel() // x.size(-1)

@@ -434,8 +434,22 @@ def head_and_epilogue(torch, fp8lin, dev, log):
 
         def candidates():
             ok(L.fp8lin_vocab_candidates(P(logits), m, n, 0, P(out), P(vws), vws.numel(), sp))
+        # Engine::local_candidates with the small-M matrix-core option
+        # (src/engine.cpp:206-213): the head at rows 2..8 on that path
+        topt = fp8lin.LinearOptions(fp8_tensor_small=True)
+        rec = fp8lin.Weight()
+        rec.data, rec.scales, rec.scale_cols, rec.cached_bf16, rec.N, rec.K = c.data_ptr(), s.data_ptr(), s.size(1), None, n, k
+        ews_n = L.fp8lin_engine_linear_candidates_workspace_bytes(ctypes.byref(topt), ctypes.byref(rec), m)
+        ews = torch.empty(max(ews_n, 16), dtype=torch.uint8, device=dev)
+
+        def engine_candidates():
+            ok(L.fp8lin_engine_linear_candidates(ctypes.byref(topt), ctypes.byref(rec), P(x), m, 0, P(out), P(ews),
+                                                 ews_n, None, sp))
         nbytes = algo_bytes(m, n, k)
-        for label, fn in (("linear", head), ("linear_candidates", head_candidates), ("candidates_only", candidates)):
+        paths = [("linear", head), ("linear_candidates", head_candidates), ("candidates_only", candidates)]
+        if m > 1:
+            paths.append(("tensor_small_candidates", engine_candidates))
+        for label, fn in paths:
             ms = graph_timed(torch, fn, sp)
             extra[f"head_m{m}_{label}_us"] = round(ms * 1e3, 2)
             if label != "candidates_only":

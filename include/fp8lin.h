@@ -270,6 +270,20 @@ int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const floa
                              double* out, void* workspace, size_t workspace_bytes,
                              fp8lin_stream_t stream);
 
+/* The head projection through Engine::linear's dispatch, then its candidates:
+ * Engine::local_candidates with gpu_candidates (src/speculative.cpp:25-27).
+ * out equals fp8lin_vocab_candidates of fp8lin_engine_linear's output for
+ * the same options (so rows 2..8 take the small-M path when the options
+ * select it).  Workspace: the bytes below (the logits, the candidate pairs
+ * and the branch's own workspace), 16-byte aligned.
+ */
+size_t fp8lin_engine_linear_candidates_workspace_bytes(const fp8lin_linear_options* options,
+                                                       const fp8lin_weight* weight, int64_t rows);
+int fp8lin_engine_linear_candidates(const fp8lin_linear_options* options, const fp8lin_weight* weight,
+                                    const uint16_t* x, int64_t rows, int64_t offset, double* out,
+                                    void* workspace, size_t workspace_bytes, int* path_out,
+                                    fp8lin_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Deterministic synthetic inputs (no reference counterpart; used by the
  * benchmark and tests so that the device and a host checker see the same

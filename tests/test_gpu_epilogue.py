@@ -280,3 +280,29 @@ def test_linear_candidates_graph_replay(fp8lin, gpu):
         want = fp8lin.linear_candidates(x, codes, scales, 62080)
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {i}"
+
+
+@pytest.mark.parametrize("rows", [1, 4, 9])
+@pytest.mark.parametrize("opts", ["default", "tensor_small", "cached"])
+def test_engine_local_candidates(fp8lin, gpu, rows, opts):
+    """Engine::local_candidates (src/speculative.cpp:25-27) through the engine's
+    dispatch: bit-identical to vocabulary_candidates of Engine::linear's output
+    on every branch the options select."""
+    n, k = 4112, 5120
+    codes, scales = fp8lin.gen_weights(n, k, seed=31, tag=1, device=gpu)
+    opt = fp8lin.LinearOptions(fp8_tensor_small=(opts == "tensor_small"))
+    eng = fp8lin.LinearEngine(opt, weight_cache_bytes=(1 << 30) if opts == "cached" else 0)
+    eng.add("lm_head.weight", codes, scales)
+    if opts == "cached":
+        eng.build_cache()
+    x = fp8lin.gen_activations(rows, k, seed=rows, tag=2, device=gpu)
+    got, path = eng.local_candidates(x, "lm_head", 62080, return_path=True)
+    y, path2 = eng.linear(x, "lm_head", return_path=True)
+    assert path == path2
+    if opts == "tensor_small" and rows == 4:
+        assert path == fp8lin.PATH_TENSOR_SMALL
+    if opts == "cached" and rows > 1:
+        assert path == fp8lin.PATH_CACHED_BF16
+    assert torch.equal(got, fp8lin.vocabulary_candidates(y, 62080))
+    if opts == "default":
+        assert torch.equal(got, fp8lin.linear_candidates(x, codes, scales, 62080))
