@@ -492,6 +492,20 @@ int fp8lin_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_
     });
 }
 
+int fp8lin_reduce_residual_rms(const uint16_t* x, const uint16_t* partials, int64_t ranks,
+                               const uint16_t* weight, uint16_t* residual, uint16_t* y, int64_t rows,
+                               int64_t D, double eps, int centered, fp8lin_stream_t stream) {
+    return guarded([&] {
+        check_rms(x, weight, y, rows, D, eps, true);
+        require(partials && residual, FP8LIN_ERR_ARGUMENT, "Invalid reduce + residual RMS input: null pointer");
+        require(ranks >= 1 && ranks <= 8, FP8LIN_ERR_SHAPE, "Invalid reduce + residual RMS input: 1..8 ranks");
+        ensure_device();
+        check_hip(fp8lin::launch_reduce_rms(x, partials, (int)ranks, weight, residual, y, rows, (int)D, (float)eps,
+                                            centered != 0, as_stream(stream)),
+                  "reduce residual rms launch");
+    });
+}
+
 size_t fp8lin_vocab_candidates_workspace_bytes(int64_t M, int64_t N) {
     if (M <= 0 || N <= 0 || M >= kMaxDim || N >= kMaxDim) return 0;
     return vocab_ws(M, N);

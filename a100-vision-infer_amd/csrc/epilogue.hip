@@ -42,13 +42,19 @@ __device__ __forceinline__ uint32_t bf16_add(uint32_t a, uint32_t b) {
 // the first two vectors of each thread stay in registers between the passes
 // and their weights are loaded before the block sum; further vectors are read
 // back from the residual (or x) in the second pass.
-template <bool RES, bool VEC>
+//
+// RED: `update` holds `ranks` partial outputs [ranks][rows][D] (the
+// row-parallel projection's per-rank results, gathered); the update is
+// bf16(sum over ranks in order, in FP32) -- the reference's reduce
+// (src/engine.cpp:183-195) folded into the residual add.
+template <bool RES, bool VEC, bool RED = false>
 __global__ __launch_bounds__(kNormMaxThreads) void rms_kernel(const uint16_t* __restrict__ x,
                                                               const uint16_t* __restrict__ update,
                                                               const uint16_t* __restrict__ w,
                                                               uint16_t* __restrict__ residual,
                                                               uint16_t* __restrict__ y, int D, float eps,
-                                                              int centered) {
+                                                              int centered, int ranks = 0,
+                                                              int64_t rank_stride = 0) {
     __shared__ float scratch[kNormMaxThreads / 64];
     const int64_t base = (int64_t)blockIdx.x * D;
     const int t = threadIdx.x, T = blockDim.x;
@@ -59,7 +65,26 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_kernel(const uint16_t* __
         auto first = [&](int i0) __attribute__((always_inline)) -> u32x4 {
             u32x4 v = load_u32x4(x + base + i0);
             if constexpr (RES) {
-                const u32x4 u = load_u32x4(update + base + i0);
+                u32x4 u = load_u32x4(update + base + i0);
+                if constexpr (RED) {
+                    float sum[8];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        sum[2 * q] = bf16_bits_to_f32(u[q] & 0xffffu);
+                        sum[2 * q + 1] = bf16_bits_to_f32(u[q] >> 16);
+                    }
+                    for (int r = 1; r < ranks; ++r) {
+                        const u32x4 p = load_u32x4(update + r * rank_stride + base + i0);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            sum[2 * q] += bf16_bits_to_f32(p[q] & 0xffffu);
+                            sum[2 * q + 1] += bf16_bits_to_f32(p[q] >> 16);
+                        }
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        u[q] = (uint32_t)f32_to_bf16_bits(sum[2 * q]) | ((uint32_t)f32_to_bf16_bits(sum[2 * q + 1]) << 16);
+                }
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     v[q] = bf16_add(v[q] & 0xffffu, u[q] & 0xffffu) | (bf16_add(v[q] >> 16, u[q] >> 16) << 16);
@@ -103,7 +128,13 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_kernel(const uint16_t* __
             for (int j = 0; j < 8 && i0 + j < D; ++j) {
                 float v = bf16_bits_to_f32(x[base + i0 + j]);
                 if constexpr (RES) {
-                    const uint16_t r = (uint16_t)bf16_add(x[base + i0 + j], update[base + i0 + j]);
+                    uint32_t u = update[base + i0 + j];
+                    if constexpr (RED) {
+                        float sum = bf16_bits_to_f32(u);
+                        for (int q = 1; q < ranks; ++q) sum += bf16_bits_to_f32(update[q * rank_stride + base + i0 + j]);
+                        u = f32_to_bf16_bits(sum);
+                    }
+                    const uint16_t r = (uint16_t)bf16_add(x[base + i0 + j], u);
                     residual[base + i0 + j] = r;
                     v = bf16_bits_to_f32(r);
                 }
@@ -265,6 +296,23 @@ hipError_t launch_rms(const uint16_t* x, const uint16_t* update, const uint16_t*
             hipLaunchKernelGGL((rms_kernel<false, false>), grid, block, 0, stream, x, update, w, residual, y, D, eps,
                                c);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce_rms(const uint16_t* x, const uint16_t* partials, int ranks, const uint16_t* w,
+                             uint16_t* residual, uint16_t* y, int64_t M, int D, float eps, bool centered,
+                             hipStream_t stream) {
+    const bool vec = D % 8 == 0 && aligned16(x) && aligned16(w) && aligned16(y) && aligned16(partials) &&
+                     aligned16(residual);
+    const dim3 grid((unsigned)M), block(norm_threads(D));
+    const int c = centered ? 1 : 0;
+    const int64_t stride = M * D;
+    if (vec)
+        hipLaunchKernelGGL((rms_kernel<true, true, true>), grid, block, 0, stream, x, partials, w, residual, y, D, eps,
+                           c, ranks, stride);
+    else
+        hipLaunchKernelGGL((rms_kernel<true, false, true>), grid, block, 0, stream, x, partials, w, residual, y, D,
+                           eps, c, ranks, stride);
     return hipGetLastError();
 }
 

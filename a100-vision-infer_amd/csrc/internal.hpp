@@ -56,6 +56,11 @@ hipError_t launch_stream_read(const void* src, size_t bytes, float* sink, hipStr
 // (update == nullptr) or of residual = bf16(x + update), also stored.
 hipError_t launch_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
                       uint16_t* y, int64_t M, int D, float eps, bool centered, hipStream_t stream);
+// Row-parallel reduce folded into the residual add: update = bf16(sum over
+// `ranks` partials [ranks][M][D] in order), then as launch_rms.
+hipError_t launch_reduce_rms(const uint16_t* x, const uint16_t* partials, int ranks, const uint16_t* w,
+                             uint16_t* residual, uint16_t* y, int64_t M, int D, float eps, bool centered,
+                             hipStream_t stream);
 // Candidates of logits [M, N] -> out [M, 2] doubles {value, id + offset};
 // part: M * vocab_chunks(N) {float bits, id} pairs.
 int64_t vocab_chunks(int64_t N);

@@ -37,6 +37,7 @@ EXPORTED = [
     "fp8lin_vocab_candidates", "fp8lin_merge_candidates",
     "fp8lin_linear_candidates_workspace_bytes", "fp8lin_linear_candidates",
     "fp8lin_engine_linear_candidates_workspace_bytes", "fp8lin_engine_linear_candidates",
+    "fp8lin_reduce_residual_rms",
 ]
 
 
@@ -111,6 +112,7 @@ def lib():
         "fp8lin_mfma_ceiling": (i32, [i64, vp, vp, vp]),
         "fp8lin_rms": (i32, [vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
         "fp8lin_residual_rms": (i32, [vp, vp, vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
+        "fp8lin_reduce_residual_rms": (i32, [vp, vp, i64, vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
         "fp8lin_vocab_candidates_workspace_bytes": (sz, [i64, i64]),
         "fp8lin_vocab_candidates": (i32, [vp, i64, i64, i64, vp, vp, sz, vp]),
         "fp8lin_merge_candidates": (i32, [vp, i64, i64, vp, vp]),

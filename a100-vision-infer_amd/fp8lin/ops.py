@@ -214,6 +214,26 @@ def residual_rms(x, update, weight, eps, centered=True):
     return residual, y
 
 
+def reduce_residual_rms(x, partials, weight, eps, centered=True):
+    """Row-parallel reduce folded into residual_rms: partials [ranks, *x.shape]
+    are per-rank outputs of a row-parallel projection; update =
+    bf16(sum over ranks in order, FP32), then (bf16(x + update), RMSNorm of
+    it) as residual_rms (src/engine.cpp:183-195 with src/dual_path.cu:68-78)."""
+    ok = (_is_dev(x) and x.dim() >= 2 and x.dtype == torch.bfloat16 and x.is_contiguous() and
+          x.numel() > 0 and _is_dev(partials) and partials.device == x.device and
+          partials.dtype == x.dtype and partials.is_contiguous() and partials.dim() == x.dim() + 1 and
+          partials.shape[1:] == x.shape and 1 <= partials.size(0) <= 8 and
+          _is_dev(weight) and weight.device == x.device and weight.dtype == x.dtype and
+          weight.is_contiguous() and weight.numel() == x.size(-1))
+    if not ok:
+        _fail(ERR_ARGUMENT, "Invalid reduce + residual RMS input")
+    residual, y = torch.empty_like(x), torch.empty_like(x)
+    D = x.size(-1)
+    check(lib().fp8lin_reduce_residual_rms(_ptr(x), _ptr(partials), partials.size(0), _ptr(weight), _ptr(residual),
+                                           _ptr(y), x.numel() // D, D, float(eps), int(bool(centered)), _stream(x)))
+    return residual, y
+
+
 def _workspace(nbytes, device):
     return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device) if nbytes else None
 

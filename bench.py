@@ -468,6 +468,14 @@ def head_and_epilogue(torch, fp8lin, dev, log):
         extra[f"residual_rms_m{m}_us"] = round(ms * 1e3, 2)
         extra[f"residual_rms_m{m}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         log(f"residual_rms M={m} D={d}: {ms * 1e3:.2f} us {nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
+        # the TP=2 row-parallel reduce folded in: two gathered partials
+        parts = torch.stack([u, fp8lin.gen_activations(m, d, seed=1, tag=5, device=dev)]).contiguous()
+        ms = graph_timed(torch, lambda: ok(L.fp8lin_reduce_residual_rms(P(x), P(parts), 2, P(w), P(res), P(y), m, d,
+                                                                        1e-6, 1, sp)), sp)
+        nbytes = (5 * m * d + d) * 2
+        extra[f"reduce2_residual_rms_m{m}_us"] = round(ms * 1e3, 2)
+        extra[f"reduce2_residual_rms_m{m}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        log(f"reduce(2 ranks)+residual_rms M={m} D={d}: {ms * 1e3:.2f} us {nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
     return extra
 
 

@@ -234,6 +234,20 @@ int fp8lin_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_
                         uint16_t* residual, uint16_t* y, int64_t rows, int64_t D, double eps,
                         int centered, fp8lin_stream_t stream);
 
+/* The row-parallel reduce folded into the residual add (no single reference
+ * counterpart; it fuses Engine::sum's BF16 reduce, src/engine.cpp:183-195,
+ * with residual_rms, src/dual_path.cu:68-78): partials [ranks][rows][D] are
+ * the per-rank outputs of a row-parallel projection, gathered on this GPU;
+ * update = bf16(sum over ranks in rank order, in FP32), then residual =
+ * bf16(x + update) and y = RMSNorm(residual) as fp8lin_residual_rms.  For
+ * ranks <= 2 the update equals the reference's BF16 all-reduce
+ * (tests/tp_reduce_test.cpp:25-32).  Requires 1 <= ranks <= 8 and the
+ * requirements of fp8lin_residual_rms.
+ */
+int fp8lin_reduce_residual_rms(const uint16_t* x, const uint16_t* partials, int64_t ranks,
+                               const uint16_t* weight, uint16_t* residual, uint16_t* y, int64_t rows,
+                               int64_t D, double eps, int centered, fp8lin_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Output head.  Per row of BF16 logits [M, N], the largest value (NaN counts
  * as +inf so that a NaN row is rejected by the merge, ties go to the smaller

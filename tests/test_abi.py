@@ -106,6 +106,10 @@ def test_epilogue_validation(fp8lin):
     assert L.fp8lin_merge_candidates(P, 0, 4, P, None) == 1
     assert L.fp8lin_merge_candidates(P, 2, 65536, P, None) == 1
     assert L.fp8lin_merge_candidates(None, 2, 4, P, None) == 2
+    assert L.fp8lin_reduce_residual_rms(P, P, 0, P, P, P, 2, 64, 1e-6, 1, None) == 1   # 1..8 ranks
+    assert L.fp8lin_reduce_residual_rms(P, P, 9, P, P, P, 2, 64, 1e-6, 1, None) == 1
+    assert L.fp8lin_reduce_residual_rms(P, None, 2, P, P, P, 2, 64, 1e-6, 1, None) == 2
+    assert L.fp8lin_reduce_residual_rms(P, P, 2, P, P, P, 2, 64, -1.0, 1, None) == 2
 
 
 def test_linear_candidates_validation(fp8lin):

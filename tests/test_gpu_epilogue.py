@@ -103,6 +103,34 @@ def test_residual_rms_rejects(fp8lin, gpu):
         fp8lin.residual_rms(x[0], x[0], w, 1e-6)   # dim() >= 2
 
 
+@pytest.mark.parametrize("ranks", [1, 2, 4, 8])
+@pytest.mark.parametrize("m,d", [(1, 5120), (4, 5120), (33, 128), (3, 1000)])
+def test_reduce_residual_rms(fp8lin, gpu, oracle, ranks, m, d):
+    """Row-parallel reduce folded into residual_rms: the update is bf16 of the
+    FP32 sum of the rank partials in rank order (for 2 ranks the reference's
+    BF16 all-reduce, tests/tp_reduce_test.cpp:25-32), then the residual is
+    bit-exact against the oracle and y equals fused_rms of it."""
+    rng = np.random.default_rng(ranks * 100 + m + d)
+    x, w = rand_bf16(rng, (m, d)), rand_bf16(rng, (d,))
+    parts = np.stack([rand_bf16(rng, (m, d), 0.5) for _ in range(ranks)])
+    acc = bf16_to_f32(parts[0]).astype(np.float32)
+    for r in range(1, ranks):
+        acc = (acc + bf16_to_f32(parts[r])).astype(np.float32)
+    update = torch.from_numpy(acc).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    xt, pt, wt = up(x, gpu), up(parts, gpu), up(w, gpu)
+    res, y = fp8lin.reduce_residual_rms(xt, pt, wt, 1e-6, True)
+    ref_res, ref_y = oracle.residual_rms(x, update, w, 1e-6, True)
+    assert np.array_equal(bits(res), ref_res)
+    assert_parity(bits(y), ref_y, f"reduce+rms r={ranks} {m}x{d}", min_exact=0.95)
+    assert torch.equal(y, fp8lin.fused_rms(res, wt, 1e-6, True))
+    if ranks == 2:
+        ref2 = (pt[0].float() + pt[1].float()).to(torch.bfloat16)
+        assert torch.equal(fp8lin.residual_rms(xt, ref2, wt, 1e-6, True)[0], res)
+    # the scalar kernel on 2-byte-aligned buffers gives the same bits
+    res_m, y_m = fp8lin.reduce_residual_rms(misaligned(xt), misaligned(pt), misaligned(wt), 1e-6, True)
+    assert torch.equal(res_m, res) and torch.equal(y_m, y)
+
+
 # ------------------------------------------------------ vocabulary candidates
 @pytest.mark.parametrize("m", [1, 4, 6])
 @pytest.mark.parametrize("n", [1, 257, 4096, 4097, 124160])
