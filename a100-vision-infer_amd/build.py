@@ -23,7 +23,7 @@ SOURCES = ["api.cpp", "gemv.hip", "small_m.hip", "gemm.hip", "elementwise.hip", 
 ARCH = "gfx950"
 
 COMMON = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 
