@@ -106,10 +106,30 @@ namespace fp8lin {
 // expf and an IEEE division so g stays within 1 BF16 ulp of the exact value.
 // Shared by the standalone kernel and every GEMM and GEMV epilogue, so the
 // fused and unfused paths agree bit for bit.
+//
+// g is computed first with the hardware exp2 and reciprocal
+// (exp(-a) = 2^(-a*log2(e)), then a * rcp(1 + e)).  For a >= -64 that value
+// is within about 64 FP32 ulp of the accurate one: the argument's rounding
+// (2^-18 absolute below 128, plus the constant's 2^-25 relative error) moves
+// e by under 4e-6 relative, and exp2, the add, rcp and the product add about
+// one ulp each.  Its BF16 rounding can differ from the accurate quotient's
+// only if its low 16 bits lie within 256 of the rounding midpoint 0x8000;
+// those values (under 1% of them), and a < -64 (where 1 / (1 + e) is an FP32
+// denormal that the reciprocal flushes to zero), take the accurate expf and
+// division.  g depends on a alone, a is BF16, so a check over all 65 536
+// gate values covers every input.
+__device__ __forceinline__ float swiglu_gate_exact(float a) {
+    return a / (1.0f + expf(-a));
+}
+
 __device__ __forceinline__ uint16_t swiglu_bf16_bits(uint16_t a_bits, uint16_t u_bits) {
     const float a = bf16_bits_to_f32(a_bits);
     const float u = bf16_bits_to_f32(u_bits);
-    const float g = bf16_bits_to_f32(f32_to_bf16_bits(a / (1.0f + expf(-a))));
+    const float e = __builtin_amdgcn_exp2f(a * -1.44269504088896340736f);
+    float gf = a * __builtin_amdgcn_rcpf(1.0f + e);
+    const uint32_t low = __builtin_bit_cast(uint32_t, gf) & 0xffffu;
+    if (!(a >= -64.0f) || (low > 0x8000u - 256u && low < 0x8000u + 256u)) gf = swiglu_gate_exact(a);
+    const float g = bf16_bits_to_f32(f32_to_bf16_bits(gf));
     return f32_to_bf16_bits(g * u);
 }
 
