@@ -282,6 +282,18 @@ void check_rms(const uint16_t* x, const uint16_t* w, const uint16_t* y, int64_t 
             "Invalid fused residual RMS input: eps must be finite and > 0");
 }
 
+// The sections only gate "f < 3 * section" for f < R/2 <= 2048: clamping
+// them to [0, 4096] keeps that test unchanged and the product in range.
+int clamp_section(int64_t s) { return s < 0 ? 0 : (s > 4096 ? 4096 : (int)s); }
+
+// src/optimized.cu:78: r > 0, r even, r <= D, positions [3, T].
+void check_rope(int64_t T, int64_t H, int64_t D, int64_t rotary, int64_t max_d) {
+    require(T > 0 && H > 0 && D > 0 && T < kMaxDim && H < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid RoPE input");
+    require(D <= max_d, FP8LIN_ERR_SHAPE, "RoPE input: head dimension above the kernel's limit");
+    require(T * H < kMaxDim, FP8LIN_ERR_SHAPE, "RoPE input: 2^31 rows or more");
+    require(rotary > 0 && rotary % 2 == 0 && rotary <= D, FP8LIN_ERR_ARGUMENT, "Invalid RoPE input: rotary size");
+}
+
 // src/dual_path.cu:73-75
 void check_candidates(int64_t M, int64_t N, int64_t offset, const double* out) {
     require(out != nullptr, FP8LIN_ERR_ARGUMENT, "Invalid vocabulary candidates: null output");
@@ -503,6 +515,43 @@ int fp8lin_reduce_residual_rms(const uint16_t* x, const uint16_t* partials, int6
         check_hip(fp8lin::launch_reduce_rms(x, partials, (int)ranks, weight, residual, y, rows, (int)D, (float)eps,
                                             centered != 0, as_stream(stream)),
                   "reduce residual rms launch");
+    });
+}
+
+int fp8lin_rope(const uint16_t* x, const int64_t* positions, uint16_t* y, int64_t T, int64_t H, int64_t D,
+                int64_t rotary, double theta, int64_t height_section, int64_t width_section,
+                fp8lin_stream_t stream) {
+    return guarded([&] {
+        if (T == 0) return;
+        require(x && positions && y, FP8LIN_ERR_ARGUMENT, "Invalid RoPE input: null pointer");
+        check_rope(T, H, D, rotary, fp8lin::kRopeMaxD);
+        ensure_device();
+        check_hip(fp8lin::launch_rope(x, positions, y, (int)T, (int)H, (int)D, (int)rotary, (float)theta,
+                                      clamp_section(height_section), clamp_section(width_section),
+                                      as_stream(stream)),
+                  "rope launch");
+    });
+}
+
+int fp8lin_qk_norm_rope(const uint16_t* projected, int64_t ld, const uint16_t* q_norm, const uint16_t* k_norm,
+                        const int64_t* positions, uint16_t* q, uint16_t* k, int64_t T, int64_t H, int64_t HK,
+                        int64_t D, int64_t rotary, double theta, int64_t height_section, int64_t width_section,
+                        double eps, fp8lin_stream_t stream) {
+    return guarded([&] {
+        if (T == 0) return;
+        require(projected && q_norm && k_norm && positions && q && k, FP8LIN_ERR_ARGUMENT,
+                "Invalid Q/K norm + RoPE input: null pointer");
+        require(HK > 0 && HK < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid Q/K norm + RoPE input: key heads");
+        check_rope(T, H + HK, D, rotary, 512);
+        require(ld >= 2 * (H + HK) * D && ld < kMaxDim, FP8LIN_ERR_SHAPE,
+                "Invalid Q/K norm + RoPE input: row stride below H*2D + 2*HK*D");
+        require(std::isfinite(eps) && eps > 0, FP8LIN_ERR_ARGUMENT, "Invalid Q/K norm + RoPE input: eps");
+        ensure_device();
+        check_hip(fp8lin::launch_qk_norm_rope(projected, ld, q_norm, k_norm, positions, q, k, (int)T, (int)H,
+                                              (int)HK, (int)D, (int)rotary, (float)theta,
+                                              clamp_section(height_section), clamp_section(width_section),
+                                              (float)eps, true, as_stream(stream)),
+                  "qk norm rope launch");
     });
 }
 

@@ -2,7 +2,10 @@
 //   - RMSNorm and the fused residual add + RMSNorm that follows each
 //     row-parallel projection (src/optimized.cu:71, src/dual_path.cu:12-28);
 //   - the per-rank vocabulary candidates of the output head and their merge
-//     across ranks (src/dual_path.cu:29-67,79-92).
+//     across ranks (src/dual_path.cu:29-67,79-92);
+//   - the multi-axis rotary embedding of the attention heads
+//     (src/optimized.cu:77-78) and its fusion with the per-head q/k RMSNorm
+//     on the QKV-gate projection output (src/engine.cpp:279-287).
 #include "device.hpp"
 #include "internal.hpp"
 
@@ -276,6 +279,115 @@ __global__ __launch_bounds__(128) void merge_candidates_kernel(const double* __r
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// ---- rotary embedding ----
+// Rows of rope and qk_norm_rope: four waves per workgroup, one row of D
+// elements per wave, staged in LDS as BF16 bits.
+constexpr int kRopeRows = 4;
+
+// cos and sin of pair f at token t, rounded to BF16 (src/optimized.cu:77):
+// the axis is 1 for f mod 3 == 1 below 3*hs, 2 for f mod 3 == 2 below 3*ws,
+// else 0; angle = float(pos) * powf(theta, -2f*f/R) in FP32.  The power is
+// evaluated in FP64 and rounded once to FP32, i.e. the correctly rounded
+// powf (CUDA's powf is within 2 ulp of it): at position p an ulp of the
+// frequency moves the angle by about p * 2^-24 rad, so a library-dependent
+// last bit would show at long contexts.
+__device__ __forceinline__ void rope_cos_sin(const int64_t* __restrict__ pos, int T, int t, int f, int R, float theta,
+                                             int hs, int ws, float& co, float& si) {
+    const int axis = (f % 3 == 1 && f < hs * 3) ? 1 : ((f % 3 == 2 && f < ws * 3) ? 2 : 0);
+    const float e = -2.0f * (float)f / (float)R;
+    const float freq = (float)pow((double)theta, (double)e);
+    const float angle = (float)pos[(int64_t)axis * T + t] * freq;
+    float s, c;
+    sincosf(angle, &s, &c);
+    co = bf16_bits_to_f32(f32_to_bf16_bits(c));
+    si = bf16_bits_to_f32(f32_to_bf16_bits(s));
+}
+
+// bf16(bf16(x * co) + bf16(rotated * si)), the reference's rounding points.
+__device__ __forceinline__ uint16_t rope_one(float x, float rotated, float co, float si) {
+    const float a = bf16_bits_to_f32(f32_to_bf16_bits(x * co));
+    const float b = bf16_bits_to_f32(f32_to_bf16_bits(rotated * si));
+    return f32_to_bf16_bits(a + b);
+}
+
+// Rotates one LDS row into y: lane l takes the pairs (f, f + R/2) for
+// f = l, l + 64, ... < R/2 (one cos/sin per pair); elements d >= R are copied.
+__device__ __forceinline__ void rope_row(const uint16_t* row, uint16_t* __restrict__ y,
+                                         const int64_t* __restrict__ pos, int T, int t, int D, int R, float theta,
+                                         int hs, int ws, int lane) {
+    const int half = R >> 1;
+    for (int f = lane; f < half; f += 64) {
+        float co, si;
+        rope_cos_sin(pos, T, t, f, R, theta, hs, ws, co, si);
+        const float x1 = bf16_bits_to_f32(row[f]), x2 = bf16_bits_to_f32(row[f + half]);
+        y[f] = rope_one(x1, -x2, co, si);
+        y[f + half] = rope_one(x2, x1, co, si);
+    }
+    for (int d = R + lane; d < D; d += 64) y[d] = row[d];
+}
+
+// x, y [T, H, D]; row r = t * H + h.  Every wave reaches the barrier.
+__global__ __launch_bounds__(64 * kRopeRows) void rope_kernel(const uint16_t* __restrict__ x,
+                                                              const int64_t* __restrict__ pos,
+                                                              uint16_t* __restrict__ y, int T, int H, int D, int R,
+                                                              float theta, int hs, int ws) {
+    extern __shared__ uint16_t rows[];  // [kRopeRows][D]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t r = (int64_t)blockIdx.x * kRopeRows + wave;
+    const bool live = r < (int64_t)T * H;
+    uint16_t* row = rows + wave * D;
+    if (live)
+        for (int d = lane; d < D; d += 64) row[d] = x[r * D + d];
+    __syncthreads();
+    if (live) rope_row(row, y + r * D, pos, T, (int)(r / H), D, R, theta, hs, ws, lane);
+}
+
+// The QKV-gate output p [T, ld] holds per token H query heads of 2D (query,
+// then gate) followed by HK key heads and HK value heads of D
+// (src/engine.cpp:279-282).  Row r = t * (H + HK) + head: the head's D values
+// are RMS-normalised with weight w (q_norm or k_norm) exactly as rms_kernel
+// does for D <= 512 -- lane l owns elements [8l, 8l + 8) and adds their
+// squares in order, one wave sum, the same normalisation arithmetic -- so the
+// result equals fp8lin_rms of the contiguous rows bit for bit; the BF16
+// result is then rotated as rope_kernel does.  q [T, H, D], k [T, HK, D].
+__global__ __launch_bounds__(64 * kRopeRows) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ p, int64_t ld, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    const int64_t* __restrict__ pos, uint16_t* __restrict__ q, uint16_t* __restrict__ k, int T, int H, int HK,
+    int D, int R, float theta, int hs, int ws, float eps, int centered) {
+    extern __shared__ uint16_t rows[];  // [kRopeRows][D]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int heads = H + HK;
+    const int64_t r = (int64_t)blockIdx.x * kRopeRows + wave;
+    const bool live = r < (int64_t)T * heads;
+    const int t = live ? (int)(r / heads) : 0, hh = live ? (int)(r % heads) : 0;
+    const bool is_q = hh < H;
+    const uint16_t* src = p + t * ld + (is_q ? (int64_t)hh * 2 * D : (int64_t)H * 2 * D + (int64_t)(hh - H) * D);
+    const uint16_t* w = is_q ? qw : kw;
+    uint16_t* dst = is_q ? q + ((int64_t)t * H + hh) * D : k + ((int64_t)t * HK + (hh - H)) * D;
+    uint16_t* row = rows + wave * D;
+    const float c = centered ? 1.0f : 0.0f;
+    float v[8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int i = 8 * lane + j;
+        v[j] = live && i < D ? bf16_bits_to_f32(src[i]) : 0.0f;
+        ss = __builtin_fmaf(v[j], v[j], ss);
+    }
+    const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int i = 8 * lane + j;
+        if (live && i < D) {
+            float n = v[j] * inv;
+            if (!centered) n = bf16_bits_to_f32(f32_to_bf16_bits(n));
+            row[i] = f32_to_bf16_bits(n * (bf16_bits_to_f32(w[i]) + c));
+        }
+    }
+    __syncthreads();
+    if (live) rope_row(row, dst, pos, T, t, D, R, theta, hs, ws, lane);
+}
+
 }  // namespace
 
 hipError_t launch_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
@@ -336,6 +448,24 @@ hipError_t launch_merge_candidates(const double* gathered, int ranks, int64_t ro
                                    hipStream_t stream) {
     hipLaunchKernelGGL(merge_candidates_kernel, dim3((unsigned)((rows + 127) / 128)), dim3(128), 0, stream,
                        gathered, ranks, rows, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const uint16_t* x, const int64_t* pos, uint16_t* y, int T, int H, int D, int R, float theta,
+                       int hs, int ws, hipStream_t stream) {
+    const int64_t rows = (int64_t)T * H;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((rows + kRopeRows - 1) / kRopeRows)), dim3(64 * kRopeRows),
+                       (size_t)kRopeRows * D * 2, stream, x, pos, y, T, H, D, R, theta, hs, ws);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope(const uint16_t* p, int64_t ld, const uint16_t* qw, const uint16_t* kw,
+                               const int64_t* pos, uint16_t* q, uint16_t* k, int T, int H, int HK, int D, int R,
+                               float theta, int hs, int ws, float eps, bool centered, hipStream_t stream) {
+    const int64_t rows = (int64_t)T * (H + HK);
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((rows + kRopeRows - 1) / kRopeRows)),
+                       dim3(64 * kRopeRows), (size_t)kRopeRows * D * 2, stream, p, ld, qw, kw, pos, q, k, T, H, HK,
+                       D, R, theta, hs, ws, eps, centered ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -69,6 +69,15 @@ hipError_t launch_vocab_candidates(const uint16_t* logits, int M, int N, int64_t
 hipError_t launch_merge_candidates(const double* gathered, int ranks, int64_t rows, int64_t* out,
                                    hipStream_t stream);
 
+// Multi-axis rotary embedding of x [T, H, D] (D <= kRopeMaxD), and the fused
+// per-head RMSNorm + rotary embedding of the QKV-gate output (D <= 512).
+constexpr int kRopeMaxD = 4096;
+hipError_t launch_rope(const uint16_t* x, const int64_t* pos, uint16_t* y, int T, int H, int D, int R, float theta,
+                       int hs, int ws, hipStream_t stream);
+hipError_t launch_qk_norm_rope(const uint16_t* p, int64_t ld, const uint16_t* qw, const uint16_t* kw,
+                               const int64_t* pos, uint16_t* q, uint16_t* k, int T, int H, int HK, int D, int R,
+                               float theta, int hs, int ws, float eps, bool centered, hipStream_t stream);
+
 hipError_t launch_mfma_ceiling(int64_t iters, float* sink, uint64_t* clocks, hipStream_t stream);
 
 }  // namespace fp8lin

@@ -38,6 +38,8 @@ EXPORTED = [
     "fp8lin_linear_candidates_workspace_bytes", "fp8lin_linear_candidates",
     "fp8lin_engine_linear_candidates_workspace_bytes", "fp8lin_engine_linear_candidates",
     "fp8lin_reduce_residual_rms",
+    "fp8lin_rope",
+    "fp8lin_qk_norm_rope",
 ]
 
 
@@ -113,6 +115,9 @@ def lib():
         "fp8lin_rms": (i32, [vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
         "fp8lin_residual_rms": (i32, [vp, vp, vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
         "fp8lin_reduce_residual_rms": (i32, [vp, vp, i64, vp, vp, vp, i64, i64, ctypes.c_double, i32, vp]),
+        "fp8lin_rope": (i32, [vp, vp, vp, i64, i64, i64, i64, ctypes.c_double, i64, i64, vp]),
+        "fp8lin_qk_norm_rope": (i32, [vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ctypes.c_double, i64,
+                                      i64, ctypes.c_double, vp]),
         "fp8lin_vocab_candidates_workspace_bytes": (sz, [i64, i64]),
         "fp8lin_vocab_candidates": (i32, [vp, i64, i64, i64, vp, vp, sz, vp]),
         "fp8lin_merge_candidates": (i32, [vp, i64, i64, vp, vp]),

@@ -14,7 +14,7 @@ import ctypes
 import torch
 
 from ._lib import ERR_ARGUMENT, Fp8linError, LinearOptions, Weight, check, lib
-from .ops import fp8_decode
+from .ops import fp8_decode, qk_norm_rope
 
 
 class StoredWeight:
@@ -109,6 +109,22 @@ class LinearEngine:
         gate = qg.narrow(-1, D, D).reshape(T, H * D)
         k = projected.narrow(-1, H * 2 * D, HK * D).reshape(T, HK, D)
         v = projected.narrow(-1, H * 2 * D + HK * D, HK * D).reshape(T, HK, D)
+        return q, gate, k, v
+
+    def full_attention_inputs(self, x, prefix, positions, q_norm, k_norm, heads, kv_heads, head_dim, rope, eps):
+        """The projection and Q/K epilogue of `Engine::full_attention`, optimized
+        branch (src/engine.cpp:276-287): projected = linear(x, prefix.qkv_gate);
+        q and k are RMS-normalised per head (centered, q_norm / k_norm) and
+        rotated by the interleaved mRoPE of `rope` (the model config's
+        rope_parameters: partial_rotary_factor, mrope_section, rope_theta), in
+        one launch; gate and v are as in qkv_gate_views.  Returns
+        (q [T,H,D], gate [T,H*D], k [T,HK,D], v [T,HK,D])."""
+        projected = self.linear(x, prefix + ".qkv_gate")
+        _, gate, _, v = self.qkv_gate_views(projected, heads, kv_heads, head_dim)
+        rotary = int(head_dim * rope.get("partial_rotary_factor", 0.25))
+        sections = rope["mrope_section"]
+        q, k = qk_norm_rope(projected, q_norm, k_norm, positions, heads, kv_heads, head_dim, rotary,
+                            rope["rope_theta"], sections[1], sections[2], eps)
         return q, gate, k, v
 
     # -- dispatch --------------------------------------------------------------

@@ -234,6 +234,56 @@ def reduce_residual_rms(x, partials, weight, eps, centered=True):
     return residual, y
 
 
+def _positions_ok(positions, x, T):
+    return (_is_dev(positions) and positions.device == x.device and positions.dtype == torch.int64 and
+            positions.dim() == 2 and positions.size(0) == 3 and positions.size(1) == T)
+
+
+def fused_rope(x, positions, rotary, theta, height_section, width_section):
+    """`at::Tensor fused_rope(x, positions, int rotary, double theta,
+    int height_section, int width_section)` -- src/optimized.cu:77-78: the
+    interleaved multi-axis rotary embedding of x [T, H, D] at positions
+    [3, T] (int64), first `rotary` dimensions of each head."""
+    ok = (_is_dev(x) and x.dim() == 3 and x.dtype == torch.bfloat16 and _positions_ok(positions, x, x.size(0)) and
+          rotary > 0 and rotary % 2 == 0 and rotary <= x.size(2))
+    if not ok:
+        _fail(ERR_ARGUMENT, "Invalid RoPE input")
+    x, positions = x.contiguous(), positions.contiguous()
+    y = torch.empty_like(x)
+    T, H, D = x.shape
+    check(lib().fp8lin_rope(_ptr(x), _ptr(positions), _ptr(y), T, H, D, int(rotary), float(theta),
+                            int(height_section), int(width_section), _stream(x)))
+    return y
+
+
+def qk_norm_rope(projected, q_norm, k_norm, positions, heads, kv_heads, head_dim, rotary, theta, height_section,
+                 width_section, eps):
+    """The optimized branch of src/engine.cpp:279-287 on the QKV-gate output
+    projected [T, H*2D + 2*HK*D] (row stride may be wider): returns q
+    [T, H, D] = rope(rms(query heads, q_norm)) and k [T, HK, D] =
+    rope(rms(key heads, k_norm)) with the centered RMSNorm, in one launch.
+    Equal bit for bit to fused_rms of the query (key) heads followed by
+    fused_rope."""
+    H, HK, D = int(heads), int(kv_heads), int(head_dim)
+    ok = (_is_dev(projected) and projected.dim() == 2 and projected.dtype == torch.bfloat16 and
+          projected.stride(1) == 1 and H > 0 and HK > 0 and 0 < D <= 512 and
+          projected.size(1) == 2 * (H + HK) * D and _positions_ok(positions, projected, projected.size(0)) and
+          rotary > 0 and rotary % 2 == 0 and rotary <= D)
+    for w in (q_norm, k_norm):
+        ok = ok and (_is_dev(w) and w.device == projected.device and w.dtype == torch.bfloat16 and
+                     w.is_contiguous() and w.numel() == D)
+    if not ok:
+        _fail(ERR_ARGUMENT, "Invalid Q/K norm + RoPE input")
+    positions = positions.contiguous()
+    T = projected.size(0)
+    q = torch.empty((T, H, D), dtype=torch.bfloat16, device=projected.device)
+    k = torch.empty((T, HK, D), dtype=torch.bfloat16, device=projected.device)
+    check(lib().fp8lin_qk_norm_rope(_ptr(projected), projected.stride(0), _ptr(q_norm), _ptr(k_norm),
+                                    _ptr(positions), _ptr(q), _ptr(k), T, H, HK, D, int(rotary), float(theta),
+                                    int(height_section), int(width_section), float(eps), _stream(projected)))
+    return q, k
+
+
 def _workspace(nbytes, device):
     return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device) if nbytes else None
 

@@ -249,6 +249,40 @@ int fp8lin_reduce_residual_rms(const uint16_t* x, const uint16_t* partials, int6
                                int64_t D, double eps, int centered, fp8lin_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Multi-axis rotary embedding (interleaved mRoPE) of x [T, H, D] (BF16) at
+ * positions [3, T] (int64: temporal, height, width), into y [T, H, D].  For
+ * d < rotary, pair index f = d mod rotary/2 reads axis 1 when f mod 3 == 1
+ * and f < 3*height_section, axis 2 when f mod 3 == 2 and f < 3*width_section,
+ * else axis 0;
+ *   angle = float(pos) * powf(float(theta), -2f*f/rotary)      (FP32)
+ *   co = bf16(cos(angle)), si = bf16(sin(angle))
+ *   y[d] = bf16(bf16(x[d]*co) - bf16(x[d+rotary/2]*si))  d < rotary/2
+ *   y[d] = bf16(bf16(x[d]*co) + bf16(x[d-rotary/2]*si))  rotary/2 <= d < rotary
+ * and y[d] = x[d] for d >= rotary.  Requires rotary even, 0 < rotary <= D,
+ * D <= 4096; T == 0 is a no-op.  Replaces `at::Tensor fused_rope(at::Tensor x,
+ * at::Tensor positions, int rotary, double theta, int height_section,
+ * int width_section)` (include/avi/ops.h:25, src/optimized.cu:77-78).
+ */
+int fp8lin_rope(const uint16_t* x, const int64_t* positions, uint16_t* y, int64_t T, int64_t H, int64_t D,
+                int64_t rotary, double theta, int64_t height_section, int64_t width_section,
+                fp8lin_stream_t stream);
+
+/* Q/K epilogue of the QKV-gate projection, read in place from projected
+ * [T, ld] (ld >= H*2D + 2*HK*D elements; per token H heads of query then gate,
+ * D each, then HK key heads and HK value heads): q [T, H, D] =
+ * rope(rms(query), q_norm) and k [T, HK, D] = rope(rms(key), k_norm), with
+ * the centered RMSNorm of fp8lin_rms and fp8lin_rope's rotation.  Bit-identical
+ * to fp8lin_rms of the contiguous query (key) rows followed by fp8lin_rope.
+ * The gate and value heads stay views of projected.  Requires D <= 512.
+ * Replaces the optimized branch of src/engine.cpp:279-287 (norm(q_norm),
+ * norm(k_norm), fused_rope(q), fused_rope(k)).
+ */
+int fp8lin_qk_norm_rope(const uint16_t* projected, int64_t ld, const uint16_t* q_norm, const uint16_t* k_norm,
+                        const int64_t* positions, uint16_t* q, uint16_t* k, int64_t T, int64_t H, int64_t HK,
+                        int64_t D, int64_t rotary, double theta, int64_t height_section, int64_t width_section,
+                        double eps, fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Output head.  Per row of BF16 logits [M, N], the largest value (NaN counts
  * as +inf so that a NaN row is rejected by the merge, ties go to the smaller
  * column) as out[m] = {value, column + offset} in doubles.  Replaces

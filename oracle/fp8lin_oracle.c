@@ -329,6 +329,40 @@ void oracle_rms(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t M, in
     free(r);
 }
 
+/* src/optimized.cu:77 (rope_kernel), the multi-axis rotary embedding of
+ * fused_rope (:78): x [T, H, D] BF16, pos [3, T] int64.  For d < R, pair
+ * index f = d mod R/2 takes its position from axis 1 when f mod 3 == 1 and
+ * f < 3*hs, from axis 2 when f mod 3 == 2 and f < 3*ws, else axis 0;
+ *   angle = float(pos) * powf(theta, -2f*f/R)   (FP32)
+ *   co = bf16(cos(angle)), si = bf16(sin(angle))
+ *   y[d] = bf16(bf16(x[d]*co) + bf16(s*x[d'] * si))
+ * with d' = d + R/2, s = -1 for d < R/2 and d' = d - R/2, s = +1 otherwise.
+ * Elements d >= R are copied. */
+void oracle_rope(const uint16_t* x, const int64_t* pos, uint16_t* y, int64_t T, int64_t H, int64_t D, int64_t R,
+                 float theta, int64_t hs, int64_t ws) {
+    const int64_t half = R / 2;
+    for (int64_t t = 0; t < T; t++)
+        for (int64_t h = 0; h < H; h++) {
+            const uint16_t* xr = x + (t * H + h) * D;
+            uint16_t* yr = y + (t * H + h) * D;
+            for (int64_t d = 0; d < D; d++) {
+                if (d >= R) {
+                    yr[d] = xr[d];
+                    continue;
+                }
+                const int64_t f = d % half;
+                const int axis = (f % 3 == 1 && f < hs * 3) ? 1 : ((f % 3 == 2 && f < ws * 3) ? 2 : 0);
+                const float angle = (float)pos[axis * T + t] * powf(theta, -2.0f * (float)f / (float)R);
+                const float co = oracle_bf16_to_float(oracle_bf16_rne(cosf(angle)));
+                const float si = oracle_bf16_to_float(oracle_bf16_rne(sinf(angle)));
+                const float rotated = d < half ? -oracle_bf16_to_float(xr[d + half]) : oracle_bf16_to_float(xr[d - half]);
+                const float a = oracle_bf16_to_float(oracle_bf16_rne(oracle_bf16_to_float(xr[d]) * co));
+                const float b = oracle_bf16_to_float(oracle_bf16_rne(rotated * si));
+                yr[d] = oracle_bf16_rne(a + b);
+            }
+        }
+}
+
 /* src/dual_path.cu:12-28 */
 void oracle_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
                          uint16_t* y, int64_t M, int64_t D, float eps, int centered) {

@@ -71,6 +71,9 @@ void oracle_swiglu(const uint16_t* in, uint16_t* y, int64_t M, int64_t D);
  * y = bf16(v * (w + (centered ? 1 : 0))).  src/optimized.cu:71 (`rms`). */
 void oracle_rms(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t M, int64_t D, float eps,
                 int centered);
+/* Multi-axis rotary embedding of x [T, H, D] at pos [3, T] (src/optimized.cu:77-78). */
+void oracle_rope(const uint16_t* x, const int64_t* pos, uint16_t* y, int64_t T, int64_t H, int64_t D, int64_t R,
+                 float theta, int64_t hs, int64_t ws);
 /* residual = bf16(float(x) + float(update)); y = oracle_rms(residual).
  * src/dual_path.cu:12-28 (`add_norm`). */
 void oracle_residual_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,

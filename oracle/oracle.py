@@ -63,6 +63,7 @@ def lib():
         L.oracle_rms.argtypes = [_u16p, _u16p, _u16p, _i64, _i64, ctypes.c_float, ctypes.c_int]
         L.oracle_residual_rms.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _i64, _i64, ctypes.c_float,
                                           ctypes.c_int]
+        L.oracle_rope.argtypes = [_u16p, _i64p, _u16p, _i64, _i64, _i64, _i64, ctypes.c_float, _i64, _i64]
         L.oracle_vocab_candidates.argtypes = [_u16p, _i64, _i64, _i64, _f64p]
         L.oracle_merge_candidates.argtypes = [_f64p, _i64, _i64, _i64p]
     return _lib
@@ -175,6 +176,37 @@ def rms(x_bits, w_bits, eps=1e-6, centered=True):
     y = np.empty_like(x)
     lib().oracle_rms(_p(x, _u16p), _p(w, _u16p), _p(y, _u16p), m, d, eps, int(centered))
     return y
+
+
+def rope(x_bits, positions, rotary, theta, height_section, width_section):
+    """x_bits [T, H, D] uint16 (BF16), positions [3, T] int64; theta is used
+    in FP32 as the reference's kernel parameter is."""
+    x = np.ascontiguousarray(x_bits, np.uint16)
+    pos = np.ascontiguousarray(positions, np.int64)
+    t, h, d = x.shape
+    assert pos.shape == (3, t) and 0 < rotary <= d and rotary % 2 == 0
+    y = np.empty_like(x)
+    lib().oracle_rope(_p(x, _u16p), _p(pos, _i64p), _p(y, _u16p), t, h, d, rotary, float(theta),
+                      height_section, width_section)
+    return y
+
+
+def qk_norm_rope(projected_bits, q_norm_bits, k_norm_bits, positions, heads, kv_heads, head_dim, rotary, theta,
+                 height_section, width_section, eps=1e-6):
+    """The optimized branch of src/engine.cpp:279-287 on the QKV-gate output
+    [T, H*2D + 2*HK*D]: q = rope(rms(q rows)), k = rope(rms(k rows)) with the
+    centered norm of src/engine.cpp:243-244 (one_center defaults to true,
+    include/avi/engine.h:50)."""
+    p = np.ascontiguousarray(projected_bits, np.uint16)
+    t = p.shape[0]
+    hd, kd = heads * head_dim, kv_heads * head_dim
+    assert p.shape[1] == 2 * hd + 2 * kd
+    q = p[:, :2 * hd].reshape(t, heads, 2 * head_dim)[:, :, :head_dim].reshape(t * heads, head_dim)
+    k = p[:, 2 * hd:2 * hd + kd].reshape(t * kv_heads, head_dim)
+    q = rms(q, q_norm_bits, eps, True).reshape(t, heads, head_dim)
+    k = rms(k, k_norm_bits, eps, True).reshape(t, kv_heads, head_dim)
+    args = (positions, rotary, theta, height_section, width_section)
+    return rope(q, *args), rope(k, *args)
 
 
 def residual_rms(x_bits, u_bits, w_bits, eps=1e-6, centered=True):

@@ -79,6 +79,35 @@ def test_shared_and_swiglu_validation(fp8lin):
     assert L.fp8lin_decode(P, P, 7, P, 4, 256, None) == 2
 
 
+def test_rope_validation(fp8lin):
+    """src/optimized.cu:78 preconditions (rotary even, 0 < rotary <= D) and the
+    kernels' own limits (D <= 4096; D <= 512 and a row stride covering the
+    head layout for the fused Q/K epilogue) as status codes."""
+    L = fp8lin.lib()
+    assert L.fp8lin_rope(P, P, P, 0, 12, 256, 64, 1e7, 11, 10, None) == 0          # no tokens: no-op
+    assert L.fp8lin_rope(None, P, P, 1, 12, 256, 64, 1e7, 11, 10, None) == 2
+    assert L.fp8lin_rope(P, None, P, 1, 12, 256, 64, 1e7, 11, 10, None) == 2
+    assert L.fp8lin_rope(P, P, P, 1, 12, 256, 63, 1e7, 11, 10, None) == 2          # odd rotary
+    assert L.fp8lin_rope(P, P, P, 1, 12, 256, 0, 1e7, 11, 10, None) == 2
+    assert L.fp8lin_rope(P, P, P, 1, 12, 256, 258, 1e7, 11, 10, None) == 2         # rotary > D
+    assert L.fp8lin_rope(P, P, P, 1, 12, 4098, 64, 1e7, 11, 10, None) == 1         # D limit
+    assert L.fp8lin_rope(P, P, P, 1, 0, 256, 64, 1e7, 11, 10, None) == 1
+    assert L.fp8lin_rope(P, P, P, 1 << 20, 1 << 12, 8, 8, 1e7, 11, 10, None) == 1  # 2^31 rows
+    args = (12, 2, 256, 64, 1e7, 11, 10, 1e-6, None)
+    ld = 2 * 14 * 256
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 0, *args) == 0              # no tokens: no-op
+    assert L.fp8lin_qk_norm_rope(P, ld, None, P, P, P, P, 1, *args) == 2
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, None, 1, *args) == 2
+    assert L.fp8lin_qk_norm_rope(P, ld - 1, P, P, P, P, P, 1, *args) == 1          # stride below the layout
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 12, 0, *args[2:]) == 1   # key heads
+    assert L.fp8lin_qk_norm_rope(P, 4 * 14 * 576, P, P, P, P, P, 1, 12, 2, 576, 64, 1e7, 11, 10, 1e-6,
+                                 None) == 1                                        # D <= 512
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 12, 2, 256, 65, 1e7, 11, 10, 1e-6, None) == 2
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 12, 2, 256, 64, 1e7, 11, 10, 0.0, None) == 2
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 12, 2, 256, 64, 1e7, 11, 10, float("nan"),
+                                 None) == 2
+
+
 def test_epilogue_validation(fp8lin):
     """src/dual_path.cu:69-72,73-75,86-88 preconditions as status codes."""
     L = fp8lin.lib()

@@ -334,3 +334,122 @@ def test_engine_local_candidates(fp8lin, gpu, rows, opts):
     assert torch.equal(got, fp8lin.vocabulary_candidates(y, 62080))
     if opts == "default":
         assert torch.equal(got, fp8lin.linear_candidates(x, codes, scales, 62080))
+
+
+# ------------------------------------------------------ rotary embedding
+ROPE_CASES = [
+    ((1, 12, 256), 64, 1e7, 11, 10),     # decode token, the model's query heads per TP=2 rank
+    ((300, 2, 256), 64, 1e7, 11, 10),    # prefill, key heads
+    ((7, 3, 128), 128, 1e4, 4, 2),       # full rotation; section bounds inside the pairs
+    ((5, 3, 100), 30, 5e5, 2, 5),        # ragged head and rotary sizes
+    ((2, 1, 4096), 4096, 1e4, 11, 10),   # largest head the kernel takes (2048 pairs)
+]
+
+
+def assert_rope_parity(got, ref, rotary, what, min_exact):
+    """The BF16 bar over the whole output (rel_l2 <= 1e-2, cos >= 0.9999,
+    the given bit-exact fraction), and per rotated element an error within
+    2^-6 of its pair's norm: a rotation keeps the pair's norm, and a one-ulp
+    difference of the BF16 cos or sin (device against host math library)
+    moves an output by about 2^-8 of it, which near a cancelling sum is many
+    ulps of the result."""
+    assert_parity(got, ref, what, min_exact=min_exact, elementwise=False)
+    half = rotary // 2
+    g = bf16_to_f32(got[..., :rotary]).astype(np.float64)
+    r = bf16_to_f32(ref[..., :rotary]).astype(np.float64)
+    partner = np.concatenate([r[..., half:], r[..., :half]], -1)
+    bound = 2.0 ** -6 * np.sqrt(r * r + partner * partner) + 1e-30
+    worst = np.max(np.abs(g - r) / bound)
+    assert worst <= 1.0, f"{what}: rotated error {worst:.3f} of the pair bound"
+
+
+@pytest.mark.parametrize("shape,rotary,theta,hs,ws", ROPE_CASES)
+def test_rope_oracle(fp8lin, gpu, oracle, shape, rotary, theta, hs, ws):
+    """fused_rope (src/optimized.cu:77-78) against the oracle: the part past
+    `rotary` bit for bit; the rotated part at the BF16 bar, with >= 99% of it
+    bit-exact (cos/sin of the device math library against the host's, both
+    rounded to BF16)."""
+    rng = np.random.default_rng(sum(shape) + rotary)
+    x = rand_bf16(rng, shape)
+    pos = rng.integers(0, 4096, size=(3, shape[0]), dtype=np.int64)
+    got = bits(fp8lin.fused_rope(up(x, gpu), torch.from_numpy(pos).to(gpu), rotary, theta, hs, ws))
+    ref = oracle.rope(x, pos, rotary, theta, hs, ws)
+    assert np.array_equal(got[..., rotary:], x[..., rotary:])
+    assert_rope_parity(got, ref, rotary, f"rope {shape}", 0.99)
+
+
+def test_rope_large_positions(fp8lin, gpu, oracle):
+    """Positions up to 2^20 (angles up to 1e6 rad): the BF16 bar and the
+    pair bound, no bit-exact fraction (the FP32 angle's cos/sin differ by an
+    ulp between math libraries often enough at this range)."""
+    rng = np.random.default_rng(20)
+    x = rand_bf16(rng, (64, 12, 256))
+    pos = rng.integers(0, 1 << 20, size=(3, 64), dtype=np.int64)
+    got = bits(fp8lin.fused_rope(up(x, gpu), torch.from_numpy(pos).to(gpu), 64, 1e7, 11, 10))
+    assert_rope_parity(got, oracle.rope(x, pos, 64, 1e7, 11, 10), 64, "rope large positions", None)
+
+
+def test_rope_zero_positions(fp8lin, gpu):
+    """tests/optimized_test.cpp:139-141: zero positions return x."""
+    rng = np.random.default_rng(141)
+    x = rand_bf16(rng, (3, 2, 64))
+    pos = torch.zeros((3, 3), dtype=torch.int64, device=gpu)
+    assert np.array_equal(bits(fp8lin.fused_rope(up(x, gpu), pos, 32, 1e4, 4, 4)), x)
+
+
+QK_CASES = [
+    (1, 12, 2, 256, 64, 0),      # decode, the model's rank shape (QKV-gate width 7168)
+    (33, 12, 2, 256, 64, 0),
+    (300, 12, 2, 256, 64, 40),   # prefill; projected is a column slice of a wider buffer
+    (5, 4, 1, 100, 30, 0),       # D not a multiple of 8 (scalar path of fused_rms)
+    (3, 2, 2, 512, 128, 8),      # largest fused head
+]
+
+
+@pytest.mark.parametrize("T,H,HK,D,R,pad", QK_CASES)
+def test_qk_norm_rope(fp8lin, gpu, oracle, T, H, HK, D, R, pad):
+    """The Q/K epilogue of src/engine.cpp:279-287 in one launch: bit-identical
+    to fused_rms of the query (key) heads followed by fused_rope, and at the
+    BF16 bar against the oracle's composition."""
+    rng = np.random.default_rng(T * 31 + D + pad)
+    W = 2 * (H + HK) * D
+    buf = rand_bf16(rng, (T, W + pad))
+    qw, kw = rand_bf16(rng, (D,), 0.1), rand_bf16(rng, (D,), 0.1)
+    pos = rng.integers(0, 8192, size=(3, T), dtype=np.int64)
+    args = (R, 1e7, 11, 10)
+    proj = up(buf, gpu)[:, :W]
+    posd = torch.from_numpy(pos).to(gpu)
+    q, k = fp8lin.qk_norm_rope(proj, up(qw, gpu), up(kw, gpu), posd, H, HK, D, *args, 1e-6)
+    qv, _, kv, _ = fp8lin.LinearEngine.qkv_gate_views(proj, H, HK, D)
+    q2 = fp8lin.fused_rope(fp8lin.fused_rms(qv.contiguous(), up(qw, gpu), 1e-6, True), posd, *args)
+    k2 = fp8lin.fused_rope(fp8lin.fused_rms(kv.contiguous(), up(kw, gpu), 1e-6, True), posd, *args)
+    assert torch.equal(q.view(torch.int16), q2.view(torch.int16))
+    assert torch.equal(k.view(torch.int16), k2.view(torch.int16))
+    rq, rk = oracle.qk_norm_rope(buf[:, :W], qw, kw, pos, H, HK, D, *args, eps=1e-6)
+    assert_rope_parity(bits(q), rq, R, "qk_norm_rope q", 0.98)
+    assert_rope_parity(bits(k), rk, R, "qk_norm_rope k", 0.98)
+    assert_parity(bits(q)[..., R:], rq[..., R:], "qk_norm_rope q pass-through", min_exact=0.98)
+
+
+def test_engine_full_attention_inputs(fp8lin, gpu):
+    """LinearEngine.full_attention_inputs (src/engine.cpp:276-287, optimized
+    branch): the fused QKV-gate projection, then the Q/K epilogue; gate and v
+    are the projection's own columns."""
+    H, HK, D, K, T = 12, 2, 256, 5120, 3
+    eng = fp8lin.LinearEngine(fp8lin.LinearOptions())
+    p = "model.language_model.layers.3.self_attn"
+    for i, (name, n) in enumerate((("q_proj", H * 2 * D), ("k_proj", HK * D), ("v_proj", HK * D))):
+        c, s = fp8lin.gen_weights(n, K, seed=5, tag=10 + i, device=gpu)
+        eng.add(f"{p}.{name}.weight", c, s)
+    eng.fuse_weights(p + ".qkv_gate", [p + ".q_proj", p + ".k_proj", p + ".v_proj"])
+    rng = np.random.default_rng(3)
+    qw, kw = up(rand_bf16(rng, (D,), 0.1), gpu), up(rand_bf16(rng, (D,), 0.1), gpu)
+    pos = torch.from_numpy(rng.integers(0, 4096, size=(3, T), dtype=np.int64)).to(gpu)
+    rope = {"partial_rotary_factor": 0.25, "mrope_section": [11, 11, 10], "rope_theta": 10000000}
+    x = fp8lin.gen_activations(T, K, seed=9, tag=2, device=gpu)
+    q, gate, k, v = eng.full_attention_inputs(x, p, pos, qw, kw, H, HK, D, rope, 1e-6)
+    proj = eng.linear(x, p + ".qkv_gate")
+    q2, k2 = fp8lin.qk_norm_rope(proj, qw, kw, pos, H, HK, D, 64, 1e7, 11, 10, 1e-6)
+    _, gate2, _, v2 = fp8lin.LinearEngine.qkv_gate_views(proj, H, HK, D)
+    for a, b in ((q, q2), (k, k2), (gate, gate2), (v, v2)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
