@@ -155,6 +155,21 @@ at::Tensor fused_rms(at::Tensor x, at::Tensor w, double eps, bool one_center) {
     return y;
 }
 
+// include/avi/ops.h:25, src/optimized.cu:77-78
+at::Tensor fused_rope(at::Tensor x, at::Tensor pos, int64_t r, double theta, int64_t hs, int64_t ws) {
+    x = x.contiguous();
+    pos = pos.contiguous();
+    TORCH_CHECK(x.dim() == 3 && x.is_cuda() && x.scalar_type() == at::kBFloat16 && pos.device() == x.device() &&
+                    pos.scalar_type() == at::kLong && pos.dim() == 2 && pos.size(0) == 3 &&
+                    pos.size(1) == x.size(0) && r > 0 && r % 2 == 0 && r <= x.size(2),
+                "Invalid RoPE input");
+    Guard guard(x.device());
+    auto y = at::empty_like(x);
+    check(fp8lin_rope(bf(x), pos.data_ptr<int64_t>(), bf_out(y), x.size(0), x.size(1), x.size(2), r, theta, hs, ws,
+                      stream_of(x)));
+    return y;
+}
+
 // include/avi/ops.h:6, src/dual_path.cu:68-78
 std::pair<at::Tensor, at::Tensor> residual_rms(at::Tensor x, at::Tensor update, at::Tensor weight, double eps,
                                                bool centered) {
@@ -219,6 +234,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("x"), py::arg("weight"), py::arg("scales") = py::none());
     m.def("fused_swiglu", &avi::fused_swiglu);
     m.def("fused_rms", &avi::fused_rms);
+    m.def("fused_rope", &avi::fused_rope);
     m.def("residual_rms", &avi::residual_rms, py::arg("residual"), py::arg("update"), py::arg("weight"),
           py::arg("eps"), py::arg("centered") = true);
     m.def("vocabulary_candidates", &avi::vocabulary_candidates, py::arg("logits"), py::arg("offset") = 0);

@@ -286,9 +286,11 @@ void check_rms(const uint16_t* x, const uint16_t* w, const uint16_t* y, int64_t 
 // them to [0, 4096] keeps that test unchanged and the product in range.
 int clamp_section(int64_t s) { return s < 0 ? 0 : (s > 4096 ? 4096 : (int)s); }
 
-// src/optimized.cu:78: r > 0, r even, r <= D, positions [3, T].
+// src/optimized.cu:78: r > 0, r even, r <= D, positions [3, T].  Heads are
+// the second grid dimension, 4 per workgroup (at most 65535 workgroups).
+constexpr int64_t kMaxRopeHeads = 4 * 65535;
 void check_rope(int64_t T, int64_t H, int64_t D, int64_t rotary, int64_t max_d) {
-    require(T > 0 && H > 0 && D > 0 && T < kMaxDim && H < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid RoPE input");
+    require(T > 0 && H > 0 && D > 0 && T < kMaxDim && H <= kMaxRopeHeads, FP8LIN_ERR_SHAPE, "Invalid RoPE input");
     require(D <= max_d, FP8LIN_ERR_SHAPE, "RoPE input: head dimension above the kernel's limit");
     require(T * H < kMaxDim, FP8LIN_ERR_SHAPE, "RoPE input: 2^31 rows or more");
     require(rotary > 0 && rotary % 2 == 0 && rotary <= D, FP8LIN_ERR_ARGUMENT, "Invalid RoPE input: rotary size");

@@ -280,9 +280,15 @@ __global__ __launch_bounds__(128) void merge_candidates_kernel(const double* __r
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 // ---- rotary embedding ----
-// Rows of rope and qk_norm_rope: four waves per workgroup, one row of D
-// elements per wave, staged in LDS as BF16 bits.
-constexpr int kRopeRows = 4;
+// Grid (T, ceil(heads / (4 * iters))): a workgroup of 4 waves takes `iters`
+// groups of 4 heads of one token, one head per wave per iteration.  The
+// token's cos/sin pairs are computed into LDS once per workgroup and shared by
+// its heads; each wave stages one head row of D values in LDS.  Every wave
+// runs `iters` iterations and reaches every barrier (`live` is false past the
+// last head).  The launcher picks iters = 1 for short inputs (parallel heads:
+// decode latency) and all heads per workgroup for long ones (one table per
+// token); the arithmetic per element is the same either way.
+constexpr int kRopeWaves = 4;
 
 // cos and sin of pair f at token t, rounded to BF16 (src/optimized.cu:77):
 // the axis is 1 for f mod 3 == 1 below 3*hs, 2 for f mod 3 == 2 below 3*ws,
@@ -291,16 +297,15 @@ constexpr int kRopeRows = 4;
 // powf (CUDA's powf is within 2 ulp of it): at position p an ulp of the
 // frequency moves the angle by about p * 2^-24 rad, so a library-dependent
 // last bit would show at long contexts.
-__device__ __forceinline__ void rope_cos_sin(const int64_t* __restrict__ pos, int T, int t, int f, int R, float theta,
-                                             int hs, int ws, float& co, float& si) {
+__device__ __forceinline__ float2 rope_cos_sin(const int64_t* __restrict__ pos, int T, int t, int f, int R,
+                                               float theta, int hs, int ws) {
     const int axis = (f % 3 == 1 && f < hs * 3) ? 1 : ((f % 3 == 2 && f < ws * 3) ? 2 : 0);
     const float e = -2.0f * (float)f / (float)R;
     const float freq = (float)pow((double)theta, (double)e);
     const float angle = (float)pos[(int64_t)axis * T + t] * freq;
     float s, c;
     sincosf(angle, &s, &c);
-    co = bf16_bits_to_f32(f32_to_bf16_bits(c));
-    si = bf16_bits_to_f32(f32_to_bf16_bits(s));
+    return make_float2(bf16_bits_to_f32(f32_to_bf16_bits(c)), bf16_bits_to_f32(f32_to_bf16_bits(s)));
 }
 
 // bf16(bf16(x * co) + bf16(rotated * si)), the reference's rounding points.
@@ -310,82 +315,167 @@ __device__ __forceinline__ uint16_t rope_one(float x, float rotated, float co, f
     return f32_to_bf16_bits(a + b);
 }
 
-// Rotates one LDS row into y: lane l takes the pairs (f, f + R/2) for
-// f = l, l + 64, ... < R/2 (one cos/sin per pair); elements d >= R are copied.
-__device__ __forceinline__ void rope_row(const uint16_t* row, uint16_t* __restrict__ y,
-                                         const int64_t* __restrict__ pos, int T, int t, int D, int R, float theta,
-                                         int hs, int ws, int lane) {
-    const int half = R >> 1;
-    for (int f = lane; f < half; f += 64) {
-        float co, si;
-        rope_cos_sin(pos, T, t, f, R, theta, hs, ws, co, si);
-        const float x1 = bf16_bits_to_f32(row[f]), x2 = bf16_bits_to_f32(row[f + half]);
-        y[f] = rope_one(x1, -x2, co, si);
-        y[f + half] = rope_one(x2, x1, co, si);
-    }
-    for (int d = R + lane; d < D; d += 64) y[d] = row[d];
+// Dynamic LDS: cs[R/2] float2 (rounded up to 16 bytes, so the rows below are
+// 16-byte aligned for the vector accesses), then kRopeWaves rows of D BF16
+// values (row stride rounded up to 8 values).
+__host__ __device__ constexpr size_t rope_rows_offset(int R) { return ((size_t)(R / 2) * 8 + 15) / 16 * 16; }
+__host__ __device__ constexpr size_t rope_lds(int D, int R) {
+    return rope_rows_offset(R) + (size_t)kRopeWaves * ((D + 7) / 8 * 8) * 2;
 }
 
-// x, y [T, H, D]; row r = t * H + h.  Every wave reaches the barrier.
-__global__ __launch_bounds__(64 * kRopeRows) void rope_kernel(const uint16_t* __restrict__ x,
-                                                              const int64_t* __restrict__ pos,
-                                                              uint16_t* __restrict__ y, int T, int H, int D, int R,
-                                                              float theta, int hs, int ws) {
-    extern __shared__ uint16_t rows[];  // [kRopeRows][D]
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t r = (int64_t)blockIdx.x * kRopeRows + wave;
-    const bool live = r < (int64_t)T * H;
-    uint16_t* row = rows + wave * D;
+// Fills cs for token t (all threads).  Called after the row loads are
+// issued, so the table's arithmetic overlaps their latency; the barrier that
+// follows the row staging publishes it.
+__device__ __forceinline__ void rope_table(float2* cs, const int64_t* __restrict__ pos, int T, int t, int R,
+                                           float theta, int hs, int ws) {
+    for (int f = threadIdx.x; f < R / 2; f += 64 * kRopeWaves) cs[f] = rope_cos_sin(pos, T, t, f, R, theta, hs, ws);
+}
+
+// The wave's row is in LDS; rotates pairs (f, f + R/2) in place (lane l takes
+// f = l, l + 64, ...), barrier, then writes the row to y (16-byte stores when
+// VEC).  `live` is wave-uniform; every wave reaches the barrier.  Row
+// staging and the final copy use one ownership, lane l <-> 8-value chunks
+// l, l + 64, ..., so the next iteration's staging writes only what the same
+// lane has already read.
+template <bool VEC>
+__device__ __forceinline__ void rope_finish(uint16_t* row, const float2* cs, uint16_t* __restrict__ y, int D, int R,
+                                            bool live, int lane) {
+    const int half = R >> 1;
     if (live)
-        for (int d = lane; d < D; d += 64) row[d] = x[r * D + d];
+        for (int f = lane; f < half; f += 64) {
+            const float2 c = cs[f];
+            const float x1 = bf16_bits_to_f32(row[f]), x2 = bf16_bits_to_f32(row[f + half]);
+            row[f] = rope_one(x1, -x2, c.x, c.y);
+            row[f + half] = rope_one(x2, x1, c.x, c.y);
+        }
     __syncthreads();
-    if (live) rope_row(row, y + r * D, pos, T, (int)(r / H), D, R, theta, hs, ws, lane);
+    if (!live) return;
+    if constexpr (VEC) {
+        for (int c = lane; c < D / 8; c += 64)
+            *reinterpret_cast<u32x4*>(y + 8 * c) = *reinterpret_cast<const u32x4*>(row + 8 * c);
+    } else {
+        for (int c = lane; c < (D + 7) / 8; c += 64)
+            for (int d = 8 * c; d < 8 * c + 8 && d < D; ++d) y[d] = row[d];
+    }
+}
+
+// x, y [T, H, D].  VEC: D % 8 == 0 and x, y 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const uint16_t* __restrict__ x,
+                                                               const int64_t* __restrict__ pos,
+                                                               uint16_t* __restrict__ y, int T, int H, int D, int R,
+                                                               float theta, int hs, int ws, int iters) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float2* cs = reinterpret_cast<float2*>(lds);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint16_t* row = reinterpret_cast<uint16_t*>(lds + rope_rows_offset(R)) + wave * ((D + 7) / 8 * 8);
+    const int t = blockIdx.x;
+    for (int it = 0; it < iters; ++it) {
+        const int h = (blockIdx.y * iters + it) * kRopeWaves + wave;
+        const bool live = h < H;
+        const int64_t base = ((int64_t)t * H + (live ? h : 0)) * D;
+        if constexpr (VEC) {
+            // the first chunk of 8 values per lane (all of a row up to D = 512)
+            // is loaded before the table; further chunks after it
+            u32x4 v0 = {0, 0, 0, 0};
+            if (live && lane < D / 8) v0 = load_u32x4(x + base + 8 * lane);
+            if (it == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
+            if (live) {
+                if (lane < D / 8) *reinterpret_cast<u32x4*>(row + 8 * lane) = v0;
+                for (int c = lane + 64; c < D / 8; c += 64)
+                    *reinterpret_cast<u32x4*>(row + 8 * c) = load_u32x4(x + base + 8 * c);
+            }
+        } else {
+            if (it == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
+            if (live)
+                for (int c = lane; c < (D + 7) / 8; c += 64)
+                    for (int d = 8 * c; d < 8 * c + 8 && d < D; ++d) row[d] = x[base + d];
+        }
+        __syncthreads();
+        rope_finish<VEC>(row, cs, y + base, D, R, live, lane);
+    }
 }
 
 // The QKV-gate output p [T, ld] holds per token H query heads of 2D (query,
 // then gate) followed by HK key heads and HK value heads of D
-// (src/engine.cpp:279-282).  Row r = t * (H + HK) + head: the head's D values
-// are RMS-normalised with weight w (q_norm or k_norm) exactly as rms_kernel
-// does for D <= 512 -- lane l owns elements [8l, 8l + 8) and adds their
-// squares in order, one wave sum, the same normalisation arithmetic -- so the
-// result equals fp8lin_rms of the contiguous rows bit for bit; the BF16
-// result is then rotated as rope_kernel does.  q [T, H, D], k [T, HK, D].
-__global__ __launch_bounds__(64 * kRopeRows) void qk_norm_rope_kernel(
+// (src/engine.cpp:279-282).  Grid (T, ceil((H + HK) / 4)); head hh < H reads
+// query head hh, else key head hh - H.  Its D values are RMS-normalised with weight w (q_norm or
+// k_norm) exactly as rms_kernel does for D <= 512 -- lane l owns elements
+// [8l, 8l + 8) and adds their squares in order, one wave sum, the same
+// normalisation arithmetic -- so the result equals fp8lin_rms of the
+// contiguous rows bit for bit; the BF16 result is then rotated as
+// rope_kernel does.  q [T, H, D], k [T, HK, D].  VEC: D % 8 == 0, ld % 8 == 0
+// and p, q, k, the weights 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(64 * kRopeWaves) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ p, int64_t ld, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
     const int64_t* __restrict__ pos, uint16_t* __restrict__ q, uint16_t* __restrict__ k, int T, int H, int HK,
-    int D, int R, float theta, int hs, int ws, float eps, int centered) {
-    extern __shared__ uint16_t rows[];  // [kRopeRows][D]
+    int D, int R, float theta, int hs, int ws, float eps, int centered, int iters) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    float2* cs = reinterpret_cast<float2*>(lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int heads = H + HK;
-    const int64_t r = (int64_t)blockIdx.x * kRopeRows + wave;
-    const bool live = r < (int64_t)T * heads;
-    const int t = live ? (int)(r / heads) : 0, hh = live ? (int)(r % heads) : 0;
-    const bool is_q = hh < H;
-    const uint16_t* src = p + t * ld + (is_q ? (int64_t)hh * 2 * D : (int64_t)H * 2 * D + (int64_t)(hh - H) * D);
-    const uint16_t* w = is_q ? qw : kw;
-    uint16_t* dst = is_q ? q + ((int64_t)t * H + hh) * D : k + ((int64_t)t * HK + (hh - H)) * D;
-    uint16_t* row = rows + wave * D;
+    uint16_t* row = reinterpret_cast<uint16_t*>(lds + rope_rows_offset(R)) + wave * ((D + 7) / 8 * 8);
+    const int t = blockIdx.x;
     const float c = centered ? 1.0f : 0.0f;
-    float v[8];
-    float ss = 0.0f;
+    const int i0 = 8 * lane;
+    for (int it = 0; it < iters; ++it) {
+        const int hh = (blockIdx.y * iters + it) * kRopeWaves + wave;
+        const bool live = hh < H + HK;
+        const bool is_q = hh < H;
+        const uint16_t* src = p + t * ld + (is_q ? (int64_t)hh * 2 * D : (int64_t)H * 2 * D + (int64_t)(hh - H) * D);
+        const uint16_t* w = is_q ? qw : kw;
+        uint16_t* dst = is_q ? q + ((int64_t)t * H + hh) * D : k + ((int64_t)t * HK + (hh - H)) * D;
+        uint32_t xb[8], wb[8];
+        if constexpr (VEC) {
+            u32x4 v = {0, 0, 0, 0}, wv = {0, 0, 0, 0};
+            if (live && i0 < D) {
+                v = load_u32x4(src + i0);
+                wv = load_u32x4(w + i0);
+            }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int i = 8 * lane + j;
-        v[j] = live && i < D ? bf16_bits_to_f32(src[i]) : 0.0f;
-        ss = __builtin_fmaf(v[j], v[j], ss);
-    }
-    const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
+            for (int j = 0; j < 4; ++j) {
+                xb[2 * j] = v[j] & 0xffffu;
+                xb[2 * j + 1] = v[j] >> 16;
+                wb[2 * j] = wv[j] & 0xffffu;
+                wb[2 * j + 1] = wv[j] >> 16;
+            }
+        } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int i = 8 * lane + j;
-        if (live && i < D) {
-            float n = v[j] * inv;
-            if (!centered) n = bf16_bits_to_f32(f32_to_bf16_bits(n));
-            row[i] = f32_to_bf16_bits(n * (bf16_bits_to_f32(w[i]) + c));
+            for (int j = 0; j < 8; ++j) {
+                xb[j] = live && i0 + j < D ? src[i0 + j] : 0u;
+                wb[j] = live && i0 + j < D ? w[i0 + j] : 0u;
+            }
         }
+        // every thread fills its share of the table, live or not
+        if (it == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
+        if (live) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = bf16_bits_to_f32(xb[j]);
+                ss = __builtin_fmaf(v, v, ss);
+            }
+            const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
+            uint32_t o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float n = bf16_bits_to_f32(xb[j]) * inv;
+                if (!centered) n = bf16_bits_to_f32(f32_to_bf16_bits(n));
+                o[j] = f32_to_bf16_bits(n * (bf16_bits_to_f32(wb[j]) + c));
+            }
+            if constexpr (VEC) {
+                if (i0 < D)
+                    *reinterpret_cast<u32x4*>(row + i0) =
+                        u32x4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (i0 + j < D) row[i0 + j] = (uint16_t)o[j];
+            }
+        }
+        __syncthreads();
+        rope_finish<VEC>(row, cs, dst, D, R, live, lane);
     }
-    __syncthreads();
-    if (live) rope_row(row, dst, pos, T, t, D, R, theta, hs, ws, lane);
 }
 
 }  // namespace
@@ -451,21 +541,42 @@ hipError_t launch_merge_candidates(const double* gathered, int ranks, int64_t ro
     return hipGetLastError();
 }
 
+// Head groups of 4 per workgroup: all of a token's heads from T = 1024 on
+// (enough workgroups to fill the chip, one table per token), else one.
+int rope_iters(int T, int heads) { return T >= 1024 ? (heads + kRopeWaves - 1) / kRopeWaves : 1; }
+dim3 rope_grid(int T, int heads, int iters) {
+    const int per = kRopeWaves * iters;
+    return dim3((unsigned)T, (unsigned)((heads + per - 1) / per));
+}
+
 hipError_t launch_rope(const uint16_t* x, const int64_t* pos, uint16_t* y, int T, int H, int D, int R, float theta,
                        int hs, int ws, hipStream_t stream) {
-    const int64_t rows = (int64_t)T * H;
-    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((rows + kRopeRows - 1) / kRopeRows)), dim3(64 * kRopeRows),
-                       (size_t)kRopeRows * D * 2, stream, x, pos, y, T, H, D, R, theta, hs, ws);
+    const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
+    const size_t lds = rope_lds(D, R);
+    const int iters = rope_iters(T, H);
+    if (vec)
+        hipLaunchKernelGGL(rope_kernel<true>, rope_grid(T, H, iters), dim3(64 * kRopeWaves), lds, stream, x, pos, y,
+                           T, H, D, R, theta, hs, ws, iters);
+    else
+        hipLaunchKernelGGL(rope_kernel<false>, rope_grid(T, H, iters), dim3(64 * kRopeWaves), lds, stream, x, pos, y,
+                           T, H, D, R, theta, hs, ws, iters);
     return hipGetLastError();
 }
 
 hipError_t launch_qk_norm_rope(const uint16_t* p, int64_t ld, const uint16_t* qw, const uint16_t* kw,
                                const int64_t* pos, uint16_t* q, uint16_t* k, int T, int H, int HK, int D, int R,
                                float theta, int hs, int ws, float eps, bool centered, hipStream_t stream) {
-    const int64_t rows = (int64_t)T * (H + HK);
-    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((rows + kRopeRows - 1) / kRopeRows)),
-                       dim3(64 * kRopeRows), (size_t)kRopeRows * D * 2, stream, p, ld, qw, kw, pos, q, k, T, H, HK,
-                       D, R, theta, hs, ws, eps, centered ? 1 : 0);
+    const bool vec = D % 8 == 0 && ld % 8 == 0 && aligned16(p) && aligned16(qw) && aligned16(kw) && aligned16(q) &&
+                     aligned16(k);
+    const size_t lds = rope_lds(D, R);
+    const int c = centered ? 1 : 0;
+    const int iters = rope_iters(T, H + HK);
+    if (vec)
+        hipLaunchKernelGGL(qk_norm_rope_kernel<true>, rope_grid(T, H + HK, iters), dim3(64 * kRopeWaves), lds,
+                           stream, p, ld, qw, kw, pos, q, k, T, H, HK, D, R, theta, hs, ws, eps, c, iters);
+    else
+        hipLaunchKernelGGL(qk_norm_rope_kernel<false>, rope_grid(T, H + HK, iters), dim3(64 * kRopeWaves), lds,
+                           stream, p, ld, qw, kw, pos, q, k, T, H, HK, D, R, theta, hs, ws, eps, c, iters);
     return hipGetLastError();
 }
 

@@ -476,6 +476,35 @@ def head_and_epilogue(torch, fp8lin, dev, log):
         extra[f"reduce2_residual_rms_m{m}_us"] = round(ms * 1e3, 2)
         extra[f"reduce2_residual_rms_m{m}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         log(f"reduce(2 ranks)+residual_rms M={m} D={d}: {ms * 1e3:.2f} us {nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
+    # Q/K epilogue of a full-attention layer (TP=2 rank: 12 query, 2 key heads
+    # of 256, rotary 64): fused, and the unfused sequence it replaces
+    # (fused_rms of the query and key heads, then fused_rope of each).
+    H, HK, D, R = 12, 2, 256, 64
+    qw = fp8lin.gen_activations(1, D, seed=2, tag=3, device=dev)
+    for t in (1, 4096):
+        proj = fp8lin.gen_activations(t, 2 * (H + HK) * D, seed=0, tag=6, device=dev)
+        pos = torch.randint(0, 8192, (3, t), dtype=torch.int64, device=dev)
+        q = torch.empty((t, H, D), dtype=torch.bfloat16, device=dev)
+        k = torch.empty((t, HK, D), dtype=torch.bfloat16, device=dev)
+        args = (t, H, HK, D, R, 1e7, 11, 10, 1e-6, sp)
+        ms = graph_timed(torch, lambda: ok(L.fp8lin_qk_norm_rope(P(proj), proj.size(1), P(qw), P(qw), P(pos), P(q),
+                                                                 P(k), *args)), sp)
+        nbytes = 2 * t * (H + HK) * D * 2 + 2 * D * 2 + 3 * t * 8
+        qv, _, kv, _ = fp8lin.LinearEngine.qkv_gate_views(proj, H, HK, D)
+        qc, kc = qv.contiguous(), kv.contiguous()
+        qn, kn = torch.empty_like(qc), torch.empty_like(kc)
+
+        def unfused():
+            ok(L.fp8lin_rms(P(qc), P(qw), P(qn), t * H, D, 1e-6, 1, sp))
+            ok(L.fp8lin_rms(P(kc), P(qw), P(kn), t * HK, D, 1e-6, 1, sp))
+            ok(L.fp8lin_rope(P(qn), P(pos), P(q), t, H, D, R, 1e7, 11, 10, sp))
+            ok(L.fp8lin_rope(P(kn), P(pos), P(k), t, HK, D, R, 1e7, 11, 10, sp))
+        ms_u = graph_timed(torch, unfused, sp)
+        extra[f"qk_norm_rope_t{t}_us"] = round(ms * 1e3, 2)
+        extra[f"qk_norm_rope_t{t}_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        extra[f"qk_norm_rope_t{t}_unfused_us"] = round(ms_u * 1e3, 2)
+        log(f"qk_norm_rope T={t} (H={H}, HK={HK}, D={D}): {ms * 1e3:.2f} us {nbytes / (ms * 1e-3) / 1e9:.1f} GB/s; "
+            f"unfused rms+rope {ms_u * 1e3:.2f} us (graph replay)")
     return extra
 
 

@@ -93,6 +93,7 @@ def test_rope_validation(fp8lin):
     assert L.fp8lin_rope(P, P, P, 1, 12, 4098, 64, 1e7, 11, 10, None) == 1         # D limit
     assert L.fp8lin_rope(P, P, P, 1, 0, 256, 64, 1e7, 11, 10, None) == 1
     assert L.fp8lin_rope(P, P, P, 1 << 20, 1 << 12, 8, 8, 1e7, 11, 10, None) == 1  # 2^31 rows
+    assert L.fp8lin_rope(P, P, P, 1, 4 * 65535 + 1, 8, 8, 1e7, 11, 10, None) == 1  # heads: 65535 groups of 4
     args = (12, 2, 256, 64, 1e7, 11, 10, 1e-6, None)
     ld = 2 * 14 * 256
     assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 0, *args) == 0              # no tokens: no-op

@@ -2,12 +2,12 @@
 without a GPU, exports the reference's avi:: linear-path operators and
 rejects host tensors with the reference's TORCH_CHECK messages
 (src/optimized.cu:62,72-74, src/kernels.cu:18, src/fp8_tensor.cu:54,
-src/deep_kernels.cu:135, src/dual_path.cu:69,80,87)."""
+src/deep_kernels.cu:135, src/dual_path.cu:69,80,87, src/optimized.cu:78)."""
 import pytest
 import torch
 
 NAMES = ["fp8_decode", "fp8_linear", "fp8_tensor_small", "tilelang_fp8_small", "small_linear_shared",
-         "fused_swiglu", "fused_rms", "residual_rms", "vocabulary_candidates", "merge_candidates"]
+         "fused_swiglu", "fused_rms", "fused_rope", "residual_rms", "vocabulary_candidates", "merge_candidates"]
 
 
 @pytest.fixture(scope="module")
@@ -29,6 +29,7 @@ def test_exports(avi):
     (lambda a, t: a.small_linear_shared(t["x"], t["codes"], t["scales"]), "Invalid shared GEMV inputs"),
     (lambda a, t: a.fused_swiglu(t["x"]), "Invalid SwiGLU input"),
     (lambda a, t: a.fused_rms(t["x"], t["w"], 1e-6, True), "Invalid RMS input"),
+    (lambda a, t: a.fused_rope(t["x"].view(2, 4, 64), t["p"], 32, 1e4, 4, 4), "Invalid RoPE input"),
     (lambda a, t: a.residual_rms(t["x"], t["x"], t["w"], 1e-6), "Invalid fused residual RMS input"),
     (lambda a, t: a.vocabulary_candidates(t["x"], 0), "Invalid vocabulary candidates"),
     (lambda a, t: a.merge_candidates(t["g"]), "Invalid gathered candidates"),
@@ -36,7 +37,7 @@ def test_exports(avi):
 def test_rejects_host_tensors(avi, call, msg):
     t = {"x": torch.zeros(2, 256, dtype=torch.bfloat16), "codes": torch.zeros(16, 256, dtype=torch.uint8),
          "scales": torch.ones(16, 2), "w": torch.zeros(256, dtype=torch.bfloat16),
-         "g": torch.zeros(2, 3, 2, dtype=torch.float64)}
+         "g": torch.zeros(2, 3, 2, dtype=torch.float64), "p": torch.zeros(3, 2, dtype=torch.int64)}
     with pytest.raises(RuntimeError) as e:
         call(avi, t)
     assert msg in str(e.value)

@@ -181,6 +181,18 @@ def test_rms_and_swiglu(avi, gpu):
     assert close(avi.fused_swiglu(gu.to(gpu)), sg, .02, .02)
 
 
+def test_rope(avi, fp8lin, gpu):
+    """tests/optimized_test.cpp:139-141 (zero positions give x back), and
+    avi::fused_rope equals the library's rotary embedding bit for bit."""
+    g = torch.Generator().manual_seed(141)
+    x = randn(g, 3, 2, 64).to(torch.bfloat16).to(gpu)
+    zero = torch.zeros((3, 3), dtype=torch.int64, device=gpu)
+    assert torch.equal(avi.fused_rope(x, zero, 32, 10000., 4, 4), x)
+    pos = torch.randint(0, 4096, (3, 3), generator=g).to(gpu)
+    assert torch.equal(avi.fused_rope(x, pos, 32, 10000., 4, 4).view(torch.int16),
+                       fp8lin.fused_rope(x, pos, 32, 10000., 4, 4).view(torch.int16))
+
+
 def fp64_w8a16(x, codes, scales):
     """tests/fp8_tensor_test.cpp:10-19: CPU decode with the BF16 rounding of
     W8A16, FP64 product, rounded to BF16."""

@@ -343,6 +343,9 @@ ROPE_CASES = [
     ((7, 3, 128), 128, 1e4, 4, 2),       # full rotation; section bounds inside the pairs
     ((5, 3, 100), 30, 5e5, 2, 5),        # ragged head and rotary sizes
     ((2, 1, 4096), 4096, 1e4, 11, 10),   # largest head the kernel takes (2048 pairs)
+    ((3, 5, 128), 30, 1e4, 4, 2),        # odd pair count with 16-byte rows
+    ((1024, 9, 136), 64, 1e7, 11, 10),   # long input: each workgroup loops over its token's heads
+    ((1050, 6, 100), 30, 5e5, 2, 5),     # the same loop on the scalar path
 ]
 
 
@@ -403,6 +406,11 @@ QK_CASES = [
     (300, 12, 2, 256, 64, 40),   # prefill; projected is a column slice of a wider buffer
     (5, 4, 1, 100, 30, 0),       # D not a multiple of 8 (scalar path of fused_rms)
     (3, 2, 2, 512, 128, 8),      # largest fused head
+    (3, 2, 1, 512, 512, 8),      # 256 pairs: the idle fourth wave still fills its part of the table
+    (4, 3, 1, 128, 30, 0),       # odd pair count with 16-byte rows
+    (2, 5, 3, 64, 64, 3),        # row stride not a multiple of 8 (scalar path), full rotation
+    (1100, 12, 2, 256, 64, 0),   # long prefill: each workgroup loops over all 14 heads of its token
+    (1030, 5, 3, 100, 30, 3),    # the same loop on the scalar path
 ]
 
 
