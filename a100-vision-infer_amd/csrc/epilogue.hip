@@ -418,63 +418,85 @@ __global__ __launch_bounds__(64 * kRopeWaves) void qk_norm_rope_kernel(
     const int t = blockIdx.x;
     const float c = centered ? 1.0f : 0.0f;
     const int i0 = 8 * lane;
-    for (int it = 0; it < iters; ++it) {
-        const int hh = (blockIdx.y * iters + it) * kRopeWaves + wave;
-        const bool live = hh < H + HK;
-        const bool is_q = hh < H;
-        const uint16_t* src = p + t * ld + (is_q ? (int64_t)hh * 2 * D : (int64_t)H * 2 * D + (int64_t)(hh - H) * D);
-        const uint16_t* w = is_q ? qw : kw;
-        uint16_t* dst = is_q ? q + ((int64_t)t * H + hh) * D : k + ((int64_t)t * HK + (hh - H)) * D;
-        uint32_t xb[8], wb[8];
-        if constexpr (VEC) {
-            u32x4 v = {0, 0, 0, 0}, wv = {0, 0, 0, 0};
-            if (live && i0 < D) {
-                v = load_u32x4(src + i0);
-                wv = load_u32x4(w + i0);
-            }
+    auto head_src = [&](int hh) -> const uint16_t* {
+        return p + t * ld + (hh < H ? (int64_t)hh * 2 * D : (int64_t)H * 2 * D + (int64_t)(hh - H) * D);
+    };
+    // VEC: the norm weights and up to kPrefetch iterations' head chunks are
+    // loaded before the table and the first barrier, so a workgroup's HBM
+    // reads are in flight together rather than one head per round trip.
+    constexpr int kPrefetch = 4;
+    u32x4 wqv = {0, 0, 0, 0}, wkv = {0, 0, 0, 0};
+    if constexpr (VEC) {
+        if (i0 < D) {
+            wqv = load_u32x4(qw + i0);
+            wkv = load_u32x4(kw + i0);
+        }
+    }
+    for (int it0 = 0; it0 < iters; it0 += kPrefetch) {
+        u32x4 pre[kPrefetch];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                xb[2 * j] = v[j] & 0xffffu;
-                xb[2 * j + 1] = v[j] >> 16;
-                wb[2 * j] = wv[j] & 0xffffu;
-                wb[2 * j + 1] = wv[j] >> 16;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                xb[j] = live && i0 + j < D ? src[i0 + j] : 0u;
-                wb[j] = live && i0 + j < D ? w[i0 + j] : 0u;
-            }
+        for (int j = 0; j < kPrefetch; ++j) {
+            const int hh = (blockIdx.y * iters + it0 + j) * kRopeWaves + wave;
+            pre[j] = u32x4{0, 0, 0, 0};
+            if constexpr (VEC)
+                if (it0 + j < iters && hh < H + HK && i0 < D) pre[j] = load_u32x4(head_src(hh) + i0);
         }
         // every thread fills its share of the table, live or not
-        if (it == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
-        if (live) {
-            float ss = 0.0f;
+        if (it0 == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float v = bf16_bits_to_f32(xb[j]);
-                ss = __builtin_fmaf(v, v, ss);
-            }
-            const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
-            uint32_t o[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float n = bf16_bits_to_f32(xb[j]) * inv;
-                if (!centered) n = bf16_bits_to_f32(f32_to_bf16_bits(n));
-                o[j] = f32_to_bf16_bits(n * (bf16_bits_to_f32(wb[j]) + c));
-            }
+        for (int j = 0; j < kPrefetch; ++j) {
+            if (it0 + j >= iters) break;  // uniform over the workgroup
+            const int hh = (blockIdx.y * iters + it0 + j) * kRopeWaves + wave;
+            const bool live = hh < H + HK;
+            const bool is_q = hh < H;
+            const uint16_t* src = head_src(hh);
+            const uint16_t* w = is_q ? qw : kw;
+            uint16_t* dst = is_q ? q + ((int64_t)t * H + hh) * D : k + ((int64_t)t * HK + (hh - H)) * D;
+            uint32_t xb[8], wb[8];
             if constexpr (VEC) {
-                if (i0 < D)
-                    *reinterpret_cast<u32x4*>(row + i0) =
-                        u32x4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+                const u32x4 wv = is_q ? wqv : wkv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xb[2 * e] = pre[j][e] & 0xffffu;
+                    xb[2 * e + 1] = pre[j][e] >> 16;
+                    wb[2 * e] = wv[e] & 0xffffu;
+                    wb[2 * e + 1] = wv[e] >> 16;
+                }
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (i0 + j < D) row[i0 + j] = (uint16_t)o[j];
+                for (int e = 0; e < 8; ++e) {
+                    xb[e] = live && i0 + e < D ? src[i0 + e] : 0u;
+                    wb[e] = live && i0 + e < D ? w[i0 + e] : 0u;
+                }
             }
+            if (live) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float v = bf16_bits_to_f32(xb[e]);
+                    ss = __builtin_fmaf(v, v, ss);
+                }
+                const float inv = rsqrtf(wave_sum(ss) / (float)D + eps);
+                uint32_t o[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float n = bf16_bits_to_f32(xb[e]) * inv;
+                    if (!centered) n = bf16_bits_to_f32(f32_to_bf16_bits(n));
+                    o[e] = f32_to_bf16_bits(n * (bf16_bits_to_f32(wb[e]) + c));
+                }
+                if constexpr (VEC) {
+                    if (i0 < D)
+                        *reinterpret_cast<u32x4*>(row + i0) =
+                            u32x4{o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16)};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (i0 + e < D) row[i0 + e] = (uint16_t)o[e];
+                }
+            }
+            __syncthreads();
+            rope_finish<VEC>(row, cs, dst, D, R, live, lane);
         }
-        __syncthreads();
-        rope_finish<VEC>(row, cs, dst, D, R, live, lane);
     }
 }
 
