@@ -461,3 +461,32 @@ def test_engine_full_attention_inputs(fp8lin, gpu):
     _, gate2, _, v2 = fp8lin.LinearEngine.qkv_gate_views(proj, H, HK, D)
     for a, b in ((q, q2), (k, k2), (gate, gate2), (v, v2)):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_qk_norm_rope_graph_replay(fp8lin, gpu):
+    """The decode step's Q/K epilogue captured once: each replay, after the
+    projection and the positions change in place (with eager work between
+    replays), equals the eager call on the new inputs."""
+    rng = np.random.default_rng(287)
+    H, HK, D = 12, 2, 256
+    proj = up(rand_bf16(rng, (1, 2 * (H + HK) * D)), gpu)
+    qw, kw = up(rand_bf16(rng, (D,), 0.1), gpu), up(rand_bf16(rng, (D,), 0.1), gpu)
+    pos = torch.from_numpy(rng.integers(0, 4096, size=(3, 1), dtype=np.int64)).to(gpu)
+    args = (H, HK, D, 64, 1e7, 11, 10, 1e-6)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        q, k = fp8lin.qk_norm_rope(proj, qw, kw, pos, *args)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            q, k = fp8lin.qk_norm_rope(proj, qw, kw, pos, *args)
+    for i in range(4):
+        proj.copy_(up(rand_bf16(rng, tuple(proj.shape)), gpu))
+        pos += 17 * (i + 1)
+        q_eager, k_eager = fp8lin.qk_norm_rope(proj, qw, kw, pos, *args)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(q.view(torch.int16), q_eager.view(torch.int16)), f"replay {i}"
+        assert torch.equal(k.view(torch.int16), k_eager.view(torch.int16)), f"replay {i}"
