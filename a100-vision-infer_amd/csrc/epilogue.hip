@@ -6,6 +6,8 @@
 //   - the multi-axis rotary embedding of the attention heads
 //     (src/optimized.cu:77-78) and its fusion with the per-head q/k RMSNorm
 //     on the QKV-gate projection output (src/engine.cpp:279-287).
+#include <cmath>
+
 #include "device.hpp"
 #include "internal.hpp"
 
@@ -293,15 +295,18 @@ constexpr int kRopeWaves = 4;
 // cos and sin of pair f at token t, rounded to BF16 (src/optimized.cu:77):
 // the axis is 1 for f mod 3 == 1 below 3*hs, 2 for f mod 3 == 2 below 3*ws,
 // else 0; angle = float(pos) * powf(theta, -2f*f/R) in FP32.  The power is
-// evaluated in FP64 and rounded once to FP32, i.e. the correctly rounded
-// powf (CUDA's powf is within 2 ulp of it): at position p an ulp of the
-// frequency moves the angle by about p * 2^-24 rad, so a library-dependent
-// last bit would show at long contexts.
+// evaluated in FP64 as exp2(e * log2(theta)) (log2t = log2(theta), computed
+// once per launch on the host; relative error about 2^-48) and rounded once
+// to FP32, i.e. the correctly rounded powf except at near-halfway values
+// (CUDA's powf is within 2 ulp of it); f = 0 gives 1 exactly, as
+// powf(theta, -0) does.  At position p an ulp of the frequency moves the
+// angle by about p * 2^-24 rad, so a library-dependent last bit would show
+// at long contexts.
 __device__ __forceinline__ float2 rope_cos_sin(const int64_t* __restrict__ pos, int T, int t, int f, int R,
-                                               float theta, int hs, int ws) {
+                                               double log2t, int hs, int ws) {
     const int axis = (f % 3 == 1 && f < hs * 3) ? 1 : ((f % 3 == 2 && f < ws * 3) ? 2 : 0);
     const float e = -2.0f * (float)f / (float)R;
-    const float freq = (float)pow((double)theta, (double)e);
+    const float freq = f == 0 ? 1.0f : (float)exp2((double)e * log2t);
     const float angle = (float)pos[(int64_t)axis * T + t] * freq;
     float s, c;
     sincosf(angle, &s, &c);
@@ -327,8 +332,8 @@ __host__ __device__ constexpr size_t rope_lds(int D, int R) {
 // issued, so the table's arithmetic overlaps their latency; the barrier that
 // follows the row staging publishes it.
 __device__ __forceinline__ void rope_table(float2* cs, const int64_t* __restrict__ pos, int T, int t, int R,
-                                           float theta, int hs, int ws) {
-    for (int f = threadIdx.x; f < R / 2; f += 64 * kRopeWaves) cs[f] = rope_cos_sin(pos, T, t, f, R, theta, hs, ws);
+                                           double log2t, int hs, int ws) {
+    for (int f = threadIdx.x; f < R / 2; f += 64 * kRopeWaves) cs[f] = rope_cos_sin(pos, T, t, f, R, log2t, hs, ws);
 }
 
 // The wave's row is in LDS; rotates pairs (f, f + R/2) in place (lane l takes
@@ -364,7 +369,7 @@ template <bool VEC>
 __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const uint16_t* __restrict__ x,
                                                                const int64_t* __restrict__ pos,
                                                                uint16_t* __restrict__ y, int T, int H, int D, int R,
-                                                               float theta, int hs, int ws, int iters) {
+                                                               double log2t, int hs, int ws, int iters) {
     extern __shared__ __align__(16) unsigned char lds[];
     float2* cs = reinterpret_cast<float2*>(lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -379,14 +384,14 @@ __global__ __launch_bounds__(64 * kRopeWaves) void rope_kernel(const uint16_t* _
             // is loaded before the table; further chunks after it
             u32x4 v0 = {0, 0, 0, 0};
             if (live && lane < D / 8) v0 = load_u32x4(x + base + 8 * lane);
-            if (it == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
+            if (it == 0) rope_table(cs, pos, T, t, R, log2t, hs, ws);
             if (live) {
                 if (lane < D / 8) *reinterpret_cast<u32x4*>(row + 8 * lane) = v0;
                 for (int c = lane + 64; c < D / 8; c += 64)
                     *reinterpret_cast<u32x4*>(row + 8 * c) = load_u32x4(x + base + 8 * c);
             }
         } else {
-            if (it == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
+            if (it == 0) rope_table(cs, pos, T, t, R, log2t, hs, ws);
             if (live)
                 for (int c = lane; c < (D + 7) / 8; c += 64)
                     for (int d = 8 * c; d < 8 * c + 8 && d < D; ++d) row[d] = x[base + d];
@@ -410,7 +415,7 @@ template <bool VEC>
 __global__ __launch_bounds__(64 * kRopeWaves) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ p, int64_t ld, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
     const int64_t* __restrict__ pos, uint16_t* __restrict__ q, uint16_t* __restrict__ k, int T, int H, int HK,
-    int D, int R, float theta, int hs, int ws, float eps, int centered, int iters) {
+    int D, int R, double log2t, int hs, int ws, float eps, int centered, int iters) {
     extern __shared__ __align__(16) unsigned char lds[];
     float2* cs = reinterpret_cast<float2*>(lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -442,7 +447,7 @@ __global__ __launch_bounds__(64 * kRopeWaves) void qk_norm_rope_kernel(
                 if (it0 + j < iters && hh < H + HK && i0 < D) pre[j] = load_u32x4(head_src(hh) + i0);
         }
         // every thread fills its share of the table, live or not
-        if (it0 == 0) rope_table(cs, pos, T, t, R, theta, hs, ws);
+        if (it0 == 0) rope_table(cs, pos, T, t, R, log2t, hs, ws);
 #pragma unroll
         for (int j = 0; j < kPrefetch; ++j) {
             if (it0 + j >= iters) break;  // uniform over the workgroup
@@ -576,12 +581,13 @@ hipError_t launch_rope(const uint16_t* x, const int64_t* pos, uint16_t* y, int T
     const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
     const size_t lds = rope_lds(D, R);
     const int iters = rope_iters(T, H);
+    const double log2t = std::log2((double)theta);
     if (vec)
         hipLaunchKernelGGL(rope_kernel<true>, rope_grid(T, H, iters), dim3(64 * kRopeWaves), lds, stream, x, pos, y,
-                           T, H, D, R, theta, hs, ws, iters);
+                           T, H, D, R, log2t, hs, ws, iters);
     else
         hipLaunchKernelGGL(rope_kernel<false>, rope_grid(T, H, iters), dim3(64 * kRopeWaves), lds, stream, x, pos, y,
-                           T, H, D, R, theta, hs, ws, iters);
+                           T, H, D, R, log2t, hs, ws, iters);
     return hipGetLastError();
 }
 
@@ -593,12 +599,13 @@ hipError_t launch_qk_norm_rope(const uint16_t* p, int64_t ld, const uint16_t* qw
     const size_t lds = rope_lds(D, R);
     const int c = centered ? 1 : 0;
     const int iters = rope_iters(T, H + HK);
+    const double log2t = std::log2((double)theta);
     if (vec)
         hipLaunchKernelGGL(qk_norm_rope_kernel<true>, rope_grid(T, H + HK, iters), dim3(64 * kRopeWaves), lds,
-                           stream, p, ld, qw, kw, pos, q, k, T, H, HK, D, R, theta, hs, ws, eps, c, iters);
+                           stream, p, ld, qw, kw, pos, q, k, T, H, HK, D, R, log2t, hs, ws, eps, c, iters);
     else
         hipLaunchKernelGGL(qk_norm_rope_kernel<false>, rope_grid(T, H + HK, iters), dim3(64 * kRopeWaves), lds,
-                           stream, p, ld, qw, kw, pos, q, k, T, H, HK, D, R, theta, hs, ws, eps, c, iters);
+                           stream, p, ld, qw, kw, pos, q, k, T, H, HK, D, R, log2t, hs, ws, eps, c, iters);
     return hipGetLastError();
 }
 

@@ -254,7 +254,8 @@ int fp8lin_reduce_residual_rms(const uint16_t* x, const uint16_t* partials, int6
  * d < rotary, pair index f = d mod rotary/2 reads axis 1 when f mod 3 == 1
  * and f < 3*height_section, axis 2 when f mod 3 == 2 and f < 3*width_section,
  * else axis 0;
- *   angle = float(pos) * powf(float(theta), -2f*f/rotary)      (FP32)
+ *   angle = float(pos) * powf(float(theta), -2f*f/rotary)      (FP32;
+ *           the power correctly rounded to FP32 but at near-halfway values)
  *   co = bf16(cos(angle)), si = bf16(sin(angle))
  *   y[d] = bf16(bf16(x[d]*co) - bf16(x[d+rotary/2]*si))  d < rotary/2
  *   y[d] = bf16(bf16(x[d]*co) + bf16(x[d-rotary/2]*si))  rotary/2 <= d < rotary
