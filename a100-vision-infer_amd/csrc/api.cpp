@@ -132,12 +132,20 @@ void tensor_small_impl(const uint16_t* x, const uint8_t* codes, const float* sca
     require(M >= 2 && M <= 8 && N > 0 && K > 0 && K % 128 == 0 && N < kMaxDim && K < kMaxDim,
             FP8LIN_ERR_SHAPE, "Invalid FP8 W8A16 geometry: need 2 <= M <= 8, N > 0, K % 128 == 0");
     require(split == 1 || split == 4, FP8LIN_ERR_ARGUMENT, "Invalid FP8 W8A16 split: must be 1 or 4");
-    require(aligned16(x) && aligned16(codes), FP8LIN_ERR_UNSUPPORTED,
-            "FP8 W8A16 matrix-core path needs 16-byte aligned x and codes");
-    require(16 * K < kMaxDim, FP8LIN_ERR_UNSUPPORTED, "FP8 W8A16 matrix-core path needs 16 * K < 2^31");
     (void)ws;
     (void)ws_bytes;
     ensure_device();
+    // The matrix-core kernel DMAs 16-byte chunks of x and codes with 32-bit
+    // buffer offsets.  The reference accepts any contiguous tensor
+    // (src/fp8_tensor.cu:54-59), so an unaligned view or a K too large for
+    // those offsets runs the multi-row GEMV instead: same operator, same
+    // parity bar, only the FP32 summation order differs.
+    if (!aligned16(x) || !aligned16(codes) || 16 * K >= kMaxDim) {
+        check_hip(fp8lin::launch_gemv(x, codes, true, scales, (int)(K / 128), y, ldy, (int)M, (int)N, (int)K,
+                                      K % 16 == 0 && aligned16(x) && aligned16(codes), stream),
+                  "fp8 small-M fallback gemv launch");
+        return;
+    }
     check_hip(fp8lin::launch_small_m(x, codes, scales, y, ldy, (int)M, (int)N, (int)K, split, stream),
               "fp8 small-M launch");
 }
@@ -199,20 +207,33 @@ int engine_path(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t 
     return FP8LIN_PATH_BF16;
 }
 
+// The option combinations the reference's Engine constructor rejects
+// (src/engine.cpp:78-81).
+bool options_consistent(const fp8lin_linear_options& o) {
+    return !(o.fp8_tensor_small && o.tilelang_fp8) && (o.fp8_tensor_split == 1 || o.fp8_tensor_split == 4) &&
+           (!(o.fp8_tensor_small || o.tilelang_fp8) || o.optimized);
+}
+
+void check_options(const fp8lin_linear_options& o) {
+    require(!(o.fp8_tensor_small && o.tilelang_fp8), FP8LIN_ERR_ARGUMENT, "Choose one FP8 Tensor Core backend");
+    require(o.fp8_tensor_split == 1 || o.fp8_tensor_split == 4, FP8LIN_ERR_ARGUMENT,
+            "FP8 Tensor Core split must be 1 or 4");
+    require(!(o.fp8_tensor_small || o.tilelang_fp8) || o.optimized, FP8LIN_ERR_ARGUMENT,
+            "FP8 Tensor Core requires optimized mode");
+}
+
 void validate_engine(const fp8lin_linear_options& o, const fp8lin_weight& w, const uint16_t* x,
                      int64_t rows, const uint16_t* y, int64_t ldy) {
+    check_options(o);
     require(x && y && w.data, FP8LIN_ERR_ARGUMENT, "Engine linear: null pointer");
     check_dims(rows, w.N, w.K);
     require(ldy >= w.N, FP8LIN_ERR_SHAPE, "Engine linear: ldy < N");
     if (w.scales) check_scales(w.scales, w.scale_cols, w.K);
-    require(o.fp8_tensor_split == 1 || o.fp8_tensor_split == 4, FP8LIN_ERR_ARGUMENT,
-            "fp8_tensor_split must be 1 or 4");
 }
 
-int engine_impl(const fp8lin_linear_options& o, const fp8lin_weight& w, const uint16_t* x,
-                int64_t rows, uint16_t* y, int64_t ldy, void* ws, size_t ws_bytes,
-                hipStream_t stream) {
-    validate_engine(o, w, x, rows, y, ldy);
+int engine_branch(const fp8lin_linear_options& o, const fp8lin_weight& w, const uint16_t* x,
+                  int64_t rows, uint16_t* y, int64_t ldy, void* ws, size_t ws_bytes,
+                  hipStream_t stream) {
     const auto* codes = static_cast<const uint8_t*>(w.data);
     // src/engine.cpp:206-213
     if (tensor_small_eligible(o, w, rows)) {
@@ -268,6 +289,16 @@ int engine_impl(const fp8lin_linear_options& o, const fp8lin_weight& w, const ui
     // :234-237
     gemm_bf16_impl(x, static_cast<const uint16_t*>(w.data), y, ldy, rows, w.N, w.K, stream);
     return FP8LIN_PATH_BF16;
+}
+
+// The branch, then the weight's bias (src/engine.cpp:240).
+int engine_impl(const fp8lin_linear_options& o, const fp8lin_weight& w, const uint16_t* x,
+                int64_t rows, uint16_t* y, int64_t ldy, void* ws, size_t ws_bytes,
+                hipStream_t stream) {
+    validate_engine(o, w, x, rows, y, ldy);
+    const int path = engine_branch(o, w, x, rows, y, ldy, ws, ws_bytes, stream);
+    if (w.bias) check_hip(fp8lin::launch_bias(y, ldy, w.bias, rows, w.N, stream), "bias launch");
+    return path;
 }
 
 // src/dual_path.cu:69-72 (residual form) and src/optimized.cu:72 (plain form).
@@ -384,6 +415,18 @@ int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* s
     });
 }
 
+int fp8lin_add_bias(uint16_t* y, int64_t ldy, const uint16_t* bias, int64_t rows, int64_t N,
+                    fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(rows >= 0 && N >= 0 && N < kMaxDim && rows < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid bias add shape");
+        if (rows == 0 || N == 0) return;
+        require(y && bias, FP8LIN_ERR_ARGUMENT, "Bias add: null pointer");
+        require(ldy >= N, FP8LIN_ERR_SHAPE, "Bias add: ldy < N");
+        ensure_device();
+        check_hip(fp8lin::launch_bias(y, ldy, bias, rows, N, as_stream(stream)), "bias launch");
+    });
+}
+
 int fp8lin_swiglu(const uint16_t* gate_up, uint16_t* y, int64_t M, int64_t D,
                   fp8lin_stream_t stream) {
     return guarded([&] {
@@ -431,13 +474,13 @@ int fp8lin_gemm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t 
 
 size_t fp8lin_engine_linear_workspace_bytes(const fp8lin_linear_options* options,
                                             const fp8lin_weight* weight, int64_t rows) {
-    if (!options || !weight || rows <= 0) return 0;
+    if (!options || !weight || rows <= 0 || !options_consistent(*options)) return 0;
     return engine_ws(*options, *weight, rows);
 }
 
 int fp8lin_engine_linear_path(const fp8lin_linear_options* options, const fp8lin_weight* weight,
                               int64_t rows) {
-    if (!options || !weight || rows <= 0) return 0;
+    if (!options || !weight || rows <= 0 || !options_consistent(*options)) return 0;
     return engine_path(*options, *weight, rows);
 }
 
@@ -543,11 +586,11 @@ int fp8lin_qk_norm_rope(const uint16_t* projected, int64_t ld, const uint16_t* q
         if (T == 0) return;
         require(projected && q_norm && k_norm && positions && q && k, FP8LIN_ERR_ARGUMENT,
                 "Invalid Q/K norm + RoPE input: null pointer");
+        require(H > 0 && H < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid Q/K norm + RoPE input: query heads");
         require(HK > 0 && HK < kMaxDim, FP8LIN_ERR_SHAPE, "Invalid Q/K norm + RoPE input: key heads");
         check_rope(T, H + HK, D, rotary, 512);
         require(ld >= 2 * (H + HK) * D && ld < kMaxDim, FP8LIN_ERR_SHAPE,
                 "Invalid Q/K norm + RoPE input: row stride below H*2D + 2*HK*D");
-        require(std::isfinite(eps) && eps > 0, FP8LIN_ERR_ARGUMENT, "Invalid Q/K norm + RoPE input: eps");
         ensure_device();
         check_hip(fp8lin::launch_qk_norm_rope(projected, ld, q_norm, k_norm, positions, q, k, (int)T, (int)H,
                                               (int)HK, (int)D, (int)rotary, (float)theta,
@@ -623,7 +666,9 @@ size_t engine_candidates_ws(const fp8lin_linear_options& o, const fp8lin_weight&
 
 size_t fp8lin_engine_linear_candidates_workspace_bytes(const fp8lin_linear_options* options,
                                                        const fp8lin_weight* weight, int64_t rows) {
-    if (!options || !weight || rows <= 0 || weight->N <= 0 || rows >= kMaxDim || weight->N >= kMaxDim) return 0;
+    if (!options || !weight || rows <= 0 || weight->N <= 0 || rows >= kMaxDim || weight->N >= kMaxDim ||
+        !options_consistent(*options))
+        return 0;
     return engine_candidates_ws(*options, *weight, rows);
 }
 

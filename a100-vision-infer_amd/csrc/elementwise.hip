@@ -59,6 +59,22 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// Bias add y[r,c] = bf16(y[r,c] + b[c]) in place over rows of stride ldy: the
+// BF16 tensor sum `y + bias` of src/engine.cpp:240 (FP32 add, one RNE
+// rounding).
+__global__ __launch_bounds__(256) void bias_kernel(uint16_t* __restrict__ y, int64_t ldy,
+                                                   const uint16_t* __restrict__ b, int64_t rows,
+                                                   int64_t cols) {
+    const int64_t total = rows * cols;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols, c = i % cols;
+        uint16_t* p = y + r * ldy + c;
+        *p = f32_to_bf16_bits(bf16_bits_to_f32(*p) + bf16_bits_to_f32(b[c]));
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Deterministic normals.  Every multiply-add below is an explicit fmaf or two
 // separately rounded operations (contraction is off), so the host checker can
 // reproduce the bits exactly with IEEE arithmetic.
@@ -288,6 +304,13 @@ hipError_t launch_dequant(const uint8_t* codes, const float* scales, int64_t S, 
 hipError_t launch_swiglu(const uint16_t* in, uint16_t* y, int64_t M, int64_t D, hipStream_t stream) {
     hipLaunchKernelGGL(swiglu_kernel, dim3(grid_for(M * D, 256, 65535)), dim3(256), 0, stream, in, y,
                        M, D);
+    return hipGetLastError();
+}
+
+hipError_t launch_bias(uint16_t* y, int64_t ldy, const uint16_t* bias, int64_t rows, int64_t cols,
+                       hipStream_t stream) {
+    hipLaunchKernelGGL(bias_kernel, dim3(grid_for(rows * cols, 256, 65535)), dim3(256), 0, stream, y, ldy,
+                       bias, rows, cols);
     return hipGetLastError();
 }
 

@@ -44,6 +44,9 @@ hipError_t launch_dequant(const uint8_t* codes, const float* scales, int64_t S, 
                           int64_t ldy, int64_t rows, int64_t cols, hipStream_t stream);
 hipError_t launch_swiglu(const uint16_t* in, uint16_t* y, int64_t M, int64_t D,
                          hipStream_t stream);
+// y[r, c] = bf16(y[r, c] + bias[c]) for r < rows, c < cols (row stride ldy).
+hipError_t launch_bias(uint16_t* y, int64_t ldy, const uint16_t* bias, int64_t rows, int64_t cols,
+                       hipStream_t stream);
 hipError_t launch_gen_weights(uint64_t seed, uint32_t tag, int64_t N, int64_t K, float std_dev,
                               uint8_t* codes, float* scales, hipStream_t stream);
 hipError_t launch_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_t K,

@@ -40,6 +40,7 @@ EXPORTED = [
     "fp8lin_reduce_residual_rms",
     "fp8lin_rope",
     "fp8lin_qk_norm_rope",
+    "fp8lin_add_bias",
 ]
 
 
@@ -53,7 +54,7 @@ class Weight(ctypes.Structure):
     """struct fp8lin_weight"""
     _fields_ = [("data", ctypes.c_void_p), ("scales", ctypes.c_void_p),
                 ("scale_cols", ctypes.c_int64), ("cached_bf16", ctypes.c_void_p),
-                ("N", ctypes.c_int64), ("K", ctypes.c_int64)]
+                ("N", ctypes.c_int64), ("K", ctypes.c_int64), ("bias", ctypes.c_void_p)]
 
 
 class LinearOptions(ctypes.Structure):
@@ -96,6 +97,7 @@ def lib():
         "fp8lin_linear_ld": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i64, i32, vp]),
         "fp8lin_linear_swiglu": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, vp]),
         "fp8lin_swiglu": (i32, [vp, vp, i64, i64, vp]),
+        "fp8lin_add_bias": (i32, [vp, i64, vp, i64, i64, vp]),
         "fp8lin_linear_shared": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, vp]),
         "fp8lin_tensor_small_workspace_bytes": (sz, [i64, i64, i32]),
         "fp8lin_tensor_small": (i32, [vp, vp, vp, vp, i64, i64, i64, i32, vp, sz, vp]),

@@ -84,14 +84,16 @@ def read_tensor(directory, desc, device="cpu"):
 
 
 def load_linear_engine(directory, rank=0, world=1, device="cuda", options=None, weight_cache_bytes=0,
-                       tp_lm_head=False, mtp=False):
+                       tp_lm_head=False, mtp=False, cache_vision_weights=False):
     """Load one rank's tensors and prepare the linear path as
     `Engine::Engine` does (src/engine.cpp:95-143).
 
     Returns (engine, tensors, config): a LinearEngine holding every 2-D
     `.weight` matrix (FP8 codes with their scales, or BF16), fused per the
-    model's layer types when `options.optimized`; every other tensor by name;
-    the manifest's model config."""
+    model's layer types when `options.optimized`, and every BF16 `.bias`
+    vector of such a matrix (added by `LinearEngine.linear`,
+    src/engine.cpp:240); every tensor that is not a matrix by name (biases
+    included); the manifest's model config."""
     from ._lib import LinearOptions
     from .engine import LinearEngine
 
@@ -101,7 +103,7 @@ def load_linear_engine(directory, rank=0, world=1, device="cuda", options=None, 
         _fail("Invalid rank")
     config = manifest["config"]
     text = config.get("text_config", config)
-    engine = LinearEngine(options, weight_cache_bytes)
+    engine = LinearEngine(options, weight_cache_bytes, cache_vision_weights=cache_vision_weights)
     tensors = {}
     for name, desc in manifest["ranks"][rank]["tensors"].items():
         if not mtp and name.startswith("mtp."):  # src/engine.cpp:97
@@ -142,7 +144,10 @@ def load_linear_engine(directory, rank=0, world=1, device="cuda", options=None, 
             engine.fuse_weights("mtp.layers.0.self_attn.qkv_gate",
                                 ["mtp.layers.0.self_attn.q_proj", "mtp.layers.0.self_attn.k_proj",
                                  "mtp.layers.0.self_attn.v_proj"])
-    if weight_cache_bytes:  # src/engine.cpp:127-143 (layer and MTP matrices, by name)
-        engine.build_cache([n for n, w in engine.weights.items() if w.scale is not None and
-                            (n.startswith("model.language_model.layers.") or n.startswith("mtp."))])
+    for name, data in tensors.items():  # src/engine.cpp:240 finds `name.bias` by name
+        if name.endswith(".bias") and data.dim() == 1 and data.dtype == torch.bfloat16 and \
+                name[:-5] + ".weight" in engine.weights:
+            engine.add(name, data)
+    if weight_cache_bytes:  # src/engine.cpp:127-143
+        engine.build_cache(engine.cache_candidates())
     return engine, tensors, config

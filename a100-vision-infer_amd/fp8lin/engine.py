@@ -5,16 +5,51 @@ the `Engine::linear` dispatch (laoyin/a100-vision-infer src/engine.cpp:94-177,
 
 The decision table itself runs in the native library
 (`fp8lin_engine_linear`, include/fp8lin.h); this class keeps the weights as
-device tensors and hands them over as `fp8lin_weight` records.  The
-tensor-parallel reduce and the bias add that follow `linear` in the reference
-(src/engine.cpp:239-240) are outside this path.
+device tensors and hands them over as `fp8lin_weight` records, together with
+the `name.bias` vector the native call adds (src/engine.cpp:240).  The
+tensor-parallel reduce that the reference runs before the bias
+(src/engine.cpp:239) needs a second GPU and is outside this path.
 """
 import ctypes
 
 import torch
 
-from ._lib import ERR_ARGUMENT, Fp8linError, LinearOptions, Weight, check, lib
+from ._lib import (ERR_ARGUMENT, PATH_TENSOR_SMALL, Fp8linError, LinearOptions, Weight, check, lib)
 from .ops import fp8_decode, qk_norm_rope
+
+
+def check_options(options):
+    """The linear-path option checks of the reference's Engine constructor
+    (src/engine.cpp:78-81), with its messages."""
+    if options.fp8_tensor_small and options.tilelang_fp8:
+        raise Fp8linError(ERR_ARGUMENT, "Choose one FP8 Tensor Core backend")
+    if options.fp8_tensor_split not in (1, 4):
+        raise Fp8linError(ERR_ARGUMENT, "FP8 Tensor Core split must be 1 or 4")
+    if (options.fp8_tensor_small or options.tilelang_fp8) and not options.optimized:
+        raise Fp8linError(ERR_ARGUMENT, "FP8 Tensor Core requires optimized mode")
+
+
+def profile_label(name):
+    """The timing label of `Engine::linear` (src/engine.cpp:203)."""
+    if name == "lm_head":
+        return "linear.head"
+    if name.startswith("model.visual."):
+        return "linear.vision"
+    if name.startswith("mtp."):
+        return "linear.mtp"
+    return "linear.text"
+
+
+def cache_order(names, cache_vision_weights):
+    """Fill order of the decoded-weight cache (src/engine.cpp:127-137): by
+    name; with cache_vision_weights, MTP matrices first, then vision, then the
+    rest, each run still by name."""
+    names = sorted(names)
+    if cache_vision_weights:
+        def priority(n):
+            return 0 if n.startswith("mtp.") else 1 if n.startswith("model.visual.") else 2
+        names = sorted(names, key=priority)  # sorted() is stable
+    return names
 
 
 class StoredWeight:
@@ -35,19 +70,37 @@ class StoredWeight:
 
 
 class LinearEngine:
-    def __init__(self, options=None, weight_cache_bytes=0):
+    """Options are the reference's `EngineOptions` linear flags
+    (`LinearOptions`) plus `cache_vision_weights` (cache fill order) and
+    `profile_kernels` (per-label event timing, `profile_report`)."""
+
+    def __init__(self, options=None, weight_cache_bytes=0, cache_vision_weights=False, profile_kernels=False):
         self.options = options or LinearOptions()
+        check_options(self.options)
         self.weight_cache_bytes = int(weight_cache_bytes)
+        self.cache_vision_weights = bool(cache_vision_weights)
+        self.profile_kernels = bool(profile_kernels)
         self.weights = {}
+        self.biases = {}
         self.mixed_projections = {}
         self.decoded_weights = {}
         self.decoded_bytes = 0
-        self._workspace = None
+        # include/avi/engine.h:78 (reported by Engine::cache_stats, src/engine.cpp:598)
+        self.fp8_tensor_calls = 0
+        self.tilelang_fp8_calls = 0
+        self._profile_events = []
+        self._workspaces = {}
 
     # -- loading -------------------------------------------------------------
     def add(self, name, data, scale=None):
         """Register `name` (e.g. "...mlp.gate_proj.weight") with device
-        tensors: uint8 codes [N,K] + float32 scales, or BF16 [N,K]."""
+        tensors: uint8 codes [N,K] + float32 scales, or BF16 [N,K]; or a
+        BF16 bias vector [N] under "....bias"."""
+        if name.endswith(".bias") and data.dim() == 1:
+            if data.dtype != torch.bfloat16 or scale is not None:
+                raise Fp8linError(ERR_ARGUMENT, f"Bias {name} must be an unquantized BF16 vector")
+            self.biases[name] = data.contiguous()
+            return
         if data.dim() != 2 or not data.is_contiguous():
             raise Fp8linError(ERR_ARGUMENT, f"Invalid matrix {name}")
         self.weights[name] = StoredWeight(data, scale)
@@ -84,11 +137,21 @@ class LinearEngine:
         for s in sources:
             del self.weights[s + ".weight"]
 
+    def cache_candidates(self):
+        """The matrices the reference may cache (src/engine.cpp:130-132):
+        quantized layer and MTP matrices, and 2-D vision matrices when
+        cache_vision_weights is set."""
+        return [n for n, w in self.weights.items() if w.scale is not None and (
+            n.startswith("model.language_model.layers.") or n.startswith("mtp.") or
+            (self.cache_vision_weights and n.startswith("model.visual.") and w.data.dim() == 2))]
+
     def build_cache(self, names=None):
-        """Bounded decoded-BF16 cache, sorted by name (src/engine.cpp:127-143)."""
-        names = sorted(names if names is not None else
-                       [n for n, w in self.weights.items() if w.scale is not None])
-        for name in names:
+        """Bounded decoded-BF16 cache (src/engine.cpp:127-143): `names` (every
+        quantized matrix when None) in cache_order, each decoded while it fits
+        in what is left of weight_cache_bytes."""
+        if names is None:
+            names = [n for n, w in self.weights.items() if w.scale is not None]
+        for name in cache_order(names, self.cache_vision_weights):
             w = self.weights[name]
             nbytes = w.data.numel() * 2
             if nbytes <= self.weight_cache_bytes - self.decoded_bytes:
@@ -139,14 +202,68 @@ class LinearEngine:
         rec.scale_cols = (1 if w.scale.dim() == 1 else w.scale.size(1)) if w.scale is not None else 1
         rec.cached_bf16 = cached.data_ptr() if cached is not None else None
         rec.N, rec.K = w.data.size(0), w.data.size(1)
+        bias = self.biases.get(name + ".bias")
+        if bias is not None and bias.numel() != rec.N:
+            raise Fp8linError(ERR_ARGUMENT, f"Bias of {name} does not match its {rec.N} output rows")
+        rec.bias = bias.data_ptr() if bias is not None else None
         return rec
 
     def _ws(self, nbytes, device):
+        """Workspace for one call on torch's current stream.  Outside graph
+        capture each stream keeps its own buffer (concurrent calls on other
+        streams never share one), grown by replacement.  During capture the
+        call gets a fresh buffer from the capture's private pool, which the
+        graph keeps for its replays, so a later larger eager call can never
+        free memory that a graph still writes."""
         if nbytes == 0:
             return None
-        if self._workspace is None or self._workspace.numel() < nbytes:
-            self._workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        return self._workspace
+        if torch.cuda.is_current_stream_capturing():
+            return torch.empty(nbytes, dtype=torch.uint8, device=device)
+        key = torch.cuda.current_stream(device).cuda_stream
+        ws = self._workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            self._workspaces[key] = ws
+        return ws
+
+    def _count(self, path):
+        # src/engine.cpp:211-212
+        if path == PATH_TENSOR_SMALL:
+            if self.options.tilelang_fp8:
+                self.tilelang_fp8_calls += 1
+            else:
+                self.fp8_tensor_calls += 1
+
+    def _profile_begin(self, name, device):
+        if not self.profile_kernels:
+            return None
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(torch.cuda.current_stream(device))
+        self._profile_events.append((profile_label(name), start, end))
+        return end
+
+    def _profile_end(self, end, device):
+        if end is not None:
+            end.record(torch.cuda.current_stream(device))
+
+    def profile_report(self):
+        """{label: {"calls", "cuda_ms"}} over the calls since the last report
+        (Engine::profile_report, src/engine.cpp:34-43); {} unless
+        profile_kernels."""
+        report = {}
+        if not self.profile_kernels:
+            return report
+        torch.cuda.synchronize()
+        for label, start, end in self._profile_events:
+            row = report.setdefault(label, {"calls": 0, "cuda_ms": 0.0})
+            row["calls"] += 1
+            row["cuda_ms"] += start.elapsed_time(end)
+        self._profile_events.clear()
+        return report
+
+    def cache_stats(self):
+        """The linear-path entries of Engine::cache_stats (src/engine.cpp:598)."""
+        return {"fp8_tensor_calls": self.fp8_tensor_calls, "tilelang_fp8_calls": self.tilelang_fp8_calls}
 
     def local_candidates(self, x, name="lm_head", offset=0, return_path=False):
         """`Engine::local_candidates` with gpu_candidates (src/speculative.cpp:25-27):
@@ -161,14 +278,18 @@ class LinearEngine:
         ws = self._ws(need, x.device)
         path = ctypes.c_int(0)
         stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        end = self._profile_begin(name, x.device)
         check(lib().fp8lin_engine_linear_candidates(
             ctypes.byref(opt), ctypes.byref(rec), ctypes.c_void_p(x2.data_ptr()), rows, int(offset),
             ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ws.data_ptr()) if ws is not None else None, need,
             ctypes.byref(path), stream))
+        self._profile_end(end, x.device)
+        self._count(path.value)
         return (out, path.value) if return_path else out
 
     def linear(self, x, name, return_path=False):
-        """`Engine::linear(x, name)` without reduce/bias (src/engine.cpp:196-242)."""
+        """`Engine::linear(x, name)` on one rank (src/engine.cpp:196-242): the
+        branch, then the `name.bias` add; the cross-rank reduce is not run."""
         rows = x.numel() // x.size(-1)
         x2 = x.reshape(rows, x.size(-1)).contiguous()
         stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
@@ -185,6 +306,8 @@ class LinearEngine:
                 ctypes.byref(opt), arr, len(recs), ctypes.c_void_p(x2.data_ptr()), rows,
                 ctypes.c_void_p(y.data_ptr()), total,
                 ctypes.c_void_p(ws.data_ptr()) if ws is not None else None, need, stream))
+            for r in recs:
+                self._count(lib().fp8lin_engine_linear_path(ctypes.byref(opt), ctypes.byref(r), rows))
             out = y.reshape(*x.shape[:-1], total)
             return (out, None) if return_path else out
         rec = self._record(name)
@@ -192,10 +315,13 @@ class LinearEngine:
         need = lib().fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(rec), rows)
         ws = self._ws(need, x.device)
         path = ctypes.c_int(0)
+        end = self._profile_begin(name, x.device)
         check(lib().fp8lin_engine_linear(
             ctypes.byref(opt), ctypes.byref(rec), ctypes.c_void_p(x2.data_ptr()), rows,
             ctypes.c_void_p(y.data_ptr()), rec.N,
             ctypes.c_void_p(ws.data_ptr()) if ws is not None else None, need,
             ctypes.byref(path), stream))
+        self._profile_end(end, x.device)
+        self._count(path.value)
         out = y.reshape(*x.shape[:-1], rec.N)
         return (out, path.value) if return_path else out

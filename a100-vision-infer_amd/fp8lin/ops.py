@@ -105,6 +105,20 @@ def fused_swiglu(gate_up):
     return y
 
 
+def add_bias(y, bias):
+    """In place y = y + bias for BF16 y [..., N] and bias [N]: the BF16 sum of
+    src/engine.cpp:240 (FP32 add, one rounding), for a caller that reduces an
+    output across ranks before adding its bias."""
+    if not (_is_dev(y) and _is_dev(bias) and y.dtype == torch.bfloat16 and bias.dtype == torch.bfloat16 and
+            y.dim() >= 1 and bias.dim() == 1 and bias.numel() == y.size(-1) and bias.is_contiguous() and
+            y.stride(-1) == 1 and (y.dim() == 1 or y.is_contiguous())):
+        _fail(ERR_ARGUMENT, "Invalid bias add")
+    N = y.size(-1)
+    rows = y.numel() // N if N else 0
+    check(lib().fp8lin_add_bias(_ptr(y), N, _ptr(bias), rows, N, _stream(y)))
+    return y
+
+
 def small_linear_shared(x, weight, scales=None):
     """`at::Tensor small_linear_shared(x, weight, scales={})` --
     src/deep_kernels.cu:134-157."""

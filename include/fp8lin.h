@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define FP8LIN_VERSION 100 /* 1.0.0 */
+#define FP8LIN_VERSION 110 /* 1.1.0 */
 
 enum fp8lin_status {
     FP8LIN_OK = 0,
@@ -99,6 +99,15 @@ int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* s
                          fp8lin_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Bias add in place: y[r,c] = bf16(y[r,c] + bias[c]) for r < rows, c < N, y
+ * with row stride ldy >= N; the BF16 `y + b` of Engine::linear
+ * (src/engine.cpp:240), for callers that reduce an output across ranks before
+ * adding its bias.  rows == 0 or N == 0 is a no-op.
+ */
+int fp8lin_add_bias(uint16_t* y, int64_t ldy, const uint16_t* bias, int64_t rows, int64_t N,
+                    fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * SwiGLU: y[r,j] = bf16(bf16(a/(1+exp(-a))) * u), a = in[r,j], u = in[r,D+j],
  * in is [M, 2D].  Replaces `at::Tensor fused_swiglu(at::Tensor gate_up)`
  * (include/avi/ops.h:20, src/optimized.cu:73-74).
@@ -121,10 +130,12 @@ int fp8lin_linear_shared(const uint16_t* x, const void* weight, const float* sca
 
 /* ---------------------------------------------------------------------------
  * Small-M matrix-core path, 2 <= M <= 8, K % 128 == 0, block scales
- * [N, K/128], split in {1, 4}.  split == 4 sums the FP32 partials of the
- * reference's four K ranges in the fixed order ((p0+p1)+p2)+p3 inside each
- * workgroup, so no workspace is needed: the workspace size is 0 and the
- * workspace arguments are accepted and ignored.  Replaces
+ * [N, K/128], split in {1, 4}.  The K partition is the kernel's own, so
+ * split 1 and split 4 give the same bits and no workspace is needed: the
+ * workspace size is 0 and the workspace arguments are accepted and ignored.
+ * Like the reference, any contiguous x and codes are accepted: when either
+ * is not 16-byte aligned (a view at an odd offset) or 16*K >= 2^31, the call
+ * runs the multi-row decode GEMV instead (same parity bar).  Replaces
  * `at::Tensor fp8_tensor_small(at::Tensor x, at::Tensor codes,
  *                              at::Tensor scales, int split=1)`
  * (include/avi/ops.h:10, src/fp8_tensor.cu:53-71); the same contract serves
@@ -150,9 +161,16 @@ int fp8lin_gemm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t 
  * tilelang_fp8 additionally N%16==0) -> multi-token shared GEMV (rows 2..8)
  * -> cached BF16 GEMM (rows > 1) -> fp8_linear (optimized, unless
  * cublas_prefill and rows > 8) -> dequant-then-GEMM in 2048-row slabs
- * (src/engine.cpp:225-233) -> BF16 GEMM for unquantized weights.
- * The bias add and the tensor-parallel reduce that follow in the reference
- * are outside this call.
+ * (src/engine.cpp:225-233) -> BF16 GEMM for unquantized weights.  Then, when
+ * the weight has a bias, y = bf16(y + bias) (src/engine.cpp:240).
+ * The tensor-parallel reduce that the reference runs between the product and
+ * the bias (src/engine.cpp:239) is the caller's: for a weight whose output is
+ * reduced across ranks, pass bias = NULL here and call fp8lin_add_bias after
+ * the reduce.  Options that the reference's Engine constructor rejects
+ * (fp8_tensor_small together with tilelang_fp8, either of them without
+ * optimized, a split other than 1 or 4; src/engine.cpp:78-81) make every
+ * engine entry point return FP8LIN_ERR_ARGUMENT (and the *_workspace_bytes
+ * and *_path queries 0).
  */
 typedef struct fp8lin_weight {
     const void* data;            /* uint8 codes [N,K], or BF16 [N,K] if scales == NULL */
@@ -160,6 +178,7 @@ typedef struct fp8lin_weight {
     int64_t scale_cols;          /* 1 or ceil(K/128); ignored for BF16 weights */
     const uint16_t* cached_bf16; /* optional decoded copy [N,K] (bounded cache) or NULL */
     int64_t N, K;
+    const uint16_t* bias;        /* optional BF16 [N] (`name.bias`), or NULL */
 } fp8lin_weight;
 
 typedef struct fp8lin_linear_options {
@@ -274,7 +293,8 @@ int fp8lin_rope(const uint16_t* x, const int64_t* positions, uint16_t* y, int64_
  * rope(rms(query), q_norm) and k [T, HK, D] = rope(rms(key), k_norm), with
  * the centered RMSNorm of fp8lin_rms and fp8lin_rope's rotation.  Bit-identical
  * to fp8lin_rms of the contiguous query (key) rows followed by fp8lin_rope.
- * The gate and value heads stay views of projected.  Requires D <= 512.
+ * The gate and value heads stay views of projected.  Requires H > 0, HK > 0,
+ * D <= 512; eps is used as given, as by fp8lin_rms.
  * Replaces the optimized branch of src/engine.cpp:279-287 (norm(q_norm),
  * norm(k_norm), fused_rope(q), fused_rope(k)).
  */

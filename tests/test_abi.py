@@ -29,7 +29,7 @@ def test_header_symbols_exported(fp8lin):
 
 def test_version_and_error_string(fp8lin):
     L = fp8lin.lib()
-    assert L.fp8lin_version() == 100
+    assert L.fp8lin_version() == 110
     assert isinstance(L.fp8lin_last_error(), bytes)
 
 
@@ -104,9 +104,9 @@ def test_rope_validation(fp8lin):
     assert L.fp8lin_qk_norm_rope(P, 4 * 14 * 576, P, P, P, P, P, 1, 12, 2, 576, 64, 1e7, 11, 10, 1e-6,
                                  None) == 1                                        # D <= 512
     assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 12, 2, 256, 65, 1e7, 11, 10, 1e-6, None) == 2
-    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 12, 2, 256, 64, 1e7, 11, 10, 0.0, None) == 2
-    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 12, 2, 256, 64, 1e7, 11, 10, float("nan"),
-                                 None) == 2
+    # query heads: H = -1 with H + HK > 0 must not reach the kernel
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, -1, 5, *args[2:]) == 1
+    assert L.fp8lin_qk_norm_rope(P, ld, P, P, P, P, P, 1, 0, 2, *args[2:]) == 1
 
 
 def test_epilogue_validation(fp8lin):
@@ -218,6 +218,36 @@ def test_engine_splitk_workspace(fp8lin):
     assert ws(256, 256, 20) == 0                          # one 256-K chunk
     assert ws(256, 640, 20) == 0                          # K % 256 != 0: general GEMM
     assert ws(7168, 5120, 8) == 0                         # GEMV rows
+
+
+def test_engine_option_consistency(fp8lin):
+    """The option combinations the reference's Engine constructor rejects
+    (src/engine.cpp:78,81) are argument errors; the queries return 0."""
+    F, O = fp8lin, fp8lin.LinearOptions
+    L = F.lib()
+    w = _weight(F)
+    for opt in (O(fp8_tensor_small=True, tilelang_fp8=True), O(fp8_tensor_small=True, optimized=False),
+                O(tilelang_fp8=True, optimized=False), O(fp8_tensor_split=2)):
+        assert _path(F, opt, w, 4) == 0
+        assert L.fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(w), 512) == 0
+        assert L.fp8lin_engine_linear_candidates_workspace_bytes(ctypes.byref(opt), ctypes.byref(w), 4) == 0
+        rc = L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(w), P, 4, P, 256, None, 0, None, None)
+        assert rc == F.ERR_ARGUMENT
+        rc = L.fp8lin_engine_linear_candidates(ctypes.byref(opt), ctypes.byref(w), P, 4, 0, P, P, 1 << 20,
+                                               None, None)
+        assert rc == F.ERR_ARGUMENT
+    # optimized=False alone stays valid (the dequant-then-GEMM branch)
+    assert _path(F, O(optimized=False), w, 4) == F.PATH_DEQUANT_GEMM
+
+
+def test_bias_validation(fp8lin):
+    L = fp8lin.lib()
+    assert L.fp8lin_add_bias(P, 8, P, 0, 8, None) == 0      # no rows: no-op
+    assert L.fp8lin_add_bias(P, 8, P, 4, 0, None) == 0      # no columns: no-op
+    assert L.fp8lin_add_bias(None, 8, P, 4, 8, None) == 2
+    assert L.fp8lin_add_bias(P, 8, None, 4, 8, None) == 2
+    assert L.fp8lin_add_bias(P, 7, P, 4, 8, None) == 1      # ldy < N
+    assert L.fp8lin_add_bias(P, 8, P, -1, 8, None) == 1
 
 
 def test_engine_validation(fp8lin):

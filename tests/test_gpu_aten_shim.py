@@ -219,6 +219,21 @@ def test_tensor_small_fp64_oracle(avi, gpu, m, k, n):
             assert torch.equal(avi.tilelang_fp8_small(x, codes, scales, split), out)
 
 
+def test_tensor_small_unaligned_views(avi, gpu):
+    """Any contiguous x and codes (src/fp8_tensor.cu:54-59), here views at an
+    odd element offset (the pattern of tests/optimized_test.cpp:15-21): the
+    operator returns the FP64-oracle result instead of throwing."""
+    g = torch.Generator().manual_seed(917)
+    m, n, k = 4, 19, 384
+    x = (randn(g, m * k + 1) * .1).to(torch.bfloat16).to(gpu).narrow(0, 1, m * k).reshape(m, k)
+    codes = randint(g, 0, 126, (n * k + 1,)).to(torch.uint8).to(gpu).narrow(0, 1, n * k).reshape(n, k)
+    scales = (torch.rand(n, k // 128, generator=g) * .001 + .0001).to(gpu)
+    expected = fp64_w8a16(x, codes, scales)
+    for split in (1, 4):
+        out = avi.fp8_tensor_small(x, codes, scales, split)
+        assert torch.isfinite(out.float()).all() and close(out, expected, .01, .001)
+
+
 def test_tensor_small_graph_replay(avi, gpu):
     """tests/fp8_tensor_test.cpp:37-49."""
     g = torch.Generator().manual_seed(916)

@@ -1,0 +1,186 @@
+"""GPU parity at every shape the benchmark times, the way
+the reference's linear benchmark checks each shape it times
+(tests/linear_benchmark.cpp:22-23,35-47):
+
+- decode gate/up + SwiGLU at M = 1, 2 on 17408 x 5120 (all 8704 outputs), and
+  the K = 8704 SwiGLU GEMV forms;
+- prefill gate/up + SwiGLU at M = 512 and 1024 on every row, and at the real
+  prompt length M = 3913 (a partial last 256-row tile) on a row sample plus
+  every row of that tile;
+- the vocab-sharded output head 75968 x 5120 at M = 1 (every logit and the
+  candidates) and at M = 512 (a row sample, plus the 192-column tail of the
+  last 256-row weight tile on every row);
+- the GDN in_proj_all mixed group, 8192 FP8 rows + 48 BF16 rows at K = 5120
+  (src/engine.cpp:198-199, tests/linear_benchmark.cpp:22), at M = 1, 4, 512;
+- fp8_tensor_small on unaligned contiguous views (the reference accepts any
+  contiguous tensor, src/fp8_tensor.cu:54-59).
+
+Inputs are the benchmark's seeded device-generated weights and activations
+(bit-identical to the oracle's generator).
+"""
+import numpy as np
+import pytest
+import torch
+
+from parity import assert_parity, ulp_distance
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def weights(fp8lin, dev, n, k, tag=1):
+    codes, scales = fp8lin.gen_weights(n, k, seed=0, tag=tag, device=dev)
+    return codes, scales, codes.cpu().numpy(), scales.cpu().numpy()
+
+
+def check_swiglu(fp8lin, oracle, x, codes, scales, c_np, s_np, rows, what):
+    """Fused gate/up + SwiGLU on the x rows `rows`: the unfused gate/up at the
+    parity bar against the oracle; the fused output bit-equal to
+    fused_swiglu(fp8_linear) (the same per-row sums, the same epilogue
+    helper), within 1 ulp of the oracle SwiGLU of the device's own gate/up,
+    and at the bar against the oracle composition."""
+    fused = fp8lin.linear_swiglu(x, codes, scales)
+    gate_up = fp8lin.fp8_linear(x, codes, scales, True)
+    assert torch.equal(fused, fp8lin.fused_swiglu(gate_up)), f"{what}: fused != unfused"
+    ref_gu = oracle.linear(bits(x)[rows], c_np, s_np)
+    gu = bits(gate_up)[rows]
+    assert_parity(gu, ref_gu, f"{what} gate/up")
+    f = bits(fused)[rows]
+    assert ulp_distance(f, oracle.swiglu(gu)).max() <= 1, what
+    assert_parity(f, oracle.swiglu(ref_gu), f"{what} swiglu", elementwise=False)
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_decode_gate_up_swiglu(fp8lin, gpu, oracle, m):
+    """Config 5, M = 1 link and config 3 M = 2: gemv_ring_kernel<M,2,5,SWIGLU>."""
+    n, k = 17408, 5120
+    codes, scales, c_np, s_np = weights(fp8lin, gpu, n, k)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=gpu)
+    check_swiglu(fp8lin, oracle, x, codes, scales, c_np, s_np, np.arange(m), f"gate/up M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_swiglu_gemv_k8704(fp8lin, gpu, oracle, m):
+    """K = 8704: the nine-step ring kernel at M = 1, the general kernel at
+    M = 2."""
+    n, k = 2048, 8704
+    codes, scales, c_np, s_np = weights(fp8lin, gpu, n, k, tag=3)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=4, device=gpu)
+    check_swiglu(fp8lin, oracle, x, codes, scales, c_np, s_np, np.arange(m), f"swiglu K=8704 M={m}")
+
+
+@pytest.mark.parametrize("m", [512, 1024])
+def test_prefill_swiglu_all_rows(fp8lin, gpu, oracle, m):
+    """Config 4 chunks, every row against the oracle."""
+    n, k = 17408, 5120
+    codes, scales, c_np, s_np = weights(fp8lin, gpu, n, k)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=gpu)
+    check_swiglu(fp8lin, oracle, x, codes, scales, c_np, s_np, np.arange(m), f"prefill M={m}")
+
+
+def test_prefill_swiglu_prompt_length(fp8lin, gpu, oracle):
+    """M = 3913 (text + image tokens): the last 256-row M tile holds 73 rows."""
+    n, k, m = 17408, 5120, 3913
+    codes, scales, c_np, s_np = weights(fp8lin, gpu, n, k)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=gpu)
+    rng = np.random.default_rng(m)
+    rows = np.unique(np.concatenate([rng.choice(m - 73, 24, replace=False), np.arange(m - 73, m)]))
+    check_swiglu(fp8lin, oracle, x, codes, scales, c_np, s_np, rows, "prefill M=3913")
+
+
+@pytest.fixture(scope="module")
+def head(fp8lin, gpu):
+    n, k = 75968, 5120
+    return weights(fp8lin, gpu, n, k, tag=5)
+
+
+def test_head_m1(fp8lin, gpu, oracle, head):
+    """Config 5 head at decode: every logit; candidates equal the oracle's
+    candidates of the device logits, and the fused call equals
+    vocabulary_candidates(fp8_linear) bit for bit."""
+    codes, scales, c_np, s_np = head
+    x = fp8lin.gen_activations(1, 5120, seed=0, tag=6, device=gpu)
+    logits = fp8lin.fp8_linear(x, codes, scales, True)
+    lb = bits(logits)
+    assert_parity(lb, oracle.linear(bits(x), c_np, s_np), "head M=1")
+    offset = 75968
+    cand = fp8lin.vocabulary_candidates(logits, offset)
+    assert np.array_equal(cand.cpu().numpy(), oracle.vocab_candidates(lb, offset))
+    fused = fp8lin.linear_candidates(x, codes, scales, offset)
+    assert torch.equal(fused, cand)
+
+
+def test_head_m512(fp8lin, gpu, oracle, head):
+    """Config 5 head at the prefill chunk: a sample of 8 rows on every column,
+    and every row on the 192 columns past the last full 256-row weight tile
+    (75776..75967)."""
+    codes, scales, c_np, s_np = head
+    m, n = 512, 75968
+    x = fp8lin.gen_activations(m, 5120, seed=0, tag=6, device=gpu)
+    y = bits(fp8lin.fp8_linear(x, codes, scales))
+    xb = bits(x)
+    rows = np.array([0, 1, 100, 255, 256, 300, 510, 511])
+    assert_parity(y[rows], oracle.linear(xb[rows], c_np, s_np), "head M=512 rows")
+    tail = (75776, n)
+    ref = oracle.linear(xb, c_np, s_np, rows=tail)
+    assert_parity(y[:, tail[0]:], ref[:, tail[0]:], "head M=512 column tail")
+
+
+@pytest.mark.parametrize("m", [1, 4, 512])
+def test_gdn_in_proj_all(fp8lin, gpu, oracle, m):
+    """The GDN in_proj_all group at one rank's size: FP8 qkv (5120 rows) + z
+    (3072) fused into 8192 rows, then BF16 b + a (24 + 24); the output is the
+    column concatenation of the four projections (src/engine.cpp:198-199)."""
+    F, k = fp8lin, 5120
+    eng = F.LinearEngine(F.LinearOptions(fp8_tensor_small=m in (2, 4, 8)))
+    parts = []
+    for i, (name, rows) in enumerate([("in_proj_qkv", 5120), ("in_proj_z", 3072)]):
+        codes, scales, c_np, s_np = weights(F, gpu, rows, k, tag=10 + i)
+        eng.add(f"l.{name}.weight", codes, scales)
+        parts.append(("fp8", c_np, s_np))
+    for i, name in enumerate(["in_proj_b", "in_proj_a"]):
+        w = (F.gen_activations(24, k, seed=1, tag=20 + i, device=gpu).float() * 0.02).to(torch.bfloat16)
+        eng.add(f"l.{name}.weight", w.contiguous())
+        parts.append(("bf16", bits(w), None))
+    eng.fuse_weights("l.in_proj_all", ["l.in_proj_qkv", "l.in_proj_z", "l.in_proj_b", "l.in_proj_a"])
+    assert eng.mixed_projections["l.in_proj_all"] == ["l.in_proj_all.group0", "l.in_proj_all.group1"]
+    x = F.gen_activations(m, k, seed=0, tag=7, device=gpu)
+    y = bits(eng.linear(x, "l.in_proj_all"))
+    assert y.shape == (m, 8240)
+    sample = np.arange(m) if m <= 8 else np.array([0, 7, 255, 256, 400, 511])
+    xb = bits(x)[sample]
+    ref = np.concatenate([oracle.linear(xb, c, s) if kind == "fp8" else oracle.linear_bf16w(xb, c)
+                          for kind, c, s in parts], axis=1)
+    assert_parity(y[sample], ref, f"in_proj_all M={m}")
+    if m == 4:
+        assert eng.cache_stats()["fp8_tensor_calls"] == 1
+
+
+@pytest.mark.parametrize("m,k", [(2, 256), (4, 5120), (8, 384)])
+def test_tensor_small_unaligned_views(fp8lin, gpu, oracle, m, k):
+    """An unaligned contiguous view of x or of the codes (the reference's own
+    pattern, tests/optimized_test.cpp:15-21) is served, not refused: the
+    multi-row GEMV runs instead, bit-equal to fp8_linear on the same views,
+    and at the parity bar against the oracle."""
+    rng = np.random.default_rng(m * k)
+    n = 19
+    codes_np = rng.integers(0, 126, (n, k), dtype=np.uint8)
+    scales_np = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x32 = rng.standard_normal(m * k).astype(np.float32)
+    xflat = torch.zeros(m * k + 1, dtype=torch.bfloat16, device=gpu)
+    xflat[1:] = torch.from_numpy(x32).to(torch.bfloat16).to(gpu)
+    xu = xflat.narrow(0, 1, m * k).reshape(m, k)
+    cflat = torch.zeros(n * k + 1, dtype=torch.uint8, device=gpu)
+    cflat[1:] = torch.from_numpy(codes_np.reshape(-1)).to(gpu)
+    cu = cflat.narrow(0, 1, n * k).reshape(n, k)
+    ca = torch.from_numpy(codes_np).to(gpu)
+    s = torch.from_numpy(scales_np).to(gpu)
+    ref = oracle.linear(bits(xu), codes_np, scales_np)
+    for xx, cc, what in [(xu, ca, "x"), (xu.clone(), cu, "codes"), (xu, cu, "both")]:
+        for split in (1, 4):
+            y = fp8lin.fp8_tensor_small(xx, cc, s, split)
+            assert_parity(bits(y), ref, f"unaligned {what} m={m} k={k} split={split}")
+            assert torch.equal(y, fp8lin.fp8_linear(xx, cc, s)), what

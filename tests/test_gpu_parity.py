@@ -471,3 +471,85 @@ def test_swiglu_every_gate_value(fp8lin, gpu, oracle):
         bad = (y != ref) & ~both_nan
         assert not bad.any(), (f"{int(bad.sum())} of 65536 differ, e.g. a={a[bad][:8]} "
                                f"got={y[bad][:8]} want={ref[bad][:8]}")
+
+
+# ------------------------------------------------------------------ bias add
+def test_engine_bias(fp8lin, gpu, oracle):
+    """Engine::linear adds `name.bias` after the product as a BF16 tensor sum
+    (src/engine.cpp:240): on every branch the biased output equals torch's
+    BF16 `y + b` of the unbiased one, bit for bit; mixed groups add each
+    group's own bias; the head candidates see the biased logits."""
+    F = fp8lin
+    rng = np.random.default_rng(21)
+    n, k = 272, 640
+    codes, scales = rand_codes(rng, n, k), (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    bias = up(rand_bf16(rng, (n,), 0.5), gpu)
+    cases = [(F.LinearOptions(), 1), (F.LinearOptions(), 33), (F.LinearOptions(fp8_tensor_small=True), 4),
+             (F.LinearOptions(multi_token_gemv=True), 3), (F.LinearOptions(cublas_prefill=True), 20),
+             (F.LinearOptions(), 600)]
+    for opt, rows in cases:
+        plain, biased = F.LinearEngine(opt), F.LinearEngine(opt)
+        for e in (plain, biased):
+            e.add("h.weight", up(codes, gpu), up(scales, gpu))
+        biased.add("h.bias", bias)
+        x = up(rand_bf16(rng, (rows, k)), gpu)
+        y0, y1 = plain.linear(x, "h"), biased.linear(x, "h")
+        assert torch.equal(y1, y0 + bias), (opt, rows)
+        c1 = biased.local_candidates(x, "h", offset=7)
+        assert torch.equal(c1, F.vocabulary_candidates(y0 + bias, 7)), (opt, rows)
+        y2 = y0.clone()
+        F.add_bias(y2, bias)
+        assert torch.equal(y2, y1)
+    # mixed FP8 / BF16 groups, each with its own bias
+    eng = F.LinearEngine()
+    w8, s8 = up(codes, gpu), up(scales, gpu)
+    wb = up(rand_bf16(rng, (48, k), 0.05), gpu)
+    eng.add("g.fp8.weight", w8, s8)
+    eng.add("g.bf.weight", wb)
+    eng.fuse_weights("g.all", ["g.fp8", "g.bf"])
+    assert eng.mixed_projections["g.all"] == ["g.fp8", "g.bf"]
+    bb = up(rand_bf16(rng, (48,), 0.5), gpu)
+    x = up(rand_bf16(rng, (5, k)), gpu)
+    y0 = eng.linear(x, "g.all")
+    eng.add("g.fp8.bias", bias)
+    eng.add("g.bf.bias", bb)
+    y1 = eng.linear(x, "g.all")
+    assert torch.equal(y1, y0 + torch.cat([bias, bb]))
+
+
+def test_engine_workspace_under_capture(fp8lin, gpu, oracle):
+    """A captured LinearEngine call keeps its own workspace: larger eager calls
+    between replays (on the capture stream and on another) grow and replace
+    the engine's per-stream buffers without touching the graph's, so every
+    replay still matches eager (the MTP draft graph captures
+    Engine::local_candidates, src/speculative.cpp:113-121)."""
+    F = fp8lin
+    rng = np.random.default_rng(22)
+    n, k = 4096, 512
+    codes, scales = rand_codes(rng, n, k), (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    eng = F.LinearEngine()
+    eng.add("lm_head.weight", up(codes, gpu), up(scales, gpu))
+    x = up(rand_bf16(rng, (1, k)), gpu)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        out = eng.local_candidates(x)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = eng.local_candidates(x)
+            logits = eng.linear(x, "lm_head")
+    for i in range(4):
+        x.copy_(up(rand_bf16(rng, (1, k)), gpu))
+        big = up(rand_bf16(rng, (600 + 100 * i, k)), gpu)
+        with torch.cuda.stream(stream):
+            eng.local_candidates(big)
+            eng.linear(big, "lm_head")
+        eng.local_candidates(big)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = eng.local_candidates(x)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        assert torch.equal(logits, eng.linear(x, "lm_head")), f"replay {i}"

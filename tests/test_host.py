@@ -79,3 +79,65 @@ def test_qkv_gate_views(fp8lin):
     import pytest
     with pytest.raises(fp8lin.Fp8linError):
         fp8lin.LinearEngine.qkv_gate_views(fused[:, 1:], H, HK, D)
+
+
+def test_engine_option_checks(fp8lin):
+    """The Engine constructor's linear-path option checks (src/engine.cpp:78-81)."""
+    O = fp8lin.LinearOptions
+    for opt, msg in [(O(fp8_tensor_small=True, tilelang_fp8=True), "Choose one FP8 Tensor Core backend"),
+                     (O(fp8_tensor_small=True, optimized=False), "FP8 Tensor Core requires optimized mode"),
+                     (O(tilelang_fp8=True, optimized=False), "FP8 Tensor Core requires optimized mode"),
+                     (O(fp8_tensor_split=2), "FP8 Tensor Core split must be 1 or 4")]:
+        with pytest.raises(fp8lin.Fp8linError, match=msg) as e:
+            fp8lin.LinearEngine(opt)
+        assert e.value.code == fp8lin.ERR_ARGUMENT
+    fp8lin.LinearEngine(O(optimized=False))
+    fp8lin.LinearEngine(O(tilelang_fp8=True, fp8_tensor_split=4))
+
+
+def test_profile_labels_and_cache_order():
+    """Engine::linear's timing labels (src/engine.cpp:203) and the decoded
+    cache's fill order (src/engine.cpp:133-137)."""
+    from fp8lin.engine import cache_order, profile_label
+    assert profile_label("lm_head") == "linear.head"
+    assert profile_label("model.visual.blocks.0.mlp.fc1") == "linear.vision"
+    assert profile_label("mtp.layers.0.mlp.gate_up") == "linear.mtp"
+    assert profile_label("model.language_model.layers.3.mlp.down_proj") == "linear.text"
+    names = ["model.language_model.layers.1.a.weight", "model.visual.b.weight", "mtp.layers.0.z.weight",
+             "model.language_model.layers.0.a.weight", "model.visual.a.weight", "mtp.fc.weight"]
+    assert cache_order(names, False) == sorted(names)
+    assert cache_order(names, True) == ["mtp.fc.weight", "mtp.layers.0.z.weight", "model.visual.a.weight",
+                                        "model.visual.b.weight", "model.language_model.layers.0.a.weight",
+                                        "model.language_model.layers.1.a.weight"]
+
+
+def test_cache_candidates_and_budget(fp8lin):
+    """Which matrices the cache may hold (src/engine.cpp:130-132) and the
+    budget rule: a matrix is decoded only if it fits in what is left."""
+    eng = fp8lin.LinearEngine(cache_vision_weights=True)
+    for name in ["model.language_model.layers.0.mlp.down_proj.weight", "mtp.fc.weight",
+                 "model.visual.blocks.0.attn.qkv.weight", "lm_head.weight"]:
+        eng.add(name, *_fp8(128, 128))
+    eng.add("model.language_model.layers.0.in_proj_b.weight", torch.zeros(4, 128, dtype=torch.bfloat16))
+    assert sorted(eng.cache_candidates()) == ["model.language_model.layers.0.mlp.down_proj.weight",
+                                              "model.visual.blocks.0.attn.qkv.weight", "mtp.fc.weight"]
+    eng.cache_vision_weights = False
+    assert "model.visual.blocks.0.attn.qkv.weight" not in eng.cache_candidates()
+
+
+def test_bias_record(fp8lin):
+    """`name.bias` travels with the weight record (added after the product,
+    src/engine.cpp:240); a bias of the wrong length or dtype is rejected."""
+    eng = fp8lin.LinearEngine()
+    eng.add("h.weight", *_fp8(16, 256))
+    assert eng._record("h").bias is None
+    b = torch.randn(16).to(torch.bfloat16)
+    eng.add("h.bias", b)
+    assert eng._record("h").bias == eng.biases["h.bias"].data_ptr()
+    eng.add("h.bias", torch.randn(15).to(torch.bfloat16))
+    with pytest.raises(fp8lin.Fp8linError):
+        eng._record("h")
+    with pytest.raises(fp8lin.Fp8linError):
+        eng.add("g.bias", torch.randn(16))
+    assert eng.cache_stats() == {"fp8_tensor_calls": 0, "tilelang_fp8_calls": 0}
+    assert eng.profile_report() == {}

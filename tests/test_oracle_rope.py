@@ -147,3 +147,26 @@ def test_qk_norm_rope_layout(oracle):
                                                      kh.reshape(T, -1), vh.reshape(T, -1)], -1),
                                      qw, kw, pos, H, HK, D, R, 1e6, 3, 2, 1e-6)
     assert not close(swapped, q, 0.5, 4)
+
+
+@pytest.mark.parametrize("theta,rotary", [(1e7, 64), (1e4, 128), (5e5, 30), (1e4, 4096), (1e4, 30)])
+def test_frequency_exp2_form_is_powf(theta, rotary):
+    """The device computes the inverse frequency theta^(-2f/R) as
+    float(exp2(double(e) * log2(double(float(theta))))) with e = -2f/R in
+    FP32 and log2 from the host.  For every pair of the tested (theta, R)
+    combinations that equals the FP32 powf the oracle uses (glibc's, correctly
+    rounded), so the device and the oracle rotate by the same angles."""
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.powf.restype = ctypes.c_float
+    libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    t32 = np.float32(theta)
+    log2t = np.log2(np.float64(t32))
+    bad = []
+    for f in range(1, rotary // 2):
+        e = np.float32(np.float32(-2.0) * np.float32(f)) / np.float32(rotary)
+        dev = np.float32(np.exp2(np.float64(e) * log2t))
+        ref = np.float32(libm.powf(float(t32), float(e)))
+        if dev != ref:
+            bad.append((f, float(dev), float(ref)))
+    assert not bad, bad
