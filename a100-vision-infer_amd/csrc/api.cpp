@@ -55,8 +55,24 @@ int guarded(F&& body) {
 constexpr int kMaxDevices = 64;
 std::mutex g_device_mutex;
 int g_device_state[kMaxDevices];  // 0 unknown, 1 gfx950, -1 other
+// Device address of `scratch` on each GPU (each holds its own copy).
+void* g_scratch[kMaxDevices];
 
-void ensure_device() {
+}  // namespace
+
+// Scratch of the allocation-free entry point fp8lin_linear_candidates_static:
+// the head logits and the candidate chunk pairs.  Every GPU the library runs
+// on holds FP8LIN_STATIC_SCRATCH_BYTES of it until the process ends.  In host
+// code `scratch` is only a host-side stand-in for the symbol: its device
+// address comes from hipGetSymbolAddress (ensure_device, once per device) and
+// only that address is ever passed to a kernel.
+static __device__ __align__(256) uint8_t scratch[FP8LIN_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+// Checks that the current device is a gfx950 and, the first time on each
+// device, looks up that device's copy of `scratch`.  Returns the device id.
+int ensure_device() {
     int dev = 0;
     const hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) fail(FP8LIN_ERR_DEVICE, std::string("hipGetDevice: ") + hipGetErrorString(e));
@@ -65,10 +81,19 @@ void ensure_device() {
     if (g_device_state[dev] == 0) {
         hipDeviceProp_t prop;
         check_hip(hipGetDeviceProperties(&prop, dev), "hipGetDeviceProperties");
-        g_device_state[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) {
+            void* ptr = nullptr;
+            check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+            require(ptr != nullptr, FP8LIN_ERR_LAUNCH, "hipGetSymbolAddress(scratch) returned null");
+            g_scratch[dev] = ptr;
+            g_device_state[dev] = 1;
+        } else {
+            g_device_state[dev] = -1;
+        }
     }
     require(g_device_state[dev] == 1, FP8LIN_ERR_DEVICE,
             "fp8lin kernels are built for gfx950 (MI355X) only");
+    return dev;
 }
 
 hipStream_t as_stream(fp8lin_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
@@ -653,6 +678,28 @@ int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const floa
         const hipStream_t s = as_stream(stream);
         auto* logits = static_cast<uint16_t*>(workspace);
         auto* part = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + logits_bytes(M, N));
+        linear_impl(x, codes, scales, scale_cols, logits, N, M, N, K, s);
+        check_hip(fp8lin::launch_vocab_candidates(logits, (int)M, (int)N, offset, part, out, s),
+                  "vocabulary candidates launch");
+    });
+}
+
+int fp8lin_linear_candidates_static(const uint16_t* x, const uint8_t* codes, const float* scales,
+                                    int64_t scale_cols, int64_t M, int64_t N, int64_t K, int64_t offset,
+                                    double* out, fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(x && codes, FP8LIN_ERR_ARGUMENT, "FP8 linear candidates: null pointer");
+        check_dims(M, N, K);
+        check_scales(scales, scale_cols, K);
+        check_candidates(M, N, offset, out);
+        require(linear_candidates_ws(M, N) <= (size_t)FP8LIN_STATIC_SCRATCH_BYTES, FP8LIN_ERR_UNSUPPORTED,
+                "static linear candidates: the logits and candidate pairs of M x N exceed the "
+                "FP8LIN_STATIC_SCRATCH_BYTES scratch; use fp8lin_linear_candidates with a workspace");
+        const int dev = ensure_device();
+        const hipStream_t s = as_stream(stream);
+        char* base = static_cast<char*>(g_scratch[dev]);
+        auto* logits = reinterpret_cast<uint16_t*>(base);
+        auto* part = reinterpret_cast<uint32_t*>(base + logits_bytes(M, N));
         linear_impl(x, codes, scales, scale_cols, logits, N, M, N, K, s);
         check_hip(fp8lin::launch_vocab_candidates(logits, (int)M, (int)N, offset, part, out, s),
                   "vocabulary candidates launch");

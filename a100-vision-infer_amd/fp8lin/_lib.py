@@ -41,6 +41,7 @@ EXPORTED = [
     "fp8lin_rope",
     "fp8lin_qk_norm_rope",
     "fp8lin_add_bias",
+    "fp8lin_linear_candidates_static",
 ]
 
 
@@ -125,6 +126,7 @@ def lib():
         "fp8lin_merge_candidates": (i32, [vp, i64, i64, vp, vp]),
         "fp8lin_linear_candidates_workspace_bytes": (sz, [i64, i64, i64]),
         "fp8lin_linear_candidates": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, sz, vp]),
+        "fp8lin_linear_candidates_static": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, vp, vp]),
         "fp8lin_engine_linear_candidates_workspace_bytes": (sz, [ctypes.POINTER(LinearOptions),
                                                                  ctypes.POINTER(Weight), i64]),
         "fp8lin_engine_linear_candidates": (i32, [ctypes.POINTER(LinearOptions), ctypes.POINTER(Weight), vp,

@@ -339,6 +339,25 @@ int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const floa
                              double* out, void* workspace, size_t workspace_bytes,
                              fp8lin_stream_t stream);
 
+/* Allocation-free form of fp8lin_linear_candidates.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory or call
+ * hipMalloc (code under HIP graph capture such as the MTP draft step, tight
+ * serving loops).  Same arguments, checks and result (bit for bit) as
+ * fp8lin_linear_candidates, without the workspace: the logits and candidate
+ * pairs go to a static device scratch of FP8LIN_STATIC_SCRATCH_BYTES that
+ * each GPU holds from the library's first use on it until the process ends.
+ * Requires fp8lin_linear_candidates_workspace_bytes(M, N, K) <= that size
+ * (4 MiB: about 2.09 million logits, e.g. M x N up to 8 x 261632 or
+ * 1 x 2093056), else FP8LIN_ERR_UNSUPPORTED.  Every call on one GPU shares that GPU's scratch:
+ * calls that may overlap on one GPU (other streams, other threads) race, so
+ * a caller serialises them.  The call allocates nothing and needs no cleared
+ * memory (every scratch byte it reads is written first in the same call).
+ */
+#define FP8LIN_STATIC_SCRATCH_BYTES (4u << 20)
+int fp8lin_linear_candidates_static(const uint16_t* x, const uint8_t* codes, const float* scales,
+                                    int64_t scale_cols, int64_t M, int64_t N, int64_t K, int64_t offset,
+                                    double* out, fp8lin_stream_t stream);
+
 /* The head projection through Engine::linear's dispatch, then its candidates:
  * Engine::local_candidates with gpu_candidates (src/speculative.cpp:25-27).
  * out equals fp8lin_vocab_candidates of fp8lin_engine_linear's output for

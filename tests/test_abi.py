@@ -157,6 +157,25 @@ def test_linear_candidates_validation(fp8lin):
     assert L.fp8lin_linear_candidates(P, P, P, 1, 0, 1000, 256, 0, P, P, ws, None) == 1
 
 
+def test_linear_candidates_static_validation(fp8lin):
+    """The allocation-free head + candidates: the checks of
+    fp8lin_linear_candidates, and sizes beyond the static scratch
+    (FP8LIN_STATIC_SCRATCH_BYTES = 4 MiB of logits and pairs) refused before
+    any device work."""
+    L = fp8lin.lib()
+    assert L.fp8lin_linear_candidates_static(None, P, P, 1, 2, 1000, 256, 0, P, None) == 2
+    assert L.fp8lin_linear_candidates_static(P, P, P, 3, 2, 1000, 256, 0, P, None) == 2
+    assert L.fp8lin_linear_candidates_static(P, P, P, 1, 2, 1000, 256, -5, P, None) == 1
+    assert L.fp8lin_linear_candidates_static(P, P, P, 1, 2, 1000, 256, 0, None, None) == 2
+    assert L.fp8lin_linear_candidates_static(P, P, P, 1, 0, 1000, 256, 0, P, None) == 1
+    limit = 4 << 20
+    assert L.fp8lin_linear_candidates_workspace_bytes(8, 261632, 256) == limit
+    assert L.fp8lin_linear_candidates_workspace_bytes(8, 261633, 256) > limit
+    assert L.fp8lin_linear_candidates_static(P, P, P, 1, 8, 261633, 256, 0, P, None) == fp8lin.ERR_UNSUPPORTED
+    assert L.fp8lin_linear_candidates_static(P, P, P, 1, 1, 2093057, 256, 0, P, None) == fp8lin.ERR_UNSUPPORTED
+    assert b"FP8LIN_STATIC_SCRATCH_BYTES" in L.fp8lin_last_error()
+
+
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error path")
 def test_no_device_is_reported(fp8lin):
     L = fp8lin.lib()
