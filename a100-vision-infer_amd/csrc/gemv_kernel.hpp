@@ -8,18 +8,16 @@
 // BF16 (v_cvt_pk_bf16_f32) and accumulated with v_dot2_f32_bf16.  A lane sums
 // its chunks in step order; the 64 lane sums are then combined by a butterfly.
 //
-// Three kernels share that per-row order, so for one (K, W) they give the same
+// Two kernels share that per-row order, so for one (K, W) they give the same
 // bits whatever the load width, the weight type or the work distribution:
 //  - gemv_kernel: W waves per workgroup split a row's steps (j = w, w+W, ...),
 //    their sums are added in LDS in wave order; pointer loads, with a byte-load
 //    variant for unaligned data or K % 16 != 0;
 //  - gemv_ring_kernel: one wave owns R rows, the step loop is unrolled so every
-//    load of the row group is issued up front (W = 1 order);
-//  - gemv_persist_kernel: each wave streams a list of row groups through a
-//    register ring that crosses row boundaries (W = 1 order).
-// The last two use raw buffer loads: a masked lane gets an out-of-range offset
-// and reads zeros, so there is no branch around any load and the hardware
-// wait counters let the loads run ahead of the arithmetic.
+//    load of the row group is issued up front (W = 1 order).  It uses raw
+//    buffer loads: a masked lane gets an out-of-range offset and reads zeros,
+//    so there is no branch around any load and the hardware wait counters let
+//    the loads run ahead of the arithmetic.
 #pragma once
 #include "device.hpp"
 
@@ -406,119 +404,6 @@ hipError_t launch_ring(const uint16_t* x, const void* w, const float* scales, in
     const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
     hipLaunchKernelGGL((gemv_ring_kernel<MR, R, MAXSTEPS, FP8, SWIGLU, AUX>), dim3((unsigned)groups),
                        dim3(64), 0, stream, x, w, scales, S, y, ldy, M, N, K);
-    return hipGetLastError();
-}
-
-// -------------------------------------------------------- persistent kernel
-// Each wave of a 4-wave workgroup walks row groups g = wave id, + total waves,
-// ... as one flat sequence of (group, step) items held in a DEPTH-deep
-// register ring, so the next group's loads are in flight while the current one
-// is reduced and stored.  The activations are staged once per workgroup in LDS
-// (MR * K * 2 bytes).
-template <int MR, int R, int DEPTH, bool FP8, bool SWIGLU, int AUX>
-__global__ __launch_bounds__(256) void gemv_persist_kernel(
-    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
-    int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K, int groups) {
-    extern __shared__ __align__(16) uint16_t xs[];  // [MR][K]
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int chunks = K >> 4;
-    const int steps = (chunks + kWave - 1) / kWave;
-    const Buffers b = make_buffers(x, w, scales, S, M, N, K, FP8);
-
-    for (int m = 0; m < MR; ++m) {
-        const int mm = m < M ? m : M - 1;
-        for (int c = threadIdx.x; c < chunks * 2; c += 256)
-            *reinterpret_cast<u32x4*>(xs + m * K + c * 8) = buf_load16<0>(b.x, (uint32_t)((mm * K + c * 8) * 2));
-    }
-    __syncthreads();
-
-    const int total_waves = gridDim.x * 4;
-    const int gw = blockIdx.x * 4 + wave;
-    const int my_groups = gw < groups ? (groups - 1 - gw) / total_waves + 1 : 0;
-    const int items = my_groups * steps;
-    const int padded = (items + DEPTH - 1) / DEPTH * DEPTH;
-
-    auto issue = [&](Chunk<FP8> (&dst)[R], int item) {
-        const bool live = item < items;
-        const int it = live ? item : 0;
-        const int64_t g = gw + (int64_t)(it / steps) * total_waves;
-        const int c = lane + (it % steps) * kWave;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            bool ok;
-            const int64_t row = slot_row<R, SWIGLU>(g, r, N, ok);
-            load_chunk_buf<FP8, AUX>(dst[r], b, S, row, K, c << 4, live && ok && c < chunks);
-        }
-    };
-
-    Chunk<FP8> ring[DEPTH][R];
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) issue(ring[d], d);
-
-    float acc[R][MR];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
-
-    for (int t0 = 0; t0 < padded; t0 += DEPTH) {
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            const int t = t0 + d;
-            const int j = t % steps;
-            const int c = lane + j * kWave;
-            const bool cv = c < chunks;
-            const int cc = cv ? c : 0;
-            uint32_t xv[MR][8];
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const u32x4 a = *reinterpret_cast<const u32x4*>(xs + m * K + cc * 16);
-                const u32x4 e = *reinterpret_cast<const u32x4*>(xs + m * K + cc * 16 + 8);
-                xv[m][0] = cv ? a.x : 0u; xv[m][1] = cv ? a.y : 0u;
-                xv[m][2] = cv ? a.z : 0u; xv[m][3] = cv ? a.w : 0u;
-                xv[m][4] = cv ? e.x : 0u; xv[m][5] = cv ? e.y : 0u;
-                xv[m][6] = cv ? e.z : 0u; xv[m][7] = cv ? e.w : 0u;
-            }
-            accumulate<R, MR, FP8>(acc, ring[d], xv);
-            issue(ring[d], t + DEPTH);
-            if (j == steps - 1 && t < items) {
-                const int64_t g = gw + (int64_t)(t / steps) * total_waves;
-                int64_t rows[R];
-                bool ok[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) rows[r] = slot_row<R, SWIGLU>(g, r, N, ok[r]);
-                float tot[R][MR];
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-#pragma unroll
-                    for (int m = 0; m < MR; ++m) {
-                        tot[r][m] = wave_sum(acc[r][m]);
-                        acc[r][m] = 0.0f;
-                    }
-                if (lane == 0) store_group<R, MR, SWIGLU>(y, ldy, M, rows, ok, tot);
-            }
-        }
-    }
-}
-
-// Waves for the persistent kernel: split the row groups evenly with at most
-// `max_waves` resident waves.
-inline int persist_waves(int64_t groups, int max_waves) {
-    const int64_t per = (groups + max_waves - 1) / max_waves;
-    const int64_t waves = (groups + per - 1) / per;
-    return (int)((waves + 3) / 4 * 4);
-}
-
-template <int MR, int R, int DEPTH, bool FP8, bool SWIGLU, int AUX>
-hipError_t launch_persist(const uint16_t* x, const void* w, const float* scales, int S,
-                          uint16_t* y, int64_t ldy, int M, int N, int K, int max_waves,
-                          hipStream_t stream) {
-    const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
-    const int waves = persist_waves(groups, max_waves);
-    const size_t lds = (size_t)MR * K * 2;
-    hipLaunchKernelGGL((gemv_persist_kernel<MR, R, DEPTH, FP8, SWIGLU, AUX>), dim3(waves / 4),
-                       dim3(256), lds, stream, x, w, scales, S, y, ldy, M, N, K, (int)groups);
     return hipGetLastError();
 }
 

@@ -147,6 +147,11 @@ def test_normal_statistics(oracle):
     # Tail mass against the normal distribution (2 and 3 sigma).
     assert abs((np.abs(z) > 2).mean() - 0.0455) < 2e-3
     assert abs((np.abs(z) > 3).mean() - 0.0027) < 5e-4
+    # Kolmogorov-Smirnov distance to the standard normal CDF on the first
+    # 2^16 draws: for n = 65536 the 1% critical value is 1.63 / sqrt(n).
+    from scipy import stats
+    d = stats.kstest(z[:1 << 16], "norm").statistic
+    assert d < 1.63 / np.sqrt(1 << 16), d
     # Different tags and seeds give different streams.
     assert not np.array_equal(z[:64], oracle.normal(0, 2, 0, 64))
     assert not np.array_equal(z[:64], oracle.normal(1, 1, 0, 64))
@@ -233,6 +238,38 @@ def test_swiglu_fixture_and_special_values(oracle):
     a = np.array([[0.0, -0.0, 20.0, -20.0, 1.0, 1.0, 1.0, 1.0]], np.float32)
     y = bf16_to_f32(oracle.swiglu(torch_bf16_bits(a)))
     assert y[0, 0] == 0 and y[0, 1] == 0 and y[0, 2] == 20.0 and abs(y[0, 3]) < 1e-6
+
+
+def bf16_rne_f64(v):
+    """FP64 values rounded once to BF16 (normal range), as bit patterns."""
+    m, e = np.frexp(v)
+    r = np.ldexp(np.rint(m * 256.0), e - 8)  # 8 significant bits, ties to even
+    return (r.astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_swiglu_against_fp64_exp(oracle):
+    """Every normal BF16 gate value a >= -88 with u = 1 (so y = g): the oracle's
+    g = bf16(a / (1 + expf(-a))) (src/optimized.cu:73, FP32 expf) against the
+    same quotient in FP64 rounded once to BF16.  An FP32 expf and division
+    move the quotient by a few FP32 ulp, so the two agree except where the
+    FP64 value lies next to a BF16 rounding midpoint, and never by more than
+    one ulp.  (Below a = -88.7 expf(-a) overflows and the reference's FP32
+    formula returns -0.)  A sign error in the exponent, a dropped "1 +" or
+    sigmoid(a) in place of a * sigmoid(a) fail this."""
+    a = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    g = np.concatenate([a, np.full(65536, 0x3F80, np.uint16)])[None, :]
+    y = oracle.swiglu(g)[0]
+    af = bf16_to_f32(a).astype(np.float64)
+    keep = np.isfinite(af) & (af >= -88.0) & (np.abs(af) >= 2.0 ** -125)  # g = a/2 stays normal
+    af, y = af[keep], y[keep]
+    exact = af / (1.0 + np.exp(-af))
+    d = ulp_distance(y, bf16_rne_f64(exact))
+    assert d.max() <= 1
+    assert (d == 0).mean() > 0.999
+    # where they differ, the FP64 value is within 2^-8 BF16 ulp of a midpoint
+    m, _ = np.frexp(exact[d == 1])
+    frac = np.abs(m) * 256.0 - np.floor(np.abs(m) * 256.0)
+    assert np.all(np.abs(frac - 0.5) < 2.0 ** -8), frac
 
 
 # ------------------------------------- decode epilogue and output head (f)
