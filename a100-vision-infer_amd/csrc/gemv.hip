@@ -17,8 +17,10 @@
 // (tests/optimized_test.cpp:11-12, :57-62).
 //
 // Kernel choice for the 128-bit FP8 path (measured on MI355X, decode shapes):
-// the unrolled ring kernel with the row group's loads all in flight --
-// R = 1 rows for K <= 4096, R = 2 for K <= 5120 and for K <= 9216.
+// the unrolled ring kernel with the row group's loads all in flight, four
+// waves per workgroup -- R = 1 rows for K <= 4096, R = 2 for K <= 5120,
+// R = 1 for K <= 9216 (R = 2 for the SwiGLU form, whose rows come in
+// gate/up pairs).
 #include "gemv_kernel.hpp"
 #include "internal.hpp"
 
@@ -39,7 +41,10 @@ hipError_t ring_fp8(const uint16_t* x, const uint8_t* w, const float* scales, in
             return launch_ring<MR, 1, 4, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
     }
     if (K <= 5120) return launch_ring<MR, 2, 5, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
-    return launch_ring<MR, 2, 9, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
+    if constexpr (SWIGLU)
+        return launch_ring<MR, 2, 9, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
+    else
+        return launch_ring<MR, 1, 9, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
 }
 
 // General kernel with the same W as the ring path for this K.
