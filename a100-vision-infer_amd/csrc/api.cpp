@@ -201,22 +201,19 @@ bool tensor_small_eligible(const fp8lin_linear_options& o, const fp8lin_weight& 
            w.K % 128 == 0 && w.scale_cols == w.K / 128 && (!o.tilelang_fp8 || w.N % 16 == 0);
 }
 
-// Split-K partials of the FP8 GEMM branch: outputs with few 256x256 tiles
-// (prefill QKV and down projections at M <= 1024) split K over more CUs.
-int engine_splits(const fp8lin_weight& w, int64_t rows, int64_t ldy) {
-    if (rows <= 8 || rows >= kMaxDim) return 1;
-    return fp8lin::gemm_splits((int)w.scale_cols, ldy, (int)rows, (int)w.N, (int)w.K, false);
-}
-size_t split_ws(const fp8lin_weight& w, int64_t rows, int splits) {
-    return splits > 1 ? (size_t)splits * (size_t)rows * (size_t)w.N * 4 : 0;
+// K-split partials of the FP8 GEMM branch (rows > 8): outputs whose tile
+// count leaves CUs idle (few tiles, or a small last round) split K.
+size_t engine_gemm_ws(const fp8lin_weight& w, int64_t rows, int64_t ldy) {
+    if (rows <= 8 || rows >= kMaxDim) return 0;
+    return fp8lin::gemm_workspace_bytes((int)w.scale_cols, ldy, (int)rows, (int)w.N, (int)w.K, false);
 }
 
 size_t engine_ws(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t rows) {
     if (tensor_small_eligible(o, w, rows)) return tensor_small_ws(rows, w.N, o.fp8_tensor_split);
     if (o.multi_token_gemv && rows > 1 && rows <= 8) return 0;
     if (w.cached_bf16 && rows > 1) return 0;
-    // (the split count for ldy = N: a wider ldy never adds splits)
-    if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) return split_ws(w, rows, engine_splits(w, rows, w.N));
+    // (the plan for ldy = N: a wider ldy never needs more)
+    if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) return engine_gemm_ws(w, rows, w.N);
     if (w.scales) return dequant_gemm_ws(w.N, w.K);
     return 0;
 }
@@ -282,14 +279,13 @@ int engine_branch(const fp8lin_linear_options& o, const fp8lin_weight& w, const 
     }
     // :222-224
     if (w.scales && o.optimized && !(o.cublas_prefill && rows > 8)) {
-        const int splits = engine_splits(w, rows, ldy);
-        if (splits > 1) {
-            const size_t need = split_ws(w, rows, splits);
-            require(ws != nullptr && ws_bytes >= need && aligned16(ws), FP8LIN_ERR_WORKSPACE,
-                    "split-K partial workspace missing, too small or unaligned");
-            check_hip(fp8lin::launch_gemm_split(x, codes, w.scales, (int)w.scale_cols, y, ldy, (int)rows,
-                                                (int)w.N, (int)w.K, false, static_cast<float*>(ws), splits, stream),
-                      "fp8 split-K gemm launch");
+        if (rows > 8) {
+            const size_t need = engine_gemm_ws(w, rows, ldy);
+            require(need == 0 || (ws != nullptr && ws_bytes >= need && aligned16(ws)), FP8LIN_ERR_WORKSPACE,
+                    "FP8 GEMM split-K partial workspace missing, too small or unaligned");
+            check_hip(fp8lin::launch_gemm_ws(x, codes, w.scales, (int)w.scale_cols, y, ldy, (int)rows, (int)w.N,
+                                             (int)w.K, false, need ? ws : nullptr, need, stream),
+                      "fp8 gemm launch");
         } else {
             linear_impl(x, codes, w.scales, w.scale_cols, y, ldy, rows, w.N, w.K, stream);
         }
@@ -449,6 +445,35 @@ int fp8lin_add_bias(uint16_t* y, int64_t ldy, const uint16_t* bias, int64_t rows
         require(ldy >= N, FP8LIN_ERR_SHAPE, "Bias add: ldy < N");
         ensure_device();
         check_hip(fp8lin::launch_bias(y, ldy, bias, rows, N, as_stream(stream)), "bias launch");
+    });
+}
+
+size_t fp8lin_linear_swiglu_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 8 || N <= 0 || K <= 0 || N % 2 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
+    return fp8lin::gemm_workspace_bytes((int)ceil_div(K, 128), N / 2, (int)M, (int)N, (int)K, true);
+}
+
+int fp8lin_linear_swiglu_ws(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t scale_cols,
+                            uint16_t* y, int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                            fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(x && codes && y, FP8LIN_ERR_ARGUMENT, "FP8 linear+SwiGLU: null pointer");
+        check_dims(M, N, K);
+        require(N % 2 == 0, FP8LIN_ERR_SHAPE, "Invalid SwiGLU input: N must be even");
+        check_scales(scales, scale_cols, K);
+        const size_t need = fp8lin_linear_swiglu_workspace_bytes(M, N, K);
+        check_workspace(workspace, workspace_bytes, need, "linear+SwiGLU: workspace too small");
+        ensure_device();
+        if (M <= 8) {
+            const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
+            check_hip(fp8lin::launch_gemv_swiglu(x, codes, scales, (int)scale_cols, y, N / 2, (int)M, (int)N, (int)K,
+                                                 wide, as_stream(stream)),
+                      "fp8 gemv+swiglu launch");
+        } else {
+            check_hip(fp8lin::launch_gemm_ws(x, codes, scales, (int)scale_cols, y, N / 2, (int)M, (int)N, (int)K,
+                                             true, need ? workspace : nullptr, need, as_stream(stream)),
+                      "fp8 gemm+swiglu launch");
+        }
     });
 }
 

@@ -109,28 +109,64 @@ namespace fp8lin {
 //
 // g is computed first with the hardware exp2 and reciprocal
 // (exp(-a) = 2^(-a*log2(e)), then a * rcp(1 + e)).  For a >= -64 that value
-// is within about 64 FP32 ulp of the accurate one: the argument's rounding
-// (2^-18 absolute below 128, plus the constant's 2^-25 relative error) moves
-// e by under 4e-6 relative, and exp2, the add, rcp and the product add about
-// one ulp each.  Its BF16 rounding can differ from the accurate quotient's
-// only if its low 16 bits lie within 256 of the rounding midpoint 0x8000;
-// those values (under 1% of them), and a < -64 (where 1 / (1 + e) is an FP32
-// denormal that the reciprocal flushes to zero), take the accurate expf and
-// division.  g depends on a alone, a is BF16, so a check over all 65 536
-// gate values covers every input.
+// is within 53 FP32 ulp of the accurate one (the argument's rounding, up to
+// 2^-18 absolute below 128, dominates).  g depends on a alone and a is BF16,
+// so the 65 536 inputs can be enumerated: for every a >= -64 the BF16
+// rounding of the fast value differs from the accurate quotient's only where
+// the fast value's low 16 bits lie within 4 of the rounding midpoint 0x8000.
+// Values within 8 of it (about 0.02% of typical gates, so under 2% of
+// 64-lane groups need the slow path at all), and a < -64 (where
+// 1 / (1 + e) is an FP32 denormal that the reciprocal flushes to zero), take
+// the accurate expf and division.  The tests check all 65 536 gate values.
 __device__ __forceinline__ float swiglu_gate_exact(float a) {
     return a / (1.0f + expf(-a));
 }
 
-__device__ __forceinline__ uint16_t swiglu_bf16_bits(uint16_t a_bits, uint16_t u_bits) {
-    const float a = bf16_bits_to_f32(a_bits);
-    const float u = bf16_bits_to_f32(u_bits);
+// The fast quotient, and whether this input must take the accurate path.
+__device__ __forceinline__ float swiglu_gate_fast(float a, bool& need) {
     const float e = __builtin_amdgcn_exp2f(a * -1.44269504088896340736f);
-    float gf = a * __builtin_amdgcn_rcpf(1.0f + e);
+    const float gf = a * __builtin_amdgcn_rcpf(1.0f + e);
     const uint32_t low = __builtin_bit_cast(uint32_t, gf) & 0xffffu;
-    if (!(a >= -64.0f) || (low > 0x8000u - 256u && low < 0x8000u + 256u)) gf = swiglu_gate_exact(a);
+    need = !(a >= -64.0f) || (low > 0x8000u - 8u && low < 0x8000u + 8u);
+    return gf;
+}
+
+// y = bf16(bf16(g) * u) from the FP32 gate quotient.
+__device__ __forceinline__ uint16_t swiglu_finish(float gf, float u) {
     const float g = bf16_bits_to_f32(f32_to_bf16_bits(gf));
     return f32_to_bf16_bits(g * u);
+}
+
+__device__ __forceinline__ uint16_t swiglu_bf16_bits(uint16_t a_bits, uint16_t u_bits) {
+    const float a = bf16_bits_to_f32(a_bits);
+    bool need;
+    float gf = swiglu_gate_fast(a, need);
+    if (need) gf = swiglu_gate_exact(a);
+    return swiglu_finish(gf, bf16_bits_to_f32(u_bits));
+}
+
+// NB SwiGLU outputs at once, each from a packed (gate | up << 16) BF16 pair:
+// the same arithmetic as swiglu_bf16_bits, laid out for a wave that runs
+// alone on its SIMD (a GEMM epilogue).  The NB fast quotients are
+// independent, so their instructions interleave instead of waiting on each
+// other's latency, and the rare accurate path is one branch per batch.
+template <int NB>
+__device__ __forceinline__ void swiglu_bf16_batch(const uint32_t (&gu)[NB], uint16_t (&out)[NB]) {
+    float gf[NB];
+    uint32_t need = 0;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+        bool n;
+        gf[k] = swiglu_gate_fast(bf16_bits_to_f32(gu[k] & 0xffffu), n);
+        need |= (uint32_t)n << k;
+    }
+    if (need) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k)
+            if ((need >> k) & 1u) gf[k] = swiglu_gate_exact(bf16_bits_to_f32(gu[k] & 0xffffu));
+    }
+#pragma unroll
+    for (int k = 0; k < NB; ++k) out[k] = swiglu_finish(gf[k], bf16_bits_to_f32(gu[k] >> 16));
 }
 
 }  // namespace fp8lin

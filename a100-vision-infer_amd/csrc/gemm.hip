@@ -9,6 +9,7 @@
 // the next stage's FP8 dequantization and LDS store placed after the second
 // MFMA group, and the scheduler's MFMA/LDS interleave strategy 1.
 #include <algorithm>
+#include <atomic>
 
 #include "gemm_fp8.hpp"
 #include "gemm_kernel.hpp"
@@ -18,10 +19,6 @@ namespace fp8lin {
 namespace {
 
 using Tile = gemm::Cfg<256, 256, 64, 2, 4>;
-// Split-K: used when the output has at most half as many 256x256 tiles as
-// there are CUs; the splits fill up to kSplitCus workgroups.
-constexpr int kSplitCus = 256;
-constexpr int kMaxSplits = 8;
 constexpr int kGroupM = 8;   // XCD-local tile patch height
 constexpr int kIglp = 1;     // MFMA / LDS interleave strategy
 constexpr int kPrefetch = 2; // global loads two K steps ahead
@@ -34,104 +31,123 @@ hipError_t run(const uint16_t* x, const void* w, const float* scales, int S, uin
                                                                              M, N, K, stream);
 }
 
-}  // namespace
-
-// Split-K reduction: out[m][c] = bf16(sum over s in order of part[s][m][c])
-// for c < N, or with SWIGLU y[m][j] = swiglu(bf16(gate sum), bf16(up sum))
-// from weight-row columns j and N/2 + j -- the rounding points of the
-// unsplit epilogue.  Four columns per thread when the row widths allow it.
-template <bool SWIGLU, bool VEC>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int splits, int M, int N,
-                                                            uint16_t* __restrict__ y, int64_t ldy) {
-    const int cols = SWIGLU ? N / 2 : N;
-    const int per_row = VEC ? cols / 4 : cols;
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (int64_t)M * per_row) return;
-    const int m = (int)(idx / per_row), c = (int)(idx % per_row) * (VEC ? 4 : 1);
-    const int64_t slice = (int64_t)M * N;
-    const float* p = part + (int64_t)m * N + c;
-    auto sum = [&](int off) __attribute__((always_inline)) -> f32x4 {
-        f32x4 t;
-        if constexpr (VEC) {
-            t = *reinterpret_cast<const f32x4*>(p + off);
-            for (int s = 1; s < splits; ++s) t += *reinterpret_cast<const f32x4*>(p + s * slice + off);
-        } else {
-            t = f32x4{p[off], 0.0f, 0.0f, 0.0f};
-            for (int s = 1; s < splits; ++s) t[0] += p[s * slice + off];
-        }
-        return t;
-    };
-    uint16_t out[4];
-    const f32x4 a = sum(0);
-    if constexpr (SWIGLU) {
-        const f32x4 u = sum(N / 2);
-#pragma unroll
-        for (int q = 0; q < (VEC ? 4 : 1); ++q)
-            out[q] = swiglu_bf16_bits(f32_to_bf16_bits(a[q]), f32_to_bf16_bits(u[q]));
-    } else {
-#pragma unroll
-        for (int q = 0; q < (VEC ? 4 : 1); ++q) out[q] = f32_to_bf16_bits(a[q]);
+// Compute units of the current device (cached per device), rounded down to a
+// multiple of the 8 XCDs: the persistent FP8 grid size.
+int grid_cus() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) cus = 256;
+        v = cus / gemm_fp8::kXcds * gemm_fp8::kXcds;
+        cached[dev].store(v, std::memory_order_relaxed);
     }
-    uint16_t* dst = y + (int64_t)m * ldy + c;
-#pragma unroll
-    for (int q = 0; q < (VEC ? 4 : 1); ++q) dst[q] = out[q];
+    return v;
 }
 
-template <bool SWIGLU, bool PARTIAL>
-hipError_t run_fp8(const uint16_t* x, const uint8_t* w, const float* scales, int S, uint16_t* y,
-                   int64_t ldy, int M, int N, int K, float* part, int splits, hipStream_t stream) {
+// Work plan of the persistent FP8 GEMM (see gemm_fp8.hpp).  Without a
+// workspace every tile is computed whole.  With one, K is split where the
+// tile count leaves CUs idle:
+//  - fewer tiles than half the CUs (e.g. the prefill QKV-gate and down
+//    projections at M = 512): every tile, into min(G / T, K / 256, 8)
+//    ranges;
+//  - otherwise a last round of at most a quarter of the CUs (M = 1024: 16 of
+//    272 tiles; M = 4096: 64 of 1088): those tiles, into min(G / R, K / 256, 8)
+//    ranges, so the last round covers at least half the CUs.
+gemm_fp8::Plan make_plan(int M, int N, int K, bool swiglu, int G, bool split) {
     using namespace gemm_fp8;
-    const int mtiles = (M + BM - 1) / BM;
-    const int ntiles = SWIGLU ? ((N >> 1) + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
-    const int per_xcd = (mtiles * ntiles + kXcds - 1) / kXcds;
-    auto kern = gemm_fp8_kernel<SWIGLU, PARTIAL>;
+    Plan p;
+    p.mtiles = (M + BM - 1) / BM;
+    p.ntiles = swiglu ? ((N >> 1) + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
+    const int T = p.mtiles * p.ntiles;
+    p.full = T;
+    p.rtiles = 0;
+    p.splits = 1;
+    if (split) {
+        const int chunks = K / 256;
+        if (2 * T <= G) {
+            const int s = std::min(std::min(G / T, chunks), kMaxSplits);
+            if (s > 1) {
+                p.full = 0;
+                p.rtiles = T;
+                p.splits = s;
+            }
+        } else if (T > G && T % G != 0 && 4 * (T % G) <= G) {
+            const int R = T % G;
+            const int s = std::min(std::min(G / R, chunks), kMaxSplits);
+            if (s > 1) {
+                p.full = T - R;
+                p.rtiles = R;
+                p.splits = s;
+            }
+        }
+    }
+    p.fpad = (p.full + kXcds - 1) / kXcds * kXcds;
+    p.units = p.fpad + p.rtiles * p.splits;
+    return p;
+}
+
+size_t plan_bytes(const gemm_fp8::Plan& p) {
+    return (size_t)p.rtiles * p.splits * gemm_fp8::kSlotFloats * sizeof(float);
+}
+
+template <bool SWIGLU>
+hipError_t run_fp8(const uint16_t* x, const uint8_t* w, const float* scales, int S, uint16_t* y, int64_t ldy,
+                   int M, int N, int K, const gemm_fp8::Plan& plan, int G, float* part, hipStream_t stream) {
+    using namespace gemm_fp8;
+    auto kern = gemm_fp8_kernel<SWIGLU>;
     static const hipError_t attr = gemm::allow_lds(reinterpret_cast<const void*>(kern), LDS_BYTES);
     if (attr != hipSuccess) return attr;
-    uint16_t* out = PARTIAL ? reinterpret_cast<uint16_t*>(part) : y;
-    hipLaunchKernelGGL(kern, dim3(per_xcd * kXcds, PARTIAL ? splits : 1), dim3(THREADS), LDS_BYTES, stream, x, w,
-                       scales, S, out, (int)ldy, M, N, K, mtiles, ntiles, splits);
+    const int grid = std::min(plan.units, G);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), LDS_BYTES, stream, x, w, scales, S, y, (int)ldy, M, N, K,
+                       plan, part);
     hipError_t e = hipGetLastError();
-    if (!PARTIAL || e != hipSuccess) return e;
-    const int cols = SWIGLU ? N / 2 : N;
-    const bool vec = cols % 4 == 0 && (!SWIGLU || (N / 2) % 4 == 0) && N % 4 == 0;
-    const int64_t threads = (int64_t)M * (vec ? cols / 4 : cols);
-    const dim3 grid((unsigned)((threads + 255) / 256));
-    if (vec)
-        hipLaunchKernelGGL((splitk_reduce_kernel<SWIGLU, true>), grid, dim3(256), 0, stream, part, splits, M, N, y, ldy);
-    else
-        hipLaunchKernelGGL((splitk_reduce_kernel<SWIGLU, false>), grid, dim3(256), 0, stream, part, splits, M, N, y,
-                           ldy);
+    if (e != hipSuccess || plan.rtiles == 0) return e;
+    const int64_t threads = (int64_t)plan.rtiles * BM * (SWIGLU ? 32 : 64);
+    hipLaunchKernelGGL(tail_reduce_kernel<SWIGLU>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                       part, plan, M, N, y, ldy);
     return hipGetLastError();
 }
 
-int gemm_splits(int S, int64_t ldy, int M, int N, int K, bool swiglu) {
-    using namespace gemm_fp8;
-    // the FP8 kernel's shape requirements (pointer alignment is the caller's)
-    if (!supported(nullptr, nullptr, S, ldy, M, N, K) || ((int64_t)M + BM) * N * 4 >= ((int64_t)1 << 31)) return 1;
-    const int64_t tiles = (int64_t)((M + BM - 1) / BM) * (swiglu ? ((N >> 1) + BN / 2 - 1) / (BN / 2)
-                                                                  : (N + BN - 1) / BN);
-    if (tiles * 2 > kSplitCus) return 1;
-    const int chunks = K / 256;
-    return std::min<int64_t>(std::min<int64_t>(kSplitCus / tiles, chunks), kMaxSplits);
+// Shapes and alignments the FP8 kernel takes.
+bool fp8_kernel_ok(const uint16_t* x, const void* w, int S, int64_t ldy, int M, int N, int K) {
+    return gemm_fp8::supported(x, w, S, ldy, M, N, K);
 }
 
-hipError_t launch_gemm_split(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
-                             int64_t ldy, int M, int N, int K, bool swiglu, float* part, int splits,
-                             hipStream_t stream) {
-    const uint8_t* codes = static_cast<const uint8_t*>(w);
-    if (splits <= 1 || !gemm_fp8::supported(x, w, S, ldy, M, N, K))
-        return launch_gemm(x, w, scales, S, y, ldy, M, N, K, swiglu, stream);
-    return swiglu ? run_fp8<true, true>(x, codes, scales, S, y, ldy, M, N, K, part, splits, stream)
-                  : run_fp8<false, true>(x, codes, scales, S, y, ldy, M, N, K, part, splits, stream);
+}  // namespace
+
+size_t gemm_workspace_bytes(int S, int64_t ldy, int M, int N, int K, bool swiglu) {
+    if (!fp8_kernel_ok(nullptr, nullptr, S, ldy, M, N, K)) return 0;
+    return plan_bytes(make_plan(M, N, K, swiglu, grid_cus(), true));
+}
+
+hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
+                          int M, int N, int K, bool swiglu, void* ws, size_t ws_bytes, hipStream_t stream) {
+    const bool fp8 = scales != nullptr;
+    if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
+        const uint8_t* codes = static_cast<const uint8_t*>(w);
+        const int G = grid_cus();
+        gemm_fp8::Plan plan = make_plan(M, N, K, swiglu, G, ws != nullptr);
+        if (plan_bytes(plan) > ws_bytes || reinterpret_cast<uintptr_t>(ws) % 16 != 0)
+            plan = make_plan(M, N, K, swiglu, G, false);
+        float* part = static_cast<float*>(ws);
+        return swiglu ? run_fp8<true>(x, codes, scales, S, y, ldy, M, N, K, plan, G, part, stream)
+                      : run_fp8<false>(x, codes, scales, S, y, ldy, M, N, K, plan, G, part, stream);
+    }
+    return launch_gemm(x, w, scales, S, y, ldy, M, N, K, swiglu, stream);
 }
 
 hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
                        int64_t ldy, int M, int N, int K, bool swiglu, hipStream_t stream) {
     const bool fp8 = scales != nullptr;
-    if (fp8 && gemm_fp8::supported(x, w, S, ldy, M, N, K)) {
+    if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
         const uint8_t* codes = static_cast<const uint8_t*>(w);
-        return swiglu ? run_fp8<true, false>(x, codes, scales, S, y, ldy, M, N, K, nullptr, 1, stream)
-                      : run_fp8<false, false>(x, codes, scales, S, y, ldy, M, N, K, nullptr, 1, stream);
+        const int G = grid_cus();
+        const gemm_fp8::Plan plan = make_plan(M, N, K, swiglu, G, false);
+        return swiglu ? run_fp8<true>(x, codes, scales, S, y, ldy, M, N, K, plan, G, nullptr, stream)
+                      : run_fp8<false>(x, codes, scales, S, y, ldy, M, N, K, plan, G, nullptr, stream);
     }
     if (fp8)
         return swiglu ? run<true, true>(x, w, scales, S, y, ldy, M, N, K, stream)

@@ -73,6 +73,12 @@ __device__ __forceinline__ i32x4 make_desc(const void* base, uint32_t bytes) {
 __device__ __forceinline__ void mfma(f32x16& acc, const u32x4& a, const u32x4& b) {
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
+// acc = 0 written straight into the accumulator registers (an MFMA of zero
+// operands with a zero addend), so cleared accumulators never pass through
+// VGPRs.
+__device__ __forceinline__ void mfma_zero(f32x16& acc, const u32x4& zero) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %1, 0" : "=a"(acc) : "v"(zero));
+}
 template <int OFF>
 __device__ __forceinline__ void ds_read(u32x4& d, uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(addr), "i"(OFF));
@@ -257,17 +263,36 @@ __device__ __forceinline__ void kstep(State& st, const Ctx& c, const Ring& rg, i
     }(std::make_integer_sequence<int, 4>{});
 }
 
-// Grid: one workgroup per tile, dealt round-robin over the 8 XCDs by the
-// dispatcher; tile index L = (bid % 8) * per_xcd + bid / 8 gives each XCD a
-// contiguous tile range, walked GROUP_M tile rows at a time so concurrently
-// running workgroups of one XCD share A and B slices in its L2.
+// Work decomposition.  The output is cut into 256 x 256 tiles (L = 0..T-1,
+// walked GROUP_M tile rows at a time so that tiles running together on one
+// XCD share A and B slices in its L2).  The grid is persistent: G workgroups
+// (one per CU, G a multiple of 8) loop over work units u = bid, bid + G, ...
+//  - units [0, fpad) are whole tiles, written to y.  Unit u runs on XCD
+//    u % 8 (the dispatcher deals workgroups round-robin over the XCDs), and
+//    takes tile L = (u % 8) * (fpad / 8) + u / 8, so each XCD owns a
+//    contiguous tile range (fpad = full rounded up to a multiple of 8; units
+//    whose L >= full do nothing);
+//  - units [fpad, fpad + rtiles * splits) cover the tail tiles full..T-1, each
+//    cut into `splits` K ranges (whole 256-K chunks, spread evenly).  Their
+//    FP32 sums go to partial slot r * splits + s (256 x 256 floats each, in
+//    the tile's own row/column order) and tail_reduce_kernel adds the splits
+//    in order, rounds once and applies the epilogue.
+// The host picks full = T and rtiles = 0 when splitting would not pay (see
+// gemm.hip), so most launches write every tile directly.
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
-__device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles, int& mt, int& nt) {
-    const int tiles = mtiles * ntiles;
-    const int per_xcd = (tiles + kXcds - 1) / kXcds;
-    const int L = (bid % kXcds) * per_xcd + bid / kXcds;
-    if (L >= tiles) return false;
+constexpr int kSlotFloats = BM * BN;
+constexpr int kMaxSplits = 8;
+
+struct Plan {
+    int mtiles, ntiles;  // tile grid (ntiles counts 256-row weight blocks, or 128 output pairs for SwiGLU)
+    int full;            // whole tiles
+    int fpad;            // full rounded up to a multiple of 8
+    int rtiles, splits;  // tail tiles and their K ranges
+    int units;           // fpad + rtiles * splits
+};
+
+__device__ __forceinline__ void tile_coords(int L, int mtiles, int ntiles, int& mt, int& nt) {
     const int per_group = kGroupM * ntiles;
     const int g = L / per_group;
     const int first_m = g * kGroupM;
@@ -275,7 +300,6 @@ __device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles, int& mt
     const int r = L - g * per_group;
     mt = first_m + r % gsize;
     nt = r / gsize;
-    return true;
 }
 
 // K range of split s of `splits`: whole 256-K chunks, spread evenly.
@@ -286,42 +310,55 @@ __device__ __forceinline__ void split_range(int K, int s, int splits, int& kbeg,
     klen = 256 * (c1 - c0);
 }
 
-// Requirements (checked by the launcher): K % 256 == 0; x and w 16-byte
-// aligned; S == K/128 or S == 1; M*K*2, N*K, N*S*4 and (M + 256)*ldy*2
-// below 2^31.  When SWIGLU, N is the number of weight rows (gate rows
-// [0, N/2), up rows [N/2, N)) and y is [M, N/2].
-//
-// PARTIAL (split-K): y is the FP32 partial buffer.  blockIdx.y = s takes
-// split s of `splits` K ranges and writes its sums to (float*)y + s*M*N as
-// [M, N] in weight-row columns (gate and up columns unpaired when SWIGLU);
-// splitk_reduce_kernel adds the splits in order and applies the BF16
-// rounding and the epilogue.  (M + 256)*N*4 < 2^31.
-template <bool SWIGLU, bool PARTIAL = false>
-__global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __restrict__ x,
-                                                          const uint8_t* __restrict__ w,
-                                                          const float* __restrict__ scales, int S,
-                                                          uint16_t* __restrict__ y, int ldy, int M, int N,
-                                                          int K, int mtiles, int ntiles, int splits = 1) {
-    extern __shared__ __align__(16) uint16_t smem[];
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int h = lane >> 5;
-    const int l32 = lane & 31;
-    int mtile, ntile;
-    if (!tile_of(blockIdx.x, mtiles, ntiles, mtile, ntile)) return;
-    const int m0 = mtile * BM;
-    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-    // This workgroup's K range: the buffers start at kbeg (rows keep the
-    // stride K), so the step offsets below are relative to it.
-    int kbeg = 0, klen = K;
-    if constexpr (PARTIAL) split_range(K, blockIdx.y, splits, kbeg, klen);
-    const int KT = klen / BK;
-    const int sbeg = S == 1 ? 0 : kbeg / 128;
+struct Unit {
+    int mtile, ntile, kbeg, klen;
+    int slot;  // partial slot, or -1 for a whole tile
+};
 
-    Ctx c;
-    c.dx = make_desc(x + kbeg, (uint32_t)((int64_t)M * K * 2 - (int64_t)kbeg * 2));
-    c.dw = make_desc(w + kbeg, (uint32_t)((int64_t)N * K - kbeg));
+__device__ __forceinline__ bool unit_of(int u, const Plan& p, int K, Unit& w) {
+    if (u < p.fpad) {
+        const int L = (u % kXcds) * (p.fpad / kXcds) + u / kXcds;
+        if (L >= p.full) return false;
+        tile_coords(L, p.mtiles, p.ntiles, w.mtile, w.ntile);
+        w.kbeg = 0;
+        w.klen = K;
+        w.slot = -1;
+        return true;
+    }
+    const int v = u - p.fpad;
+    const int r = v / p.splits, s = v % p.splits;
+    tile_coords(p.full + r, p.mtiles, p.ntiles, w.mtile, w.ntile);
+    split_range(K, s, p.splits, w.kbeg, w.klen);
+    w.slot = v;
+    return true;
+}
+
+// Weight row of local column rr (0..63) of wave `wave` in tile column
+// block nt, or -1 past the end.  SwiGLU tiles hold 128 gate rows and the
+// 128 matching up rows: wave w's columns 0..31 are gate rows, 32..63 up.
+template <bool SWIGLU>
+__device__ __forceinline__ int64_t weight_row(int nt, int wave, int rr, int N) {
+    if constexpr (SWIGLU) {
+        const int D = N >> 1;
+        const int o = nt * (BN / 2) + wave * (WN / 2) + (rr & 31);
+        return o < D ? (rr < 32 ? (int64_t)o : (int64_t)D + o) : -1;
+    } else {
+        const int64_t n = (int64_t)nt * BN + wave * WN + rr;
+        return n < N ? n : -1;
+    }
+}
+
+// Buffer descriptors and lane offsets of one unit (its tile and K range).
+template <bool SWIGLU>
+__device__ __forceinline__ void setup(Ctx& c, const Unit& w, const uint16_t* x, const uint8_t* wt, const float* scales,
+                                      int S, int M, int N, int K, int wave, int lane, uint32_t lds0) {
+    const int h = lane >> 5, l32 = lane & 31;
+    const int m0 = w.mtile * BM;
+    const int sbeg = S == 1 ? 0 : w.kbeg / 128;
+    // The buffers start at kbeg (rows keep the stride K), so the step offsets
+    // of the loop are relative to it.
+    c.dx = make_desc(x + w.kbeg, (uint32_t)((int64_t)M * K * 2 - (int64_t)w.kbeg * 2));
+    c.dw = make_desc(wt + w.kbeg, (uint32_t)((int64_t)N * K - w.kbeg));
     c.ds = make_desc(scales + sbeg, (uint32_t)((int64_t)N * S * 4 - (int64_t)sbeg * 4));
     c.scol = S == 1 ? 0 : 4;
     // A DMA instruction ii of wave w fills rows 8G..8G+7 (G = 8w + ii) of a
@@ -334,30 +371,19 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
         c.aoff[ii] = m < M ? (uint32_t)((int64_t)m * K * 2 + ch * 16) : kBufferOob;
     }
     c.m0a = __builtin_amdgcn_readfirstlane(lds0 + wave * 8 * 1024);
-    // This wave's 64 weight rows: local row rr -> weight row (or -1).
-    auto wrow = [&](int rr) -> int64_t {
-        if constexpr (SWIGLU) {
-            const int D = N >> 1;
-            const int o = ntile * (BN / 2) + wave * (WN / 2) + (rr & 31);
-            return o < D ? (rr < 32 ? (int64_t)o : (int64_t)D + o) : -1;
-        } else {
-            const int64_t n = (int64_t)ntile * BN + wave * WN + rr;
-            return n < N ? n : -1;
-        }
-    };
     // B DMA instruction gi fills rows 16gi..16gi+15 of a slot: lane -> row
     // 16gi + lane/4, LDS slot lane%4 <- chunk slot ^ gb(row).
 #pragma unroll
     for (int gi = 0; gi < 4; ++gi) {
         const int rr = 16 * gi + (lane >> 2);
         const int ch = (lane & 3) ^ gb(rr);
-        const int64_t n = wrow(rr);
+        const int64_t n = weight_row<SWIGLU>(w.ntile, wave, rr, N);
         c.boff[gi] = n >= 0 ? (uint32_t)(n * K + ch * 16) : kBufferOob;
     }
     c.m0b = __builtin_amdgcn_readfirstlane(lds0 + A_BYTES + wave * B_WAVE);
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-        const int64_t n = wrow(32 * j + l32);
+        const int64_t n = weight_row<SWIGLU>(w.ntile, wave, 32 * j + l32, N);
         c.soff[j] = n >= 0 ? (uint32_t)(n * S * 4) : kBufferOob;
     }
 #pragma unroll
@@ -368,17 +394,11 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
 #pragma unroll
     for (int cp = 0; cp < 2; ++cp)
         c.brd[cp] = lds0 + A_BYTES + wave * B_WAVE + l32 * 64 + 16 * ((2 * cp + h) ^ gb(l32));
+}
 
-    State st;
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) st.acc[i][j][r] = 0.0f;
-
-    // ---- prologue: A(0), A(1) into stages 0, 1; B(0..2) into slots 0..2;
-    // scale blocks 0, 1; B(0) dequantized; step 0's first fragments read.
+// Prologue loads of a unit: A(0), A(1) into stages 0, 1; B(0..2) into slots
+// 0..2; scale blocks 0, 1.
+__device__ __forceinline__ void issue_prologue(State& st, const Ctx& c) {
 #pragma unroll
     for (int ii = 0; ii < 8; ++ii) dma16(c.m0a + ii * 1024, c.aoff[ii], c.dx, 0);
 #pragma unroll
@@ -392,6 +412,12 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
         buf_load1(st.bsc[0][j], c.soff[j], c.ds, 0);
         buf_load1(st.bsc[1][j], c.soff[j], c.ds, c.scol);
     }
+}
+
+// The rest of the prologue once those loads (and anything else in flight)
+// have landed: B(0) dequantized, B(1) codes and step 0's first A fragments
+// read; the accumulators cleared.
+__device__ __forceinline__ void finish_prologue(State& st, const Ctx& c) {
     wait_vm4<0>(st.bsc[0], st.bsc[1]);
     barrier();
 #pragma unroll
@@ -407,90 +433,208 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
     }(std::make_integer_sequence<int, 128>{});
 #pragma unroll
     for (int i = 0; i < MT; ++i) ds_read<0>(st.af[0][i], c.ard[0] + i * 4096);
+    const u32x4 zero{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) mfma_zero(st.acc[i][j], zero);
     wait_lgkm8<0>(st.af[0]);
+}
 
-    // ---- K loop, 4 steps per iteration; only LDS DMA stays in flight
-    // across the back edge.
-    Ring rg{0u, (uint32_t)A_STAGE, (uint32_t)(2 * A_STAGE), 0u, (uint32_t)(2 * B_SLOT)};
-    for (int kt = 0; kt < KT; kt += 4) {
-        kstep<0>(st, c, rg, kt);
-        rg.advance();
-        kstep<1>(st, c, rg, kt + 1);
-        rg.advance();
-        kstep<2>(st, c, rg, kt + 2);
-        rg.advance();
-        kstep<3>(st, c, rg, kt + 3);
-        rg.advance();
-        // step kt+3 read step kt+4's fragments and B(kt+5) (LDS) and loaded
-        // scale block (kt+6)/2 into bsc[1], followed by 10 DMA.
-        wait_lgkm12<0>(st.af[0], st.braw[1]);
-        wait_vm2<10>(st.bsc[1]);
-    }
-    // The last steps prefetched past K (the next rows, or zeros past the
-    // buffers); their LDS DMA must land before the workgroup's LDS is freed.
-    wait_vm<0>();
+// Requirements (checked by the launcher): K % 256 == 0; x and w 16-byte
+// aligned; S == K/128 or S == 1; M*K*2, N*K, N*S*4 and (M + 256)*ldy*2
+// below 2^31.  When SWIGLU, N is the number of weight rows (gate rows
+// [0, N/2), up rows [N/2, N)) and y is [M, N/2].  part: rtiles * splits
+// partial slots of 256 x 256 floats (unused when rtiles == 0).
+template <bool SWIGLU>
+__global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __restrict__ x,
+                                                          const uint8_t* __restrict__ w,
+                                                          const float* __restrict__ scales, int S,
+                                                          uint16_t* __restrict__ y, int ldy, int M, int N,
+                                                          int K, Plan plan, float* __restrict__ part) {
+    extern __shared__ __align__(16) uint16_t smem[];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
-    // ---- epilogue: acc[i][j][r] = C[32i + 8(r/4) + 4h + r%4][wave col 32j + l32].
-    // Stores go through a buffer bounded to the M x ldy output: rows >= M fall
-    // outside it and columns past the end get an out-of-range lane offset.
-    const int row0 = m0 + 4 * h;
-    if constexpr (PARTIAL) {
-        const rsrc_t rp = make_rsrc(reinterpret_cast<float*>(y) + (int64_t)blockIdx.y * M * N,
-                                    (uint32_t)((int64_t)M * N * 4));
-        uint32_t voff[NT];
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const int64_t n = wrow(32 * j + l32);
-            voff[j] = n >= 0 ? (uint32_t)(((int64_t)row0 * N + n) * 4) : kBufferOob;
+    int u = blockIdx.x;
+    Unit cur;
+    while (u < plan.units && !unit_of(u, plan, K, cur)) u += gridDim.x;
+    if (u >= plan.units) return;
+    Ctx c;
+    State st;
+    setup<SWIGLU>(c, cur, x, w, scales, S, M, N, K, wave, lane, lds0);
+    issue_prologue(st, c);
+    finish_prologue(st, c);
+
+    for (;;) {
+        // ---- K loop, 4 steps per iteration; only LDS DMA stays in flight
+        // across the back edge.
+        const int KT = cur.klen / BK;
+        Ring rg{0u, (uint32_t)A_STAGE, (uint32_t)(2 * A_STAGE), 0u, (uint32_t)(2 * B_SLOT)};
+        for (int kt = 0; kt < KT; kt += 4) {
+            kstep<0>(st, c, rg, kt);
+            rg.advance();
+            kstep<1>(st, c, rg, kt + 1);
+            rg.advance();
+            kstep<2>(st, c, rg, kt + 2);
+            rg.advance();
+            kstep<3>(st, c, rg, kt + 3);
+            rg.advance();
+            // step kt+3 read step kt+4's fragments and B(kt+5) (LDS) and loaded
+            // scale block (kt+6)/2 into bsc[1], followed by 10 DMA.
+            wait_lgkm12<0>(st.af[0], st.braw[1]);
+            wait_vm2<10>(st.bsc[1]);
         }
+        // The last steps prefetched past the K range (the next K, or zeros
+        // past the buffers); their LDS DMA must land before the rings are
+        // reused or the workgroup's LDS is freed.
+        wait_vm<0>();
+
+        // ---- next unit: once every wave is done reading the rings, its
+        // prologue loads run under this unit's epilogue.
+        int un = u + gridDim.x;
+        Unit nxt;
+        while (un < plan.units && !unit_of(un, plan, K, nxt)) un += gridDim.x;
+        const bool more = un < plan.units;
+        const int ep_mtile = cur.mtile, ep_ntile = cur.ntile, ep_slot = cur.slot;
+        if (more) {
+            barrier();
+            setup<SWIGLU>(c, nxt, x, w, scales, S, M, N, K, wave, lane, lds0);
+            issue_prologue(st, c);
+        }
+
+        // ---- epilogue: acc[i][j][r] = C[32i + 8(r/4) + 4h + r%4][wave col 32j + l32].
+        // Each accumulator pair is copied to VGPRs by an empty asm before its
+        // elements are read: with the accumulators live around the unit loop,
+        // element reads straight from them made the register allocator move
+        // every accumulator through scratch memory.
+        if (ep_slot >= 0) {
+            // FP32 partial of a split tail tile: rows and columns in tile order.
+            const rsrc_t rp = make_rsrc(part + (int64_t)ep_slot * kSlotFloats, (uint32_t)(kSlotFloats * 4));
+            uint32_t voff[NT];
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+            for (int j = 0; j < NT; ++j) voff[j] = (uint32_t)((4 * h * BN + wave * WN + 32 * j + l32) * 4);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+            for (int i = 0; i < MT; ++i) {
+                f32x16 av[NT] = {st.acc[i][0], st.acc[i][1]};
+                asm volatile("" : "+v"(av[0]), "+v"(av[1]));
 #pragma unroll
-                for (int j = 0; j < NT; ++j) {
-                    // copy the element first: __builtin_bit_cast of a vector
-                    // element reads element 0 with hipcc (ROCm 7.2)
-                    const float a = st.acc[i][j][r];
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, a), rp, (int)voff[j],
-                                                          dr * N * 4, 0);
+                for (int r = 0; r < 16; ++r) {
+                    const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) {
+                        // copy the element first: __builtin_bit_cast of a vector
+                        // element reads element 0 with hipcc (ROCm 7.2)
+                        const float a = av[j][r];
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, a), rp, (int)voff[j],
+                                                              dr * BN * 4, 0);
+                    }
                 }
             }
-        return;
-    }
-    const rsrc_t ry = make_rsrc(y, (uint32_t)((int64_t)M * ldy * 2));
-    if constexpr (SWIGLU) {
-        const int D = N >> 1;
-        const int col = ntile * (BN / 2) + wave * (WN / 2) + l32;
-        const uint32_t voff = col < D ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
+        } else {
+            // Stores go through a buffer bounded to the M x ldy output: rows
+            // >= M fall outside it and columns past the end get an
+            // out-of-range lane offset.
+            const int row0 = ep_mtile * BM + 4 * h;
+            const rsrc_t ry = make_rsrc(y, (uint32_t)((int64_t)M * ldy * 2));
+            if constexpr (SWIGLU) {
+                const int D = N >> 1;
+                const int col = ep_ntile * (BN / 2) + wave * (WN / 2) + l32;
+                const uint32_t voff = col < D ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
+                // 16 outputs per batch: with one wave per SIMD nothing else
+                // hides an output's dependency chain (exp2, rcp, the window
+                // test, two BF16 roundings), so independent outputs are
+                // computed side by side.
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+                for (int i = 0; i < MT; ++i) {
+                    uint32_t gu[16];
+                    uint16_t v[16];
+                    f32x16 a0 = st.acc[i][0], a1 = st.acc[i][1];
+                    asm volatile("" : "+v"(a0), "+v"(a1));
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
-                const uint32_t p = pack_bf16x2(f32x2{st.acc[i][0][r], st.acc[i][1][r]});
-                const uint16_t v = swiglu_bf16_bits((uint16_t)(p & 0xffffu), (uint16_t)(p >> 16));
-                __builtin_amdgcn_raw_buffer_store_b16(v, ry, (int)voff, dr * ldy * 2, 0);
+                    for (int r = 0; r < 16; ++r) gu[r] = pack_bf16x2(f32x2{a0[r], a1[r]});
+                    swiglu_bf16_batch<16>(gu, v);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+                        __builtin_amdgcn_raw_buffer_store_b16(v[r], ry, (int)voff, dr * ldy * 2, 0);
+                    }
+                }
+            } else {
+                // both accumulator columns of a row at once, in the order the
+                // SwiGLU epilogue reads them (fewer accumulators live at a time)
+                uint32_t voff[NT];
+#pragma unroll
+                for (int j = 0; j < NT; ++j) {
+                    const int col = ep_ntile * BN + wave * WN + 32 * j + l32;
+                    voff[j] = col < N ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
+                }
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    f32x16 a0 = st.acc[i][0], a1 = st.acc[i][1];
+                    asm volatile("" : "+v"(a0), "+v"(a1));
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
+                        const uint32_t p = pack_bf16x2(f32x2{a0[r], a1[r]});
+                        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(p & 0xffffu), ry, (int)voff[0],
+                                                              dr * ldy * 2, 0);
+                        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(p >> 16), ry, (int)voff[1], dr * ldy * 2,
+                                                              0);
+                    }
+                }
             }
-    } else {
-        // both accumulator columns of a row at once, in the order the SwiGLU
-        // epilogue reads them (fewer accumulators live at a time)
-        uint32_t voff[NT];
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            const int col = ntile * BN + wave * WN + 32 * j + l32;
-            voff[j] = col < N ? (uint32_t)(((int64_t)row0 * ldy + col) * 2) : kBufferOob;
         }
+        if (!more) break;
+        u = un;
+        cur = nxt;
+        finish_prologue(st, c);
+    }
+}
+
+// Tail reduction: tail tile r of the plan gets out = bf16(sum over s in
+// order of its partial slots) at the unsplit epilogue's rounding points, or
+// with SWIGLU y = swiglu(bf16(gate sum), bf16(up sum)), for rows < M and
+// columns inside the output.  Four tile columns per thread.
+template <bool SWIGLU>
+__global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restrict__ part, Plan plan, int M, int N,
+                                                          uint16_t* __restrict__ y, int64_t ldy) {
+    constexpr int CG = SWIGLU ? 32 : 64;  // 4-column groups per tile row
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)plan.rtiles * BM * CG) return;
+    const int r = (int)(idx / (BM * CG));
+    const int rem = (int)(idx % (BM * CG));
+    const int row = rem / CG, cg = rem % CG;
+    int mt, nt;
+    tile_coords(plan.full + r, plan.mtiles, plan.ntiles, mt, nt);
+    const int m = mt * BM + row;
+    if (m >= M) return;
+    // tile-local column of the first of the four (the gate column for SWIGLU)
+    const int lc = SWIGLU ? (cg / 8) * WN + 4 * (cg % 8) : 4 * cg;
+    const float* p = part + (int64_t)r * plan.splits * kSlotFloats + row * BN + lc;
+    auto sum = [&](int off) __attribute__((always_inline)) -> f32x4 {
+        f32x4 s = *reinterpret_cast<const f32x4*>(p + off);
+        for (int k = 1; k < plan.splits; ++k) s += *reinterpret_cast<const f32x4*>(p + (int64_t)k * kSlotFloats + off);
+        return s;
+    };
+    const f32x4 a = sum(0);
+    uint16_t* dst = y + (int64_t)m * ldy;
+    if constexpr (SWIGLU) {
+        const f32x4 g = sum(32);
+        const int D = N >> 1;
+        const int col = nt * (BN / 2) + (cg / 8) * (WN / 2) + 4 * (cg % 8);
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+        for (int q = 0; q < 4; ++q)
+            if (col + q < D) dst[col + q] = swiglu_bf16_bits(f32_to_bf16_bits(a[q]), f32_to_bf16_bits(g[q]));
+    } else {
+        const int col = nt * BN + lc;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int dr = 32 * i + 8 * (r >> 2) + (r & 3);
-                const uint32_t p = pack_bf16x2(f32x2{st.acc[i][0][r], st.acc[i][1][r]});
-                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(p & 0xffffu), ry, (int)voff[0], dr * ldy * 2, 0);
-                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(p >> 16), ry, (int)voff[1], dr * ldy * 2, 0);
-            }
+        for (int q = 0; q < 4; ++q)
+            if (col + q < N) dst[col + q] = f32_to_bf16_bits(a[q]);
     }
 }
 

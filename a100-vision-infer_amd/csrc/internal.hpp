@@ -30,14 +30,14 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
 hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, int S,
                        uint16_t* y, int64_t ldy, int M, int N, int K, bool swiglu,
                        hipStream_t stream);
-// Split-K form of the FP8 GEMM for outputs with few tiles: gemm_splits()
-// K ranges (1 = no split) whose FP32 sums go to part (splits * M * N floats,
-// 16-byte aligned), then one reduction launch writes y.  Unaligned x or w
-// run the unsplit GEMM (part unused).
-int gemm_splits(int S, int64_t ldy, int M, int N, int K, bool swiglu);
-hipError_t launch_gemm_split(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
-                             int64_t ldy, int M, int N, int K, bool swiglu, float* part, int splits,
-                             hipStream_t stream);
+// The FP8 GEMM with a workspace for K-split partials: where the tile count
+// leaves CUs idle (few tiles, or a small last round) K is split and a second
+// launch adds the FP32 partials.  gemm_workspace_bytes() is what that needs
+// (0 when nothing splits); a smaller or unaligned workspace, unaligned x or
+// w, or another kernel's shape run unsplit.
+size_t gemm_workspace_bytes(int S, int64_t ldy, int M, int N, int K, bool swiglu);
+hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
+                          int M, int N, int K, bool swiglu, void* ws, size_t ws_bytes, hipStream_t stream);
 
 // Elementwise kernels (elementwise.hip).
 hipError_t launch_dequant(const uint8_t* codes, const float* scales, int64_t S, uint16_t* y,

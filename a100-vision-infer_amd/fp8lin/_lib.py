@@ -42,6 +42,7 @@ EXPORTED = [
     "fp8lin_qk_norm_rope",
     "fp8lin_add_bias",
     "fp8lin_linear_candidates_static",
+    "fp8lin_linear_swiglu_workspace_bytes", "fp8lin_linear_swiglu_ws",
 ]
 
 
@@ -98,6 +99,8 @@ def lib():
         "fp8lin_linear_ld": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i64, i32, vp]),
         "fp8lin_linear_swiglu": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, vp]),
         "fp8lin_swiglu": (i32, [vp, vp, i64, i64, vp]),
+        "fp8lin_linear_swiglu_workspace_bytes": (sz, [i64, i64, i64]),
+        "fp8lin_linear_swiglu_ws": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, vp, sz, vp]),
         "fp8lin_add_bias": (i32, [vp, i64, vp, i64, i64, vp]),
         "fp8lin_linear_shared": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, vp]),
         "fp8lin_tensor_small_workspace_bytes": (sz, [i64, i64, i32]),

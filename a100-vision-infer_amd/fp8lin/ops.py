@@ -80,8 +80,11 @@ def fp8_linear(x, codes, scales, vector_gemv=False):
     return y
 
 
-def linear_swiglu(x, codes, scales):
-    """Fused `fused_swiglu(fp8_linear(x, gate_up))` (src/engine.cpp:415)."""
+def linear_swiglu(x, codes, scales, split=True):
+    """Fused `fused_swiglu(fp8_linear(x, gate_up))` (src/engine.cpp:415).
+    split: give the prefill GEMM a workspace so it may split K where whole
+    tiles would leave CUs idle (fp8lin_linear_swiglu_ws); False runs every
+    tile whole (fp8lin_linear_swiglu)."""
     _check_x(x, "FP8 linear expects CUDA BF16 [M,K]")
     _check_codes(codes, x)
     sc = _scale_cols(scales, codes.size(0), codes.size(1))
@@ -89,8 +92,14 @@ def linear_swiglu(x, codes, scales):
     if not (M > 0 and N > 0 and K > 0) or N % 2:
         _fail(ERR_SHAPE, "Invalid gate/up geometry")
     y = torch.empty((M, N // 2), dtype=torch.bfloat16, device=x.device)
-    check(lib().fp8lin_linear_swiglu(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K,
-                                     _stream(x)))
+    need = lib().fp8lin_linear_swiglu_workspace_bytes(M, N, K) if split else 0
+    if need:
+        ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+        check(lib().fp8lin_linear_swiglu_ws(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K, _ptr(ws),
+                                            need, _stream(x)))
+    else:
+        check(lib().fp8lin_linear_swiglu(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K,
+                                         _stream(x)))
     return y
 
 

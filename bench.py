@@ -336,7 +336,10 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
     for m in ((512, 1024, 4096) if "prefill" in sections else ()):
         x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
         y = torch.empty((m, n // 2), dtype=torch.bfloat16, device=dev)
-        ms = timed(torch, lambda: ok(L.fp8lin_linear_swiglu(P(x), P(c), P(s), s.size(1), P(y), m, n, k, sp)),
+        need = L.fp8lin_linear_swiglu_workspace_bytes(m, n, k)
+        pws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        ms = timed(torch, lambda: ok(L.fp8lin_linear_swiglu_ws(P(x), P(c), P(s), s.size(1), P(y), m, n, k, P(pws),
+                                                               need, sp)),
                    10 if m == 4096 else 20)
         tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         extra[f"prefill_swiglu_m{m}_TFLOPs"] = round(tflops, 1)
@@ -537,20 +540,24 @@ def layer_chain(torch, fp8lin, dev, ws, log):
         feeds = {"qkv_gate": x, "gate_up_swiglu": x, "down": outs["gate_up_swiglu"], "head": outs["down"]}
 
         # Non-SwiGLU links go through Engine::linear's dispatch (split-K for
-        # the few-tile prefill projections); gate/up through the fused kernel.
+        # the few-tile prefill projections); gate/up through the fused kernel,
+        # with its workspace.
         opt = fp8lin.LinearOptions()
         recs, wss = {}, {}
         for name, (c, s), n, k, sw in links:
             r = fp8lin.Weight()
             r.data, r.scales, r.scale_cols, r.cached_bf16, r.N, r.K = c.data_ptr(), s.data_ptr(), s.size(1), None, n, k
             recs[name] = r
-            need = L.fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(r), m)
+            need = (L.fp8lin_linear_swiglu_workspace_bytes(m, n, k) if sw else
+                    L.fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(r), m))
             wss[name] = (torch.empty(need, dtype=torch.uint8, device=dev) if need else None, need)
 
         def call(name, w, n, k, sw):
             c, s = w
             if sw:
-                ok(L.fp8lin_linear_swiglu(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k, sp))
+                ws, need = wss[name]
+                ok(L.fp8lin_linear_swiglu_ws(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k,
+                                             P(ws) if ws is not None else None, need, sp))
             else:
                 ws, need = wss[name]
                 ok(L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(recs[name]), P(feeds[name]), m,

@@ -98,6 +98,21 @@ int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* s
                          int64_t scale_cols, uint16_t* y, int64_t M, int64_t N, int64_t K,
                          fp8lin_stream_t stream);
 
+/* The same with a workspace, which lets the prefill GEMM (M > 8) split K
+ * where whole tiles would leave CUs idle: when the 256x256 tiles number
+ * fewer than half the CUs, or leave a last round on at most a quarter of
+ * them (M = 1024 and M = 4096 at N = 17408, K = 5120), those tiles are cut
+ * into K ranges whose FP32 sums a second launch adds in order before the
+ * SwiGLU rounding points.  Within the parity bar of the unsplit call (only
+ * the FP32 summation order of the split tiles differs).  The workspace is
+ * what fp8lin_linear_swiglu_workspace_bytes reports (0: none needed), 16-byte
+ * aligned.  Same replacement as fp8lin_linear_swiglu.
+ */
+size_t fp8lin_linear_swiglu_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int fp8lin_linear_swiglu_ws(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t scale_cols,
+                            uint16_t* y, int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                            fp8lin_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Bias add in place: y[r,c] = bf16(y[r,c] + bias[c]) for r < rows, c < N, y
  * with row stride ldy >= N; the BF16 `y + b` of Engine::linear
@@ -193,9 +208,10 @@ typedef struct fp8lin_linear_options {
 } fp8lin_linear_options;
 
 /* Workspace needed by fp8lin_engine_linear for this weight and row count;
- * 0 if none.  The FP8 GEMM branch (rows > 8) splits K when the output has at
- * most 128 tiles of 256x256 and then needs splits * rows * N FP32 partials;
- * the dequant-then-GEMM branch needs a 2048-row BF16 slab. */
+ * 0 if none.  The FP8 GEMM branch (rows > 8) splits K where its 256x256
+ * tiles would leave CUs idle (as fp8lin_linear_swiglu_ws does) and then needs
+ * 256 KiB of FP32 partials per split tile and K range; the dequant-then-GEMM
+ * branch needs a 2048-row BF16 slab. */
 size_t fp8lin_engine_linear_workspace_bytes(const fp8lin_linear_options* options,
                                             const fp8lin_weight* weight, int64_t rows);
 /* Id of the branch fp8lin_engine_linear takes for this weight, options and

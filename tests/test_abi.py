@@ -221,22 +221,45 @@ def test_engine_decision_table(fp8lin):
     assert _path(F, O(), _weight(F, scales=False), 4) == F.PATH_BF16
 
 
+SLOT = 256 * 256 * 4  # one FP32 partial tile
+
+
 def test_engine_splitk_workspace(fp8lin):
-    """FP8 GEMM branch: split-K partials when the output has <= 128 tiles of
-    256x256; splits = min(256 / tiles, K / 256, 8)."""
+    """FP8 GEMM branch on a 256-CU device: K-split partials (one 256x256 FP32
+    slot per split tile and K range) when the tiles number at most half the
+    CUs (every tile, min(256 / T, K / 256, 8) ranges) or leave a last round
+    on at most a quarter of them (those tiles, min(256 / R, K / 256, 8))."""
     F, O = fp8lin, fp8lin.LinearOptions
 
     def ws(n, k, rows, **kw):
         w = _weight(F, n=n, k=k, **kw)
         return F.lib().fp8lin_engine_linear_workspace_bytes(ctypes.byref(O()), ctypes.byref(w), rows)
-    assert ws(7168, 5120, 512) == 4 * 512 * 7168 * 4      # QKV-gate, 56 tiles
-    assert ws(5120, 8704, 512) == 6 * 512 * 5120 * 4      # down, 40 tiles
-    assert ws(7168, 5120, 1024) == 2 * 1024 * 7168 * 4    # 112 tiles
-    assert ws(17408, 5120, 512) == 0                      # 136 tiles: no split
-    assert ws(256, 512, 20) == 2 * 20 * 256 * 4           # K / 256 = 2 caps the splits
-    assert ws(256, 256, 20) == 0                          # one 256-K chunk
-    assert ws(256, 640, 20) == 0                          # K % 256 != 0: general GEMM
-    assert ws(7168, 5120, 8) == 0                         # GEMV rows
+    assert ws(7168, 5120, 512) == 56 * 4 * SLOT          # QKV-gate, 56 tiles
+    assert ws(5120, 8704, 512) == 40 * 6 * SLOT          # down, 40 tiles
+    assert ws(7168, 5120, 1024) == 112 * 2 * SLOT        # 112 tiles
+    assert ws(17408, 5120, 512) == 0                     # 136 tiles: no split
+    assert ws(17408, 5120, 1024) == 16 * 8 * SLOT        # 272 = 256 + 16: the 16 tail tiles
+    assert ws(17408, 5120, 4096) == 64 * 4 * SLOT        # 1088 = 4 * 256 + 64
+    assert ws(17408, 5120, 2560) == 0                    # 680 = 2 * 256 + 168: last round over a quarter
+    assert ws(256, 512, 20) == 1 * 2 * SLOT              # K / 256 = 2 caps the splits
+    assert ws(256, 256, 20) == 0                         # one 256-K chunk
+    assert ws(256, 640, 20) == 0                         # K % 256 != 0: general GEMM
+    assert ws(7168, 5120, 8) == 0                        # GEMV rows
+
+
+def test_linear_swiglu_workspace(fp8lin):
+    """The fused gate/up + SwiGLU splits by SwiGLU tiles (128 output pairs)."""
+    L = fp8lin.lib()
+    assert L.fp8lin_linear_swiglu_workspace_bytes(8, 17408, 5120) == 0        # GEMV rows
+    assert L.fp8lin_linear_swiglu_workspace_bytes(512, 17408, 5120) == 0      # 136 tiles
+    assert L.fp8lin_linear_swiglu_workspace_bytes(1024, 17408, 5120) == 16 * 8 * SLOT
+    assert L.fp8lin_linear_swiglu_workspace_bytes(4096, 17408, 5120) == 64 * 4 * SLOT
+    assert L.fp8lin_linear_swiglu_workspace_bytes(3913, 17408, 5120) == 64 * 4 * SLOT
+    assert L.fp8lin_linear_swiglu_workspace_bytes(64, 512, 512) == 2 * 2 * SLOT
+    assert L.fp8lin_linear_swiglu_workspace_bytes(64, 511, 512) == 0          # odd N
+    n = L.fp8lin_linear_swiglu_workspace_bytes(1024, 17408, 5120)
+    assert L.fp8lin_linear_swiglu_ws(P, P, P, 40, P, 1024, 17408, 5120, P, n - 16, None) == 4
+    assert L.fp8lin_linear_swiglu_ws(P, P, P, 40, P, 1024, 17407, 5120, P, n, None) == 1
 
 
 def test_engine_option_consistency(fp8lin):
