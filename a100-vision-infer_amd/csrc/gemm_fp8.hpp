@@ -73,6 +73,23 @@ __device__ __forceinline__ i32x4 make_desc(const void* base, uint32_t bytes) {
 __device__ __forceinline__ void mfma(f32x16& acc, const u32x4& a, const u32x4& b) {
     asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
+// The MFMAs are inline asm, so the compiler's hazard recognizer does not see
+// that their accumulators are still being written when the epilogue reads
+// them: wait for the last MFMA to finish (a 32x32x16 MFMA is 16 passes of 4
+// cycles; 80 wait states leave margin), and tie every accumulator to that
+// wait so no accumulator read is scheduled above it.
+template <int ROWS, int COLS>
+__device__ __forceinline__ void mfma_drain(f32x16 (&acc)[ROWS][COLS]) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\t"
+                 "s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+a"(acc[0][0]));
+#pragma unroll
+    for (int i = 0; i < ROWS; ++i)
+#pragma unroll
+        for (int j = 0; j < COLS; ++j)
+            if (i | j) asm volatile("" : "+a"(acc[i][j]));
+}
+
 // acc = 0 written straight into the accumulator registers (an MFMA of zero
 // operands with a zero addend), so cleared accumulators never pass through
 // VGPRs.
@@ -493,6 +510,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
         // past the buffers); their LDS DMA must land before the rings are
         // reused or the workgroup's LDS is freed.
         wait_vm<0>();
+        mfma_drain(st.acc);
 
         // ---- next unit: once every wave is done reading the rings, its
         // prologue loads run under this unit's epilogue.
