@@ -31,22 +31,6 @@ hipError_t run(const uint16_t* x, const void* w, const float* scales, int S, uin
                                                                              M, N, K, stream);
 }
 
-// Compute units of the current device (cached per device), rounded down to a
-// multiple of the 8 XCDs: the persistent FP8 grid size.
-int grid_cus() {
-    static std::atomic<int> cached[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    int v = cached[dev].load(std::memory_order_relaxed);
-    if (v == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) cus = 256;
-        v = cus / gemm_fp8::kXcds * gemm_fp8::kXcds;
-        cached[dev].store(v, std::memory_order_relaxed);
-    }
-    return v;
-}
-
 // Work plan of the persistent FP8 GEMM (see gemm_fp8.hpp).  Without a
 // workspace every tile is computed whole.  With one, K is split where the
 // tile count leaves CUs idle:
@@ -118,9 +102,25 @@ bool fp8_kernel_ok(const uint16_t* x, const void* w, int S, int64_t ldy, int M, 
 
 }  // namespace
 
+// Compute units of the current device (cached per device), rounded down to a
+// multiple of the 8 XCDs: the persistent kernels' grid size.
+int compute_units() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (v == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 8) cus = 256;
+        v = cus / gemm_fp8::kXcds * gemm_fp8::kXcds;
+        cached[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
 size_t gemm_workspace_bytes(int S, int64_t ldy, int M, int N, int K, bool swiglu) {
     if (!fp8_kernel_ok(nullptr, nullptr, S, ldy, M, N, K)) return 0;
-    return plan_bytes(make_plan(M, N, K, swiglu, grid_cus(), true));
+    return plan_bytes(make_plan(M, N, K, swiglu, compute_units(), true));
 }
 
 hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
@@ -128,7 +128,7 @@ hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales,
     const bool fp8 = scales != nullptr;
     if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
         const uint8_t* codes = static_cast<const uint8_t*>(w);
-        const int G = grid_cus();
+        const int G = compute_units();
         gemm_fp8::Plan plan = make_plan(M, N, K, swiglu, G, ws != nullptr);
         if (plan_bytes(plan) > ws_bytes || reinterpret_cast<uintptr_t>(ws) % 16 != 0)
             plan = make_plan(M, N, K, swiglu, G, false);
@@ -144,7 +144,7 @@ hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, in
     const bool fp8 = scales != nullptr;
     if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
         const uint8_t* codes = static_cast<const uint8_t*>(w);
-        const int G = grid_cus();
+        const int G = compute_units();
         const gemm_fp8::Plan plan = make_plan(M, N, K, swiglu, G, false);
         return swiglu ? run_fp8<true>(x, codes, scales, S, y, ldy, M, N, K, plan, G, nullptr, stream)
                       : run_fp8<false>(x, codes, scales, S, y, ldy, M, N, K, plan, G, nullptr, stream);

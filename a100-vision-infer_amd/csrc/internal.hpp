@@ -17,6 +17,10 @@ hipError_t launch_gemv_swiglu(const uint16_t* x, const uint8_t* codes, const flo
                               uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
                               hipStream_t stream);
 
+// Compute units of the current device, rounded down to a multiple of the 8
+// XCDs (cached per device): the grid of the persistent kernels (gemm.hip).
+int compute_units();
+
 // Small-M matrix-core kernel, 2 <= M <= 8, K % 128 == 0, block scales
 // (small_m.hip).  The K partition is the kernel's own, so split 1 and 4 give
 // the same bits; no workspace.  M * K * 2 and 16 * K must be below 2^31.

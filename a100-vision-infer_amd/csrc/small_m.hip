@@ -32,6 +32,13 @@
 // for every shape and the s_waitcnt counts below are fixed numbers.  The same
 // template also builds 64-row workgroups (NBW == 4: each wave its own 16 rows
 // over all blocks), which measured slower at every decode shape.
+//
+// Wide weights (N >= 32 rows per compute unit, K in a 1024-wide band ending
+// at 4096, 5120 or 9216) run small_m_stream_kernel instead: one workgroup per
+// compute unit, each owning an equal contiguous range of rows (ceil(N / CUs)),
+// so the work is balanced to a few rows instead of the 16-row workgroup
+// granularity that leaves a partial last round (1088 workgroups over 512
+// slots at the 17408-row gate/up).  See the kernel for its pipeline.
 #include <utility>
 
 #include "gemm_fp8.hpp"
@@ -48,6 +55,7 @@ using gemm_fp8::wait_vm;
 
 constexpr int kRowX = 1040;  // LDS stride of an activation row (1 KiB + 16 B)
 constexpr int kMaxM = 8;
+constexpr int kMaxLds = 160 * 1024;
 
 __device__ __forceinline__ int sw(int r) { return (r >> 1) & 7; }
 
@@ -278,6 +286,235 @@ hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, 
     return hipGetLastError();
 }
 
+// ---- persistent row-range form -------------------------------------------
+//
+// Workgroup b owns rows [b * per, min(N, (b + 1) * per)) and walks them in
+// pieces of 16 rows.  Its 8 waves split K block-wise: wave w owns the 128-K
+// blocks w + 8j, j < NB, of every piece, so its activation fragments (the
+// MFMA A operand of those blocks, 16 VGPRs per block) are loaded once and stay
+// in registers for the whole kernel.  Per step (piece p, own block j) a wave
+// consumes one 16-row x 128-code slot of its LDS ring of D slots (step
+// t = p * NB + j lives in slot t % D, D <= NB) and immediately refills it with
+// the codes of step t + D; the scales of a whole piece ([j][row] per wave)
+// come by DMA two pieces ahead into three piece buffers.  At the end of a
+// piece the eight partial 16x16 sums go through LDS and one wave adds them in
+// wave order into a BF16 staging row block; the staged outputs are written
+// once at the end.
+//
+// Issue order x fragments, scales of pieces 0 and 1, codes of steps 0..D-1,
+// then per step (scales of piece p + 2 at j == 0) and 2 code DMAs: the
+// number of loads issued after a step's codes is then the same fixed number
+// at every step from the first on, which is what wait_vm counts.  The
+// activations are raw buffer loads in inline asm, outside the compiler's wait
+// counting; their registers are tied to the first explicit wait.
+//
+// Summation order: per wave, its blocks in K order through MFMA; then the 8
+// wave partials in wave order.  It depends on K only (not on the row range),
+// so split 1 and 4 and every workgroup count give the same bits.
+constexpr int kStreamWaves = 8;
+constexpr int kStreamRed = 2 * kStreamWaves * 512;  // two buffers of 8 waves x 8 x 16 floats
+
+template <int NB>
+constexpr int stream_scale_dmas() { return (16 * NB + 63) / 64; }
+template <int NB, int D>
+constexpr int stream_lds_fixed() {
+    return kStreamWaves * D * 2048 + kStreamWaves * 3 * stream_scale_dmas<NB>() * 256 + kStreamRed;
+}
+constexpr int floordiv(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+
+// Requirements (checked by the host): 1 <= M <= 8, K % 128 == 0,
+// 8 * (NB - 1) < K / 128 <= 8 * NB, N * K < 2^31, per * M * 2 bytes of LDS
+// beyond stream_lds_fixed.
+template <int NB, int D>
+__global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const uint16_t* __restrict__ x,
+                                                                          const uint8_t* __restrict__ codes,
+                                                                          const float* __restrict__ scales,
+                                                                          uint16_t* __restrict__ y, int64_t ldy,
+                                                                          int M, int N, int K, int per) {
+    constexpr int W = kStreamWaves;
+    constexpr int SC = stream_scale_dmas<NB>();
+    static_assert(D <= NB, "the prologue matches the steady-state issue order only for D <= NB");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+    const int KB = K >> 7;
+    const int r0 = (int)blockIdx.x * per;
+    const int r1 = min(N, r0 + per);
+    const int np = r1 > r0 ? (r1 - r0 + 15) >> 4 : 0;
+    // piece order starts at blockIdx % np, so the short last piece of each
+    // range does not come at the same time on every compute unit
+    const int rot = np ? (int)blockIdx.x % np : 0;
+    const uint32_t o_codes = (uint32_t)(wave * D * 2048);
+    const uint32_t o_sc = (uint32_t)(W * D * 2048 + wave * 3 * SC * 256);
+    const uint32_t o_red = (uint32_t)(W * D * 2048 + W * 3 * SC * 256);
+    const uint32_t o_out = o_red + kStreamRed;
+
+    const i32x4 dw = make_desc(codes, (uint32_t)((int64_t)N * K));
+    const i32x4 ds = make_desc(scales, (uint32_t)((int64_t)N * KB * 4));
+    const i32x4 dx = make_desc(x, (uint32_t)(M * K * 2));
+
+    auto piece = [&](int p) __attribute__((always_inline)) -> int {  // first row of piece p
+        int q = p + rot;
+        if (q >= np) q -= np;
+        return r0 + 16 * q;
+    };
+    // Code DMA lanes: instruction q, lane -> row 8q + lane/8, LDS position
+    // lane%8 <- 16-byte chunk (lane%8) ^ sw(row) of the block's 128 codes.
+    uint32_t cvoff[2];
+    int crow[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int r = 8 * q + (lane >> 3);
+        crow[q] = r;
+        cvoff[q] = (uint32_t)(16 * ((lane & 7) ^ sw(r)));
+    }
+    const int row = lane & 15, g = lane >> 4;
+    auto issue_codes = [&](int p, int j, int slot) __attribute__((always_inline)) {
+        const int blk = wave + W * j;
+        const bool ok = p < np && blk < KB;
+        const int base = ok ? piece(p) : 0;
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + o_codes + (uint32_t)slot * 2048u);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int n = base + crow[q];
+            dma16(m0 + q * 1024, ok && n < r1 ? (uint32_t)(n * K + blk * 128) + cvoff[q] : kBufferOob, dw, 0);
+        }
+    };
+    // scales of piece p into buffer p % 3 as [j][row]
+    auto issue_scales = [&](int p) __attribute__((always_inline)) {
+        const int base = p < np ? piece(p) : 0;
+        const uint32_t m0 = lds0 + o_sc + (uint32_t)((p % 3) * SC * 256);
+#pragma unroll
+        for (int i = 0; i < SC; ++i) {
+            const int e = 64 * i + lane;
+            const int j = e >> 4, n = base + (e & 15), blk = wave + W * j;
+            const bool ok = p < np && j < NB && blk < KB && n < r1;
+            dma4(__builtin_amdgcn_readfirstlane(m0 + i * 256), ok ? (uint32_t)((n * KB + blk) * 4) : kBufferOob,
+                 ds);
+        }
+    };
+
+    // Activation fragments of the own blocks, A operand layout: lane (m = row,
+    // K sub-range g); K offset within a block 16g + 64(f/2) + 8(f%2), the same
+    // permutation as the code words the lane converts.  Rows >= M read zeros.
+    u32x4 xr[NB][4];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int blk = wave + W * j;
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const int k = blk * 128 + 16 * g + 64 * (f >> 1) + 8 * (f & 1);
+            const uint32_t off = row < M && blk < KB ? (uint32_t)((row * K + k) * 2) : kBufferOob;
+            asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(xr[j][f]) : "v"(off), "s"(dx));
+        }
+    }
+    issue_scales(0);
+    issue_scales(1);
+#pragma unroll
+    for (int t = 0; t < D; ++t) issue_codes(t / NB, t % NB, t);
+    wait_vm<2 * (D - 1)>();  // the activations, the first two scale pieces, step 0's codes
+#pragma unroll
+    for (int j = 0; j < NB; ++j) asm volatile("" : "+v"(xr[j][0]), "+v"(xr[j][1]), "+v"(xr[j][2]), "+v"(xr[j][3]));
+    float* red = reinterpret_cast<float*>(lds + o_red);
+    uint16_t* out = reinterpret_cast<uint16_t*>(lds + o_out);
+
+    int sbase = 0;  // (p * NB) % D
+    for (int p = 0; p < np; ++p) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const uint32_t sbuf = o_sc + (uint32_t)((p % 3) * SC * 256);
+        [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
+            ([&]() __attribute__((always_inline)) {
+                constexpr int j = J;
+                // loads issued after this step's codes: 2 per step over the
+                // D - 1 steps since, plus SC at each piece start among them
+                constexpr int starts = floordiv(j - 1, NB) - floordiv(j - D, NB);
+                wait_vm<2 * (D - 1) + SC * starts>();
+                int slot = sbase + j;
+                slot = slot >= D ? slot - D : slot;
+                if constexpr (NB > D) slot = slot >= D ? slot - D : slot;
+                const uint32_t sa = o_codes + (uint32_t)slot * 2048u;
+                const u32x4 c0 = *reinterpret_cast<const u32x4*>(lds + sa + row * 128 + 16 * (g ^ sw(row)));
+                const u32x4 c1 = *reinterpret_cast<const u32x4*>(lds + sa + row * 128 + 16 * ((4 + g) ^ sw(row)));
+                const float s = *reinterpret_cast<const float*>(lds + sbuf + (j * 16 + row) * 4);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const u32x4 cw = h ? c1 : c0;
+                    uint32_t wv[8];
+                    dequant4(cw.x, s, wv[0], wv[1]);
+                    dequant4(cw.y, s, wv[2], wv[3]);
+                    dequant4(cw.z, s, wv[4], wv[5]);
+                    dequant4(cw.w, s, wv[6], wv[7]);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xr[j][2 * h]),
+                                                                   as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc,
+                                                                   0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xr[j][2 * h + 1]),
+                                                                   as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc,
+                                                                   0, 0, 0);
+                }
+                // the slot's codes and the scale are in registers: refill
+                gemm_fp8::wait_lgkm<0>();
+                if constexpr (j == 0) issue_scales(p + 2);
+                issue_codes(p + (j + D) / NB, (j + D) % NB, slot);
+            }(), ...);
+        }(std::make_integer_sequence<int, NB>{});
+        sbase += NB % D;
+        sbase = sbase >= D ? sbase - D : sbase;
+        // acc[i] = C[m = 4g + i][n = row]; lanes g < 2 hold the rows m < 8
+        float* rb = red + (p & 1) * (W * 128);
+        if (g < 2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rb[wave * 128 + (4 * g + i) * 16 + row] = acc[i];
+        }
+        // Two buffers: wave (p % 8) reads buffer p & 1 before it reaches the
+        // barrier that ends piece p + 1, after which buffer p & 1 is rewritten.
+        gemm_fp8::wait_lgkm<0>();
+        barrier();
+        if (wave == (p & (W - 1)) && g < 2) {
+            const int n0 = piece(p);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 4 * g + i;
+                float t = rb[m * 16 + row];
+#pragma unroll
+                for (int w = 1; w < W; ++w) t = t + rb[w * 128 + m * 16 + row];
+                if (m < M && n0 + row < r1) out[m * per + (n0 - r0) + row] = f32_to_bf16_bits(t);
+            }
+        }
+    }
+    // DMAs past the last piece still target this workgroup's LDS
+    wait_vm<0>();
+    gemm_fp8::wait_lgkm<0>();
+    __syncthreads();
+    const int rows = r1 - r0;
+    for (int e = threadIdx.x; e < M * rows; e += 64 * W) {
+        const int m = e / rows, r = e - m * rows;
+        y[(int64_t)m * ldy + r0 + r] = out[m * per + r];
+    }
+}
+
+template <int NB, int D>
+hipError_t launch_stream(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy,
+                         int M, int N, int K, int per, hipStream_t stream) {
+    auto kern = small_m_stream_kernel<NB, D>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+    if (attr != hipSuccess) return attr;
+    const int groups = (N + per - 1) / per;
+    const size_t lds = (size_t)stream_lds_fixed<NB, D>() + (size_t)per * M * 2;
+    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kStreamWaves), lds, stream, x, codes, scales, y, ldy, M, N, K,
+                       per);
+    return hipGetLastError();
+}
+
+// Blocks per wave of the stream kernel for this K (0: not served).
+int stream_nb(int K) {
+    const int KB = K / 128;
+    for (int nb : {4, 5, 9})
+        if (KB > 8 * (nb - 1) && KB <= 8 * nb) return nb;
+    return 0;
+}
+
 }  // namespace
 
 // Four waves share 16 weight rows and split every chunk's 4 blocks, with a
@@ -288,8 +525,25 @@ hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, 
 // prefetch distance does not change the arithmetic.  Measured on MI355X at
 // the decode shapes (M = 2..8) this beats 64-row workgroups (the NBW == 4
 // form) for every shape, and deeper rings that leave one workgroup per CU.
+//
+// The stream kernel serves N >= 32 rows per compute unit (measured on MI355X
+// at M = 2, 4, 8: 17408 x 5120 gate/up 16-18% faster, the 75968-row head
+// 7-21%, the 8240-row in_proj_all 3-10%; at 7168 and 5120 rows the 16-row
+// workgroups stay faster).
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                           int64_t ldy, int M, int N, int K, int /*split*/, hipStream_t stream) {
+    const int cus = compute_units();
+    const int nb = stream_nb(K);
+    if (nb && N >= 32 * cus && (int64_t)N * K < ((int64_t)1 << 31)) {
+        const int per = (N + cus - 1) / cus;
+        const int fixed = nb == 4 ? stream_lds_fixed<4, 4>() : nb == 5 ? stream_lds_fixed<5, 5>()
+                                                                         : stream_lds_fixed<9, 7>();
+        if ((int64_t)fixed + (int64_t)per * M * 2 <= kMaxLds) {
+            if (nb == 4) return launch_stream<4, 4>(x, codes, scales, y, ldy, M, N, K, per, stream);
+            if (nb == 5) return launch_stream<5, 5>(x, codes, scales, y, ldy, M, N, K, per, stream);
+            return launch_stream<9, 7>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        }
+    }
     if (M <= 4) return launch<4, 4, 1, 2>(x, codes, scales, y, ldy, M, N, K, stream);
     return launch<4, 4, 1, 3>(x, codes, scales, y, ldy, M, N, K, stream);
 }

@@ -28,6 +28,11 @@ METRIC = "FP8 GEMV HBM GB/s (% peak) at M=1; prefill GEMM TFLOP/s (% MFMA peak)"
 # (272.0 KiB); the factors are what the counters read for a 256 MiB device copy
 # (`bench.py --calibrate`).  Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 92_912_640
+# MFMA busy fraction of the prefill kernel over its whole dispatch (M=4096
+# gate/up+SwiGLU): SQ_VALU_MFMA_BUSY_CYCLES summed over the SIMDs, divided by
+# GRBM_GUI_ACTIVE x SIMDs (rocprofv3's MfmaUtil), one --pmc pass.
+PREFILL_MFMA_BUSY = None
+PREFILL_MFMA_BUSY_SOURCE = "not measured"
 SHAPES = [("gate_up", 17408, 5120), ("down", 5120, 8704), ("qkv_gate", 7168, 5120)]
 
 
@@ -46,9 +51,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
-    p.add_argument("--sections", default="gemv,small,prefill,chain,head,stream,ceiling",
+    p.add_argument("--sections", default="gemv,small,prefill,chain,inproj,head,stream,ceiling",
                    help="secondary measurements to run (comma list of gemv, small, prefill, "
-                        "chain, head, stream, ceiling)")
+                        "chain, inproj, head, stream, ceiling)")
     p.add_argument("--calibrate", action="store_true",
                    help="also run a 256 MiB device copy (known HBM bytes) for counter scaling")
     return p.parse_args()
@@ -227,6 +232,21 @@ def main():
         "cpu_baseline": cpu,
         "extra": extra,
     }
+    if "prefill_swiglu_m4096_TFLOPs" in extra:
+        tf = extra["prefill_swiglu_m4096_TFLOPs"]
+        out["roofline_prefill"] = {
+            "bound": "mfma",
+            "kernel": "gemm_fp8_kernel<true> + tail_reduce_kernel<true> (gate/up+SwiGLU 17408x5120, M=4096)",
+            "achieved": tf,
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+            "avg_call_us": extra["prefill_swiglu_m4096_us"],
+            "algorithmic_flop_per_call": 2 * 4096 * 17408 * 5120,
+            "mfma_busy": PREFILL_MFMA_BUSY,
+            "mfma_busy_source": PREFILL_MFMA_BUSY_SOURCE,
+            "traffic": None,
+        }
     print(json.dumps(out), flush=True)
 
 
@@ -306,8 +326,13 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
         extra[f"gemv_m1_{name}_us"] = round(ms * 1e3, 2)
         log(f"gemv M=1 {name}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
     del cfg1
-    # small M (config 3): GEMV and matrix-core paths on the three shapes
-    for name, n, k in (SHAPES if "small" in sections else []):
+    # small M (config 3): GEMV and matrix-core paths on the three shapes and
+    # the reference benchmark's 8240 x 5120 (in_proj_all, all FP8; 13 copies)
+    small_copies = {name: [ws[name] for ws in sets] for name, _, _ in SHAPES}
+    if "small" in sections:
+        small_copies["in_proj_all"] = [fp8lin.gen_weights(8240, 5120, seed=0, tag=400 + c, device=dev)
+                                       for c in range(13)]
+    for name, n, k in (SHAPES + [("in_proj_all", 8240, 5120)] if "small" in sections else []):
         for m in (2, 4, 8):
             x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
             y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
@@ -323,13 +348,14 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
                 i = [0]
 
                 def run():
-                    c, s = sets[i[0] % len(sets)][name]
+                    c, s = small_copies[name][i[0] % len(small_copies[name])]
                     i[0] += 1
                     fn(c, s)
-                ms = graph_timed(torch, run, sp, reps=4 * len(sets), replays=10)
+                ms = graph_timed(torch, run, sp, reps=2 * len(small_copies[name]), replays=10)
                 gbs = algo_bytes(m, n, k) / (ms * 1e-3) / 1e9
                 extra[f"m{m}_{name}_{label}_GBs"] = round(gbs, 1)
                 log(f"M={m} {name} {label}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
+    del small_copies
     # prefill GEMM with fused SwiGLU (config 4)
     n, k = 17408, 5120
     c, s = sets[0]["gate_up"]
@@ -343,6 +369,7 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
                    10 if m == 4096 else 20)
         tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         extra[f"prefill_swiglu_m{m}_TFLOPs"] = round(tflops, 1)
+        extra[f"prefill_swiglu_m{m}_us"] = round(ms * 1e3, 2)
         extra[f"prefill_swiglu_m{m}_frac"] = round(tflops / BF16_PEAK_TFLOPS, 4)
         log(f"prefill M={m} gate/up+SwiGLU: {ms:.3f} ms {tflops:.1f} TFLOP/s "
             f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of BF16 peak)")
@@ -359,7 +386,9 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
         log(f"reference: torch.mm BF16 (hipBLASLt) M={m} N={n} K={k}: {ms:.3f} ms {tflops:.1f} TFLOP/s")
         del xa, wb
     if "chain" in sections:
-        extra.update(layer_chain(torch, fp8lin, dev, sets[0], log))
+        extra.update(layer_chain(torch, fp8lin, dev, sets, log))
+    if "inproj" in sections:
+        extra.update(in_proj_all(torch, fp8lin, dev, log))
     if "head" in sections:
         extra.update(head_and_epilogue(torch, fp8lin, dev, log))
     # streaming-read ceiling: 1 GiB and each decode weight size.  Each launch
@@ -511,66 +540,87 @@ def head_and_epilogue(torch, fp8lin, dev, log):
     return extra
 
 
-def layer_chain(torch, fp8lin, dev, ws, log):
+def layer_chain(torch, fp8lin, dev, sets, log):
     """Config 5: QKV-gate -> gate/up+SwiGLU -> down -> vocab-sharded head
     (75968 x 5120) at M = 512 and M = 1, each link fed by the previous one's
     output where the shapes chain (QKV-gate and gate/up both read the layer
-    input; attention between them is out of scope).  One step touches 577 MB
-    of weights, more than twice the 256 MB Infinity Cache, so no rotation is
-    needed."""
+    input; attention between them is out of scope).  The three layer links
+    rotate over the weight copies of `sets` (more than 512 MB together) and
+    the 389 MB head is one matrix, so every figure streams from HBM, for the
+    whole chain and for each link alone.  M = 1 is timed as graph replays of
+    back-to-back calls (the host's launch rate stays out), M = 512 eagerly."""
     import ctypes
     L = fp8lin.lib()
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
     head = fp8lin.gen_weights(75968, 5120, seed=0, tag=90, device=dev)
-    links = [("qkv_gate", ws["qkv_gate"], 7168, 5120, False),
-             ("gate_up_swiglu", ws["gate_up"], 17408, 5120, True),
-             ("down", ws["down"], 5120, 8704, False),
-             ("head", head, 75968, 5120, False)]
+    shapes = {"qkv_gate": (7168, 5120, False), "gate_up_swiglu": (17408, 5120, True),
+              "down": (5120, 8704, False), "head": (75968, 5120, False)}
+    weights = {"qkv_gate": [ws["qkv_gate"] for ws in sets], "gate_up_swiglu": [ws["gate_up"] for ws in sets],
+               "down": [ws["down"] for ws in sets], "head": [head]}
+    copies = len(sets)
     extra = {}
 
     def ok(rc):
         if rc:
             raise RuntimeError(L.fp8lin_last_error())
 
+    def record(w, n, k):
+        c, s = w
+        r = fp8lin.Weight()
+        r.data, r.scales, r.scale_cols, r.cached_bf16, r.N, r.K = c.data_ptr(), s.data_ptr(), s.size(1), None, n, k
+        return r
+
     for m in (1, 512):
         x = fp8lin.gen_activations(m, 5120, seed=0, tag=2, device=dev)
         outs = {name: torch.empty((m, n // 2 if sw else n), dtype=torch.bfloat16, device=dev)
-                for name, _, n, _, sw in links}
+                for name, (n, _, sw) in shapes.items()}
         feeds = {"qkv_gate": x, "gate_up_swiglu": x, "down": outs["gate_up_swiglu"], "head": outs["down"]}
 
         # Non-SwiGLU links go through Engine::linear's dispatch (split-K for
         # the few-tile prefill projections); gate/up through the fused kernel,
         # with its workspace.
         opt = fp8lin.LinearOptions()
-        recs, wss = {}, {}
-        for name, (c, s), n, k, sw in links:
-            r = fp8lin.Weight()
-            r.data, r.scales, r.scale_cols, r.cached_bf16, r.N, r.K = c.data_ptr(), s.data_ptr(), s.size(1), None, n, k
-            recs[name] = r
+        recs = {name: [record(w, n, k) for w in weights[name]] for name, (n, k, _) in shapes.items()}
+        wss = {}
+        for name, (n, k, sw) in shapes.items():
             need = (L.fp8lin_linear_swiglu_workspace_bytes(m, n, k) if sw else
-                    L.fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(r), m))
+                    L.fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(recs[name][0]), m))
             wss[name] = (torch.empty(need, dtype=torch.uint8, device=dev) if need else None, need)
 
-        def call(name, w, n, k, sw):
-            c, s = w
+        def call(name, i):
+            n, k, sw = shapes[name]
+            ws, need = wss[name]
+            wp = P(ws) if ws is not None else None
             if sw:
-                ws, need = wss[name]
-                ok(L.fp8lin_linear_swiglu_ws(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k,
-                                             P(ws) if ws is not None else None, need, sp))
+                c, s = weights[name][i % len(weights[name])]
+                ok(L.fp8lin_linear_swiglu_ws(P(feeds[name]), P(c), P(s), s.size(1), P(outs[name]), m, n, k, wp,
+                                             need, sp))
             else:
-                ws, need = wss[name]
-                ok(L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(recs[name]), P(feeds[name]), m,
-                                          P(outs[name]), n, P(ws) if ws is not None else None, need, None, sp))
+                rec = recs[name][i % len(recs[name])]
+                ok(L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(rec), P(feeds[name]), m,
+                                          P(outs[name]), n, wp, need, None, sp))
 
-        def chain():
-            for link in links:
-                call(*link)
-        iters = 200 if m == 1 else 10
-        total_ms = timed(torch, chain, iters)
+        def rotating(fn):
+            i = [0]
+
+            def run():
+                fn(i[0])
+                i[0] += 1
+            return run
+
+        def chain(i):
+            for name in shapes:
+                call(name, i)
+
+        def time_it(fn):
+            if m == 1:
+                return graph_timed(torch, rotating(fn), sp, reps=4 * copies, replays=10)
+            return timed(torch, rotating(fn), 2 * copies)
+        total_ms = time_it(chain)
         tot_bytes = tot_flops = 0
-        for name, w, n, k, sw in links:
-            ms = timed(torch, lambda: call(name, w, n, k, sw), iters)
+        for name, (n, k, sw) in shapes.items():
+            ms = time_it(lambda i: call(name, i))
             nbytes = algo_bytes(m, n, k, n // 2 if sw else n)
             flops = 2.0 * m * n * k
             tot_bytes += nbytes
@@ -590,7 +640,66 @@ def layer_chain(torch, fp8lin, dev, ws, log):
             tf = tot_flops / (total_ms * 1e-3) / 1e12
             extra[f"chain_m{m}_TFLOPs"] = round(tf, 1)
             log(f"chain M={m}: {total_ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / BF16_PEAK_TFLOPS:.1f}% MFMA)")
-        log("  " + ", ".join(f"{name} {extra[f'chain_m{m}_{name}_us']} us" for name, *_ in links))
+        log("  " + ", ".join(f"{name} {extra[f'chain_m{m}_{name}_us']} us" for name in shapes))
+    return extra
+
+
+def in_proj_all(torch, fp8lin, dev, log):
+    """The GDN in_proj_all group at one rank's size (src/engine.cpp:198-199,
+    tests/linear_benchmark.cpp:22): qkv + z fused into 8192 FP8 rows, then the
+    BF16 b and a projections (24 + 24 rows), K = 5120, through
+    fp8lin_engine_linear_groups into one [M, 8240] output.  M = 1 and 4 are
+    decode (M = 4 with the small-M matrix-core option, as the reference's
+    benchmark runs its tensor-small variants), M = 512 a prefill chunk.  The
+    FP8 group rotates over 13 copies (545 MB), so the decode figures are HBM
+    figures."""
+    import ctypes
+    L = fp8lin.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    k, nf, nb = 5120, 8192, 48
+    fp8 = [fp8lin.gen_weights(nf, k, seed=0, tag=300 + c, device=dev) for c in range(13)]
+    bf16 = (fp8lin.gen_activations(nb, k, seed=1, tag=20, device=dev).float() * 0.02).to(torch.bfloat16)
+    extra = {}
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(L.fp8lin_last_error())
+
+    def groups(c, s):
+        g = (fp8lin.Weight * 2)()
+        g[0].data, g[0].scales, g[0].scale_cols, g[0].cached_bf16, g[0].N, g[0].K = (
+            c.data_ptr(), s.data_ptr(), s.size(1), None, nf, k)
+        g[1].data, g[1].scales, g[1].scale_cols, g[1].cached_bf16, g[1].N, g[1].K = (
+            bf16.data_ptr(), None, 0, None, nb, k)
+        return g
+    recs = [groups(c, s) for c, s in fp8]
+    for m in (1, 4, 512):
+        opt = fp8lin.LinearOptions(fp8_tensor_small=(m == 4))
+        x = fp8lin.gen_activations(m, k, seed=0, tag=7, device=dev)
+        y = torch.empty((m, nf + nb), dtype=torch.bfloat16, device=dev)
+        need = max(L.fp8lin_engine_linear_workspace_bytes(ctypes.byref(opt), ctypes.byref(recs[0][j]), m)
+                   for j in range(2))
+        ws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        i = [0]
+
+        def run():
+            g = recs[i[0] % len(recs)]
+            i[0] += 1
+            ok(L.fp8lin_engine_linear_groups(ctypes.byref(opt), g, 2, P(x), m, P(y), nf + nb, P(ws), need, sp))
+        ms = (graph_timed(torch, run, sp, reps=2 * len(recs), replays=10) if m <= 8 else
+              timed(torch, run, 2 * len(recs)))
+        nbytes = algo_bytes(m, nf, k) + nb * k * 2 + 2 * m * nb
+        key = f"in_proj_all_m{m}"
+        extra[key + "_us"] = round(ms * 1e3, 2)
+        if m <= 8:
+            extra[key + "_GBs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            log(f"in_proj_all M={m} (8192 FP8 + 48 BF16 rows, K=5120): {ms * 1e3:.2f} us "
+                f"{nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
+        else:
+            tf = 2.0 * m * (nf + nb) * k / (ms * 1e-3) / 1e12
+            extra[key + "_TFLOPs"] = round(tf, 1)
+            log(f"in_proj_all M={m}: {ms:.3f} ms {tf:.1f} TFLOP/s")
     return extra
 
 
@@ -603,6 +712,19 @@ def calibrate(torch, dev, log):
     gbs = 2 * (1 << 28) / (ms * 1e-3) / 1e9
     log(f"calibration copy 256 MiB: {ms * 1e3:.1f} us ({gbs:.1f} GB/s read+write)")
     return {"calibration_copy_256MiB_us": round(ms * 1e3, 1)}
+
+
+def cpu_model():
+    """The host CPU's model name and logical CPU count (what lscpu prints as
+    "Model name" and "CPU(s)"), from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            names = [line.split(":", 1)[1].strip() for line in f if line.startswith("model name")]
+    except OSError:
+        return None
+    if not names:
+        return None
+    return f"{names[0]} ({len(names)} logical CPUs; {os.cpu_count()} visible)"
 
 
 def cpu_baseline(ws, xs, seconds, log):
@@ -647,7 +769,7 @@ def cpu_baseline(ws, xs, seconds, log):
     part = time.perf_counter() - t0
     est = part * 17408 / 64
     log(f"cpu oracle prefill M=4096 gate/up: {est:.1f} s extrapolated from 64 rows ({part:.2f} s)")
-    cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
            "sample": f"{reps} full decode steps (3 GEMVs, M=1) in {el:.1f} s; "
                      f"{per * 1e3:.1f} ms per step; FP64 oracle, OpenMP over output rows"}
     extra = {"cpu_1thread_ms_per_step": round(per1 * 1e3, 1),

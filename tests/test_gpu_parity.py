@@ -172,6 +172,26 @@ def test_tensor_small_vs_fp64(fp8lin, gpu, oracle, m, k, n):
             assert torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("n,k,m", [(8192, 4096, 2), (8200, 3584, 8), (9000, 8704, 5), (8240, 5120, 3),
+                                   (12000, 4224, 7), (8192, 5120, 8)])
+def test_tensor_small_wide(fp8lin, gpu, oracle, n, k, m):
+    """Wide weights (32 or more rows per compute unit) take the persistent
+    row-range kernel: ranges of ceil(N / CUs) rows walked in 16-row pieces,
+    with a short last piece (33 rows: 16 + 16 + 1; 36: 16 + 16 + 4), each K
+    band (4096, 5120, 9216) and a K with one block in the last step (4224).
+    Every row against the FP64 oracle; split 1 and 4 bit-equal."""
+    rng = np.random.default_rng(n + k + m)
+    codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
+    codes[(codes == 127) | (codes == 255)] = 0
+    scales = (rng.random((n, k // 128)) * .001 + .0001).astype(np.float32)
+    x = rand_bf16(rng, (m, k), 0.1)
+    ref = oracle.linear(x, codes, scales)
+    xg, cg, sg = up(x, gpu), up(codes, gpu), up(scales, gpu)
+    y1 = fp8lin.fp8_tensor_small(xg, cg, sg, 1)
+    assert_parity(bits(y1), ref, f"tensor_small wide {m}x{n}x{k}")
+    assert torch.equal(y1, fp8lin.fp8_tensor_small(xg, cg, sg, 4))
+
+
 def test_tensor_small_graph_replay(fp8lin, gpu, oracle):
     """tests/fp8_tensor_test.cpp:40-52: a captured graph sees updated
     activations on every replay."""
