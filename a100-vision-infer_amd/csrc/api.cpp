@@ -132,6 +132,15 @@ void linear_impl(const uint16_t* x, const uint8_t* codes, const float* scales, i
     }
 }
 
+// fp8lin_linear(x, W) followed by its vocabulary candidates, in `ws`
+// (linear_candidates_ws bytes).  Where the linear runs the ring GEMV, the
+// candidates come from that kernel's epilogue (the same per-row sums, rounded
+// to the same BF16 logits, never stored) and one finishing launch; otherwise
+// the logits go to the workspace and the two-stage candidate kernels read
+// them.
+void linear_candidates_impl(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S, int64_t M,
+                            int64_t N, int64_t K, int64_t offset, void* ws, double* out, hipStream_t stream);
+
 void gemm_bf16_impl(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t ldy, int64_t M,
                     int64_t N, int64_t K, hipStream_t stream) {
     if (M <= 8) {
@@ -364,7 +373,28 @@ size_t vocab_ws(int64_t M, int64_t N) { return (size_t)(M * fp8lin::vocab_chunks
 
 // Output head: the logits (padded to 256 bytes), then the chunk partials.
 int64_t logits_bytes(int64_t M, int64_t N) { return (M * N * 2 + 255) / 256 * 256; }
-size_t linear_candidates_ws(int64_t M, int64_t N) { return (size_t)logits_bytes(M, N) + vocab_ws(M, N); }
+// Either candidate form: the logits and chunk pairs of the two-stage form, or
+// the GEMV candidate form's pairs, slices and counters (no logits).
+size_t linear_candidates_ws(int64_t M, int64_t N) {
+    const size_t two_stage = (size_t)logits_bytes(M, N) + vocab_ws(M, N);
+    return M <= 2 ? std::max(two_stage, fp8lin::gemv_candidates_ws_bytes((int)M, (int)N)) : two_stage;
+}
+
+void linear_candidates_impl(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S, int64_t M,
+                            int64_t N, int64_t K, int64_t offset, void* ws, double* out, hipStream_t stream) {
+    const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
+    if (M <= 8 && fp8lin::gemv_candidates_supported((int)M, (int)N, (int)K, wide)) {
+        check_hip(fp8lin::launch_gemv_candidates(x, codes, scales, (int)S, (int)M, (int)N, (int)K, offset, ws, out,
+                                                 stream),
+                  "fp8 gemv candidates launch");
+        return;
+    }
+    auto* logits = static_cast<uint16_t*>(ws);
+    auto* part = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + logits_bytes(M, N));
+    linear_impl(x, codes, scales, S, logits, N, M, N, K, stream);
+    check_hip(fp8lin::launch_vocab_candidates(logits, (int)M, (int)N, offset, part, out, stream),
+              "vocabulary candidates launch");
+}
 
 }  // namespace
 
@@ -701,11 +731,7 @@ int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const floa
                         "linear candidates: workspace too small");
         ensure_device();
         const hipStream_t s = as_stream(stream);
-        auto* logits = static_cast<uint16_t*>(workspace);
-        auto* part = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + logits_bytes(M, N));
-        linear_impl(x, codes, scales, scale_cols, logits, N, M, N, K, s);
-        check_hip(fp8lin::launch_vocab_candidates(logits, (int)M, (int)N, offset, part, out, s),
-                  "vocabulary candidates launch");
+        linear_candidates_impl(x, codes, scales, scale_cols, M, N, K, offset, workspace, out, s);
     });
 }
 
@@ -723,17 +749,16 @@ int fp8lin_linear_candidates_static(const uint16_t* x, const uint8_t* codes, con
         const int dev = ensure_device();
         const hipStream_t s = as_stream(stream);
         char* base = static_cast<char*>(g_scratch[dev]);
-        auto* logits = reinterpret_cast<uint16_t*>(base);
-        auto* part = reinterpret_cast<uint32_t*>(base + logits_bytes(M, N));
-        linear_impl(x, codes, scales, scale_cols, logits, N, M, N, K, s);
-        check_hip(fp8lin::launch_vocab_candidates(logits, (int)M, (int)N, offset, part, out, s),
-                  "vocabulary candidates launch");
+        linear_candidates_impl(x, codes, scales, scale_cols, M, N, K, offset, base, out, s);
     });
 }
 
+size_t engine_candidates_head(int64_t rows, int64_t N) {
+    return (linear_candidates_ws(rows, N) + 255) / 256 * 256;
+}
+
 size_t engine_candidates_ws(const fp8lin_linear_options& o, const fp8lin_weight& w, int64_t rows) {
-    const size_t head = (size_t)logits_bytes(rows, w.N) + (vocab_ws(rows, w.N) + 255) / 256 * 256;
-    return head + engine_ws(o, w, rows);
+    return engine_candidates_head(rows, w.N) + engine_ws(o, w, rows);
 }
 
 size_t fp8lin_engine_linear_candidates_workspace_bytes(const fp8lin_linear_options* options,
@@ -760,13 +785,20 @@ int fp8lin_engine_linear_candidates(const fp8lin_linear_options* options, const 
         char* base = static_cast<char*>(workspace);
         auto* logits = reinterpret_cast<uint16_t*>(base);
         auto* part = reinterpret_cast<uint32_t*>(base + logits_bytes(rows, weight->N));
-        const size_t head = (size_t)logits_bytes(rows, weight->N) + (vocab_ws(rows, weight->N) + 255) / 256 * 256;
+        const size_t head = engine_candidates_head(rows, weight->N);
         validate_engine(*options, *weight, x, rows, logits, weight->N);
         ensure_device();
         const hipStream_t s = as_stream(stream);
-        const int path = engine_impl(*options, *weight, x, rows, logits, weight->N, base + head, workspace_bytes - head, s);
-        check_hip(fp8lin::launch_vocab_candidates(logits, (int)rows, (int)weight->N, offset, part, out, s),
-                  "vocabulary candidates launch");
+        int path = engine_path(*options, *weight, rows);
+        if (path == FP8LIN_PATH_FP8_GEMV && !weight->bias) {
+            // the FP8 GEMV branch is fp8lin_linear: its candidate form
+            linear_candidates_impl(x, static_cast<const uint8_t*>(weight->data), weight->scales, weight->scale_cols,
+                                   rows, weight->N, weight->K, offset, base, out, s);
+        } else {
+            path = engine_impl(*options, *weight, x, rows, logits, weight->N, base + head, workspace_bytes - head, s);
+            check_hip(fp8lin::launch_vocab_candidates(logits, (int)rows, (int)weight->N, offset, part, out, s),
+                      "vocabulary candidates launch");
+        }
         if (path_out) *path_out = path;
     });
 }

@@ -59,6 +59,25 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                            __builtin_bit_cast(bf16x2, b), acc, false);
 }
 
+// ---- vocabulary candidates ----
+// (value, id) order: larger value first, then the smaller id.  It is a total
+// order on the pairs, so any reduction tree gives the reference's result
+// (torch.max over a row, src/dual_path.cu:37-55).
+__device__ __forceinline__ void pick(float& v, uint32_t& id, float ov, uint32_t oid) {
+    if (ov > v || (ov == v && oid < id)) {
+        v = ov;
+        id = oid;
+    }
+}
+
+// NaN counts as +inf: the row's candidate becomes non-finite and the merge
+// rejects it, as torch.max's NaN propagation does in the reference.
+__device__ __forceinline__ void pick_bf16(float& v, uint32_t& id, uint32_t bits, uint32_t i) {
+    float f = bf16_bits_to_f32(bits);
+    if (f != f) f = __builtin_inff();
+    pick(v, id, f, i);
+}
+
 // Butterfly sum over the 64 lanes of a wave; every lane gets the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -159,23 +159,6 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_kernel(const uint16_t* __
 }
 
 // ---- vocabulary candidates ----
-// (value, id) order: larger value first, then the smaller id.  It is a total
-// order on the pairs, so any reduction tree gives the reference's result.
-__device__ __forceinline__ void pick(float& v, uint32_t& id, float ov, uint32_t oid) {
-    if (ov > v || (ov == v && oid < id)) {
-        v = ov;
-        id = oid;
-    }
-}
-
-// NaN counts as +inf: the row's candidate becomes non-finite and the merge
-// rejects it, as torch.max's NaN propagation does in the reference.
-__device__ __forceinline__ void pick_bf16(float& v, uint32_t& id, uint32_t bits, uint32_t i) {
-    float f = bf16_bits_to_f32(bits);
-    if (f != f) f = __builtin_inff();
-    pick(v, id, f, i);
-}
-
 // Stage 1, grid (chunks, M) x 256 threads: the best of one 2048-column chunk
 // of a row as {float bits, column} into part[(m * chunks + chunk) * 2].  One
 // 16-byte load per thread (VEC: N % 8 == 0 and 16-byte aligned rows), so
@@ -238,19 +221,114 @@ __global__ __launch_bounds__(kVocabThreads) void vocab_partial_kernel(const uint
     }
 }
 
-__global__ __launch_bounds__(64) void vocab_finish_kernel(const uint32_t* __restrict__ part, int chunks,
-                                                          int64_t offset, double* __restrict__ out) {
+// THREADS threads per row; pairs are read as 8-byte words, UNROLL per thread
+// in flight (branch-free raw buffer loads).
+template <int THREADS, int UNROLL>
+__global__ __launch_bounds__(THREADS) void vocab_finish_kernel(const uint32_t* __restrict__ part, int chunks,
+                                                               int64_t offset, double* __restrict__ out) {
+    __shared__ float sv[THREADS / 64];
+    __shared__ uint32_t sid[THREADS / 64];
     const int m = blockIdx.x;
+    // raw buffer loads: a pair past the row's end reads zeros instead of
+    // branching, so all UNROLL loads of a thread issue back to back
+    const rsrc_t r = make_rsrc(part + (int64_t)m * chunks * 2, (uint32_t)chunks * 8u);
     float best = -__builtin_inff();
     uint32_t id = 0xffffffffu;
-    for (int c = threadIdx.x; c < chunks; c += 64) {
-        const uint32_t* p = part + ((int64_t)m * chunks + c) * 2;
-        pick(best, id, __builtin_bit_cast(float, p[0]), p[1]);
+    for (int c0 = threadIdx.x; c0 < chunks; c0 += UNROLL * THREADS) {
+        u32x2 p[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+            p[u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                 r, (int)((uint32_t)(c0 + u * THREADS) * 8u), 0, 0));
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+            if (c0 + u * THREADS < chunks) pick(best, id, __builtin_bit_cast(float, p[u].x), p[u].y);
     }
     wave_pick(best, id);
+    if constexpr (THREADS > 64) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        if (lane == 0) {
+            sv[wave] = best;
+            sid[wave] = id;
+        }
+        __syncthreads();
+        if (threadIdx.x != 0) return;
+#pragma unroll
+        for (int q = 1; q < THREADS / 64; ++q) pick(best, id, sv[q], sid[q]);
+    }
     if (threadIdx.x == 0) {
         out[2 * m] = (double)best;
         out[2 * m + 1] = (double)((int64_t)id + offset);
+    }
+}
+
+// grid (kCandSlices, M) x 256 threads, over the pairs of nb workgroups in
+// 8 XCD runs of ceil(nb / 8) slots (gemv_ring_cand_kernel's layout; slot
+// (x, j) holds workgroup x + 8j, unwritten when that is nb or more).  Slice s
+// of row m reduces slots [s * per, (s + 1) * per) in one round of loads and
+// publishes its best pair;
+// the slice workgroup that arrives last (device-scope counter, cleared by the
+// producing kernel) reduces the kCandSlices slice pairs in slice order (any
+// order gives the same pair: the candidate order is total) and writes out[m].
+constexpr int kSliceThreads = 256;
+__global__ __launch_bounds__(kSliceThreads) void cand_finish_sliced_kernel(const uint32_t* __restrict__ part,
+                                                                           int nb, int per,
+                                                                           uint32_t* __restrict__ slices,
+                                                                           uint32_t* __restrict__ counters,
+                                                                           int64_t offset, double* __restrict__ out) {
+    __shared__ float sv[kSliceThreads / 64];
+    __shared__ uint32_t sid[kSliceThreads / 64];
+    __shared__ int last;
+    const int s = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+    const int run = (nb + 7) / 8, chunks = 8 * run;
+    const int lo = s * per, hi = min(chunks, lo + per);
+    const rsrc_t r = make_rsrc(part + (int64_t)m * chunks * 2, (uint32_t)chunks * 8u);
+    float best = -__builtin_inff();
+    uint32_t id = 0xffffffffu;
+    for (int c0 = lo + t; c0 < hi; c0 += 8 * kSliceThreads) {
+        u32x2 p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            p[u] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                 r, (int)((uint32_t)(c0 + u * kSliceThreads) * 8u), 0, 0));
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * kSliceThreads;
+            if (c < hi && c / run + 8 * (c % run) < nb) pick(best, id, __builtin_bit_cast(float, p[u].x), p[u].y);
+        }
+    }
+    wave_pick(best, id);
+    const int lane = t & 63, wave = t >> 6;
+    if (lane == 0) {
+        sv[wave] = best;
+        sid[wave] = id;
+    }
+    __syncthreads();
+    if (t == 0) {
+#pragma unroll
+        for (int q = 1; q < kSliceThreads / 64; ++q) pick(best, id, sv[q], sid[q]);
+        uint32_t* sp = slices + ((int64_t)m * kCandSlices + s) * 2;
+        __hip_atomic_store(sp, __builtin_bit_cast(uint32_t, best), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sp + 1, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // release the slice pair, then count this slice in
+        const uint32_t before = __hip_atomic_fetch_add(counters + m, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last = before == (uint32_t)(kCandSlices - 1);
+    }
+    __syncthreads();
+    if (!last) return;
+    if (t < 64) {
+        float b = -__builtin_inff();
+        uint32_t i = 0xffffffffu;
+        if (t < kCandSlices) {
+            const uint32_t* sp = slices + ((int64_t)m * kCandSlices + t) * 2;
+            b = __builtin_bit_cast(float, __hip_atomic_load(sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            i = __hip_atomic_load(sp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        wave_pick(b, i);
+        if (t == 0) {
+            out[2 * m] = (double)b;
+            out[2 * m + 1] = (double)((int64_t)i + offset);
+        }
     }
 }
 
@@ -547,6 +625,9 @@ hipError_t launch_reduce_rms(const uint16_t* x, const uint16_t* partials, int ra
 
 int64_t vocab_chunks(int64_t N) { return (N + kVocabChunk - 1) / kVocabChunk; }
 
+static hipError_t launch_candidates_finish(const uint32_t* part, int M, int64_t chunks, int64_t offset,
+                                          double* out, hipStream_t stream);
+
 hipError_t launch_vocab_candidates(const uint16_t* logits, int M, int N, int64_t offset, uint32_t* part,
                                    double* out, hipStream_t stream) {
     const int chunks = (int)vocab_chunks(N);
@@ -557,7 +638,21 @@ hipError_t launch_vocab_candidates(const uint16_t* logits, int M, int N, int64_t
         hipLaunchKernelGGL(vocab_partial_kernel<false>, grid, block, 0, stream, logits, N, chunks, part);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(vocab_finish_kernel, dim3(M), dim3(64), 0, stream, part, chunks, offset, out);
+    return launch_candidates_finish(part, M, chunks, offset, out, stream);
+}
+
+hipError_t launch_candidates_finish_sliced(const uint32_t* part, int M, int64_t chunks, uint32_t* slices,
+                                           uint32_t* counters, int64_t offset, double* out, hipStream_t stream) {
+    const int64_t slots = (chunks + 7) / 8 * 8;
+    const int per = (int)((slots + kCandSlices - 1) / kCandSlices);
+    hipLaunchKernelGGL(cand_finish_sliced_kernel, dim3(kCandSlices, M), dim3(kSliceThreads), 0, stream, part,
+                       (int)chunks, per, slices, counters, offset, out);
+    return hipGetLastError();
+}
+
+static hipError_t launch_candidates_finish(const uint32_t* part, int M, int64_t chunks, int64_t offset,
+                                          double* out, hipStream_t stream) {
+    hipLaunchKernelGGL((vocab_finish_kernel<64, 4>), dim3(M), dim3(64), 0, stream, part, (int)chunks, offset, out);
     return hipGetLastError();
 }
 

@@ -56,16 +56,22 @@ hipError_t general(const uint16_t* x, const void* w, const float* scales, int S,
     return launch<MR, R, 4, FP8, SWIGLU, true>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
 }
 
+// Whether the 128-bit FP8 path runs the ring kernel (raw-buffer kernels take
+// 32-bit byte offsets).
+bool ring_path(bool fp8, bool wide, int M, int N, int K) {
+    if (!(fp8 && wide && K <= kRingMaxK && (int64_t)N * K < ((int64_t)1 << 31) &&
+          (int64_t)M * K * 2 < ((int64_t)1 << 31)))
+        return false;
+    return M <= 1 || (M <= 2 && K <= 5120);
+}
+
 template <bool FP8, bool SWIGLU>
 hipError_t dispatch(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
                     int64_t ldy, int M, int N, int K, bool wide, hipStream_t stream) {
-    // Raw-buffer kernels take 32-bit byte offsets.
-    const bool ring = FP8 && wide && K <= kRingMaxK && (int64_t)N * K < ((int64_t)1 << 31) &&
-                      (int64_t)M * K * 2 < ((int64_t)1 << 31);
-    if (ring) {
+    if (ring_path(FP8, wide, M, N, K)) {
         const auto* codes = static_cast<const uint8_t*>(w);
         if (M <= 1) return ring_fp8<1, SWIGLU>(x, codes, scales, S, y, ldy, M, N, K, stream);
-        if (M <= 2 && K <= 5120) return ring_fp8<2, SWIGLU>(x, codes, scales, S, y, ldy, M, N, K, stream);
+        return ring_fp8<2, SWIGLU>(x, codes, scales, S, y, ldy, M, N, K, stream);
     }
     if (M <= 1) return general<1, 4, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
     if (M <= 2) return general<2, 4, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
@@ -73,7 +79,48 @@ hipError_t dispatch(const uint16_t* x, const void* w, const float* scales, int S
     return general<8, 2, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
 }
 
+// The ring kernel of ring_fp8<MR, false> with the candidate epilogue (the
+// same instantiation parameters, so the same per-row totals).
+template <int MR>
+hipError_t ring_cand(const uint16_t* x, const uint8_t* w, const float* scales, int S, int M, int N, int K,
+                     uint32_t* part, uint32_t* counters, int64_t& chunks, hipStream_t stream) {
+    using namespace gemv;
+    if (K <= 4096) {
+        chunks = ring_cand_blocks<MR, 1, 4, kNT>(N);
+        return launch_ring_cand<MR, 1, 4, kNT>(x, w, scales, S, M, N, K, part, counters, stream);
+    }
+    if (K <= 5120) {
+        chunks = ring_cand_blocks<MR, 2, 5, kNT>(N);
+        return launch_ring_cand<MR, 2, 5, kNT>(x, w, scales, S, M, N, K, part, counters, stream);
+    }
+    chunks = ring_cand_blocks<MR, 1, 9, kNT>(N);
+    return launch_ring_cand<MR, 1, 9, kNT>(x, w, scales, S, M, N, K, part, counters, stream);
+}
+
+// Workspace of the candidate form: the workgroup pairs (at most one per 4
+// columns: R = 1, four waves per workgroup), 256-byte aligned, then the
+// finishing launch's slice pairs and arrival counters.
+size_t pairs_bytes(int M, int N) { return ((size_t)M * (size_t)((N + 3) / 4 + 7) * 8 + 255) / 256 * 256; }
+
 }  // namespace
+
+bool gemv_candidates_supported(int M, int N, int K, bool wide) { return ring_path(true, wide, M, N, K); }
+
+size_t gemv_candidates_ws_bytes(int M, int N) {
+    return pairs_bytes(M, N) + (size_t)M * kCandSlices * 8 + (size_t)M * 4;
+}
+
+hipError_t launch_gemv_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int S, int M,
+                                  int N, int K, int64_t offset, void* ws, double* out, hipStream_t stream) {
+    auto* part = static_cast<uint32_t*>(ws);
+    auto* slices = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + pairs_bytes(M, N));
+    uint32_t* counters = slices + (size_t)M * kCandSlices * 2;
+    int64_t chunks = 0;
+    const hipError_t e = M <= 1 ? ring_cand<1>(x, codes, scales, S, M, N, K, part, counters, chunks, stream)
+                                : ring_cand<2>(x, codes, scales, S, M, N, K, part, counters, chunks, stream);
+    if (e != hipSuccess) return e;
+    return launch_candidates_finish_sliced(part, M, chunks, slices, counters, offset, out, stream);
+}
 
 hipError_t launch_gemv(const uint16_t* x, const void* w, bool fp8, const float* scales, int S,
                        uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,

@@ -349,15 +349,10 @@ hipError_t launch(const uint16_t* x, const void* w, const float* scales, int S, 
 // share a workgroup only to cut the number of workgroups the dispatcher
 // launches (measured 3-9% faster at the decode shapes with WPG = 4); they do
 // not cooperate.
-template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG>
-__global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
-    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
-    int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t g = (int64_t)blockIdx.x * WPG + threadIdx.x / kWave;
-    const Buffers b = make_buffers(x, w, scales, S, M, N, K, FP8);
-    int64_t rows[R];
-    bool row_ok[R];
+// The R x MR wave-summed totals of row group g (every lane gets them).
+template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX>
+__device__ __forceinline__ void ring_group(const Buffers& b, int S, int M, int N, int K, int64_t g, int lane,
+                                           int64_t (&rows)[R], bool (&row_ok)[R], float (&acc)[R][MR]) {
 #pragma unroll
     for (int r = 0; r < R; ++r) rows[r] = slot_row<R, SWIGLU>(g, r, N, row_ok[r]);
     const int chunks = K >> 4;
@@ -374,7 +369,6 @@ __global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
 #pragma unroll
         for (int m = 0; m < MR; ++m) load_x_buf(xv[j][m], b, m < M ? m : M - 1, K, c << 4, c < chunks);
     }
-    float acc[R][MR];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -398,7 +392,74 @@ __global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[r][m] = wave_sum(acc[r][m]);
+}
+
+template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG>
+__global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
+    int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t g = (int64_t)blockIdx.x * WPG + threadIdx.x / kWave;
+    const Buffers b = make_buffers(x, w, scales, S, M, N, K, FP8);
+    int64_t rows[R];
+    bool row_ok[R];
+    float acc[R][MR];
+    ring_group<MR, R, MAXSTEPS, FP8, SWIGLU, AUX>(b, S, M, N, K, g, lane, rows, row_ok, acc);
     if (lane == 0) store_group<R, MR, SWIGLU>(y, ldy, M, rows, row_ok, acc);
+}
+
+// The ring kernel with the output head's candidate epilogue: no logits are
+// written.  Each workgroup rounds its rows' totals to BF16 (the logits
+// fp8lin_linear would store) and writes, per activation row m, the best
+// {value bits, column} of its WPG * R columns to one of the row's
+// 8 * ceil(gridDim.x / 8) pair slots under the candidate order (larger value,
+// then smaller column; NaN as +inf).  Workgroup b writes slot
+// (b % 8) * ceil(gridDim.x / 8) + b / 8; the finishing launch skips the slots
+// no workgroup writes.  A finishing launch reduces the pairs of a row; its
+// per-row arrival counters are cleared here (workgroup 0), so they start at
+// zero whatever the workspace held.
+template <int MR, int R, int MAXSTEPS, int AUX, int WPG>
+__global__ __launch_bounds__(64 * WPG) void gemv_ring_cand_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
+    int S, int M, int N, int K, uint32_t* __restrict__ part, uint32_t* __restrict__ counters) {
+    if (blockIdx.x == 0 && (int)threadIdx.x < M) counters[threadIdx.x] = 0;
+    __shared__ float sv[WPG][MR];
+    __shared__ uint32_t sid[WPG][MR];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int64_t g = (int64_t)blockIdx.x * WPG + wave;
+    const Buffers b = make_buffers(x, w, scales, S, M, N, K, true);
+    int64_t rows[R];
+    bool row_ok[R];
+    float acc[R][MR];
+    ring_group<MR, R, MAXSTEPS, true, false, AUX>(b, S, M, N, K, g, lane, rows, row_ok, acc);
+    if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float best = -__builtin_inff();
+            uint32_t id = 0xffffffffu;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (row_ok[r]) pick_bf16(best, id, f32_to_bf16_bits(acc[r][m]), (uint32_t)rows[r]);
+            sv[wave][m] = best;
+            sid[wave][m] = id;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < MR && (int)threadIdx.x < M) {
+        const int m = threadIdx.x;
+        float best = sv[0][m];
+        uint32_t id = sid[0][m];
+#pragma unroll
+        for (int v = 1; v < WPG; ++v) pick(best, id, sv[v][m], sid[v][m]);
+        // Workgroup b runs on XCD b % 8: slot b / 8 of that XCD's contiguous
+        // run of pairs, so a cache line of pairs is written from one L2.
+        const int64_t nb = gridDim.x, per_xcd = (nb + 7) / 8, xcd = blockIdx.x % 8;
+        const int64_t slot = xcd * per_xcd + blockIdx.x / 8;
+        uint32_t* p = part + ((int64_t)m * 8 * per_xcd + slot) * 2;
+        p[0] = __builtin_bit_cast(uint32_t, best);
+        p[1] = id;
+    }
 }
 
 template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG = 4>
@@ -408,6 +469,20 @@ hipError_t launch_ring(const uint16_t* x, const void* w, const float* scales, in
     const int64_t blocks = (groups + WPG - 1) / WPG;
     hipLaunchKernelGGL((gemv_ring_kernel<MR, R, MAXSTEPS, FP8, SWIGLU, AUX, WPG>), dim3((unsigned)blocks),
                        dim3(64 * WPG), 0, stream, x, w, scales, S, y, ldy, M, N, K);
+    return hipGetLastError();
+}
+
+template <int MR, int R, int MAXSTEPS, int AUX, int WPG = 4>
+int64_t ring_cand_blocks(int N) {
+    return ((int64_t)N + (int64_t)R * WPG - 1) / ((int64_t)R * WPG);
+}
+
+template <int MR, int R, int MAXSTEPS, int AUX, int WPG = 4>
+hipError_t launch_ring_cand(const uint16_t* x, const void* w, const float* scales, int S, int M, int N, int K,
+                            uint32_t* part, uint32_t* counters, hipStream_t stream) {
+    const int64_t blocks = ring_cand_blocks<MR, R, MAXSTEPS, AUX, WPG>(N);
+    hipLaunchKernelGGL((gemv_ring_cand_kernel<MR, R, MAXSTEPS, AUX, WPG>), dim3((unsigned)blocks), dim3(64 * WPG), 0,
+                       stream, x, w, scales, S, M, N, K, part, counters);
     return hipGetLastError();
 }
 

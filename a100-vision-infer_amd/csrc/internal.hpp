@@ -71,6 +71,22 @@ hipError_t launch_reduce_rms(const uint16_t* x, const uint16_t* partials, int ra
 // Candidates of logits [M, N] -> out [M, 2] doubles {value, id + offset};
 // part: M * vocab_chunks(N) {float bits, id} pairs.
 int64_t vocab_chunks(int64_t N);
+// Per row m, the best pair of the `chunks` workgroups of the GEMV candidate
+// kernel (8 XCD runs of ceil(chunks / 8) slots per row) as out[2m] = value,
+// out[2m + 1] = column + offset (epilogue.hip): kCandSlices workgroups per row
+// each reduce a slice into slices[(m * kCandSlices + s) * 2], and the last to
+// arrive (per-row counters[m], zero at launch) reduces the slices.
+constexpr int kCandSlices = 16;
+hipError_t launch_candidates_finish_sliced(const uint32_t* part, int M, int64_t chunks, uint32_t* slices,
+                                           uint32_t* counters, int64_t offset, double* out, hipStream_t stream);
+// The output head's GEMV with the candidate epilogue (gemv.hip): for the calls
+// where fp8lin_linear runs the ring kernel (gemv_candidates_supported), the
+// candidates of its logits without writing them, in a workspace of
+// gemv_candidates_ws_bytes(M, N) (16-byte aligned; no cleared bytes needed).
+bool gemv_candidates_supported(int M, int N, int K, bool wide);
+size_t gemv_candidates_ws_bytes(int M, int N);
+hipError_t launch_gemv_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int S, int M,
+                                  int N, int K, int64_t offset, void* ws, double* out, hipStream_t stream);
 hipError_t launch_vocab_candidates(const uint16_t* logits, int M, int N, int64_t offset, uint32_t* part,
                                    double* out, hipStream_t stream);
 hipError_t launch_merge_candidates(const double* gathered, int ranks, int64_t rows, int64_t* out,

@@ -29,10 +29,14 @@ METRIC = "FP8 GEMV HBM GB/s (% peak) at M=1; prefill GEMM TFLOP/s (% MFMA peak)"
 # (`bench.py --calibrate`).  Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 92_912_640
 # MFMA busy fraction of the prefill kernel over its whole dispatch (M=4096
-# gate/up+SwiGLU): SQ_VALU_MFMA_BUSY_CYCLES summed over the SIMDs, divided by
-# GRBM_GUI_ACTIVE x SIMDs (rocprofv3's MfmaUtil), one --pmc pass.
-PREFILL_MFMA_BUSY = None
-PREFILL_MFMA_BUSY_SOURCE = "not measured"
+# gate/up+SwiGLU), one --pmc pass: SQ_VALU_MFMA_BUSY_CYCLES summed over the
+# 1024 SIMDs, per SIMD, over the dispatch's cycles.  GRBM_GUI_ACTIVE comes back
+# summed over the 8 XCDs (8 x the dispatch's cycles at the shader clock), so
+# rocprofv3's own MfmaUtil formula reads 8x low on this part.  Re-measure when
+# the kernel changes.
+PREFILL_MFMA_BUSY = 0.736
+PREFILL_MFMA_BUSY_SOURCE = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE: 715.65e6 busy cycles "
+                            "/ 1024 SIMDs over GRBM_GUI_ACTIVE / 8 XCDs = 0.95e6 cycles (1.61 GHz)")
 SHAPES = [("gate_up", 17408, 5120), ("down", 5120, 8704), ("qkv_gate", 7168, 5120)]
 
 
@@ -54,6 +58,8 @@ def parse():
     p.add_argument("--sections", default="gemv,small,prefill,chain,inproj,head,stream,ceiling",
                    help="secondary measurements to run (comma list of gemv, small, prefill, "
                         "chain, inproj, head, stream, ceiling)")
+    p.add_argument("--prefill-m", default="512,1024,4096",
+                   help="prefill row counts of the prefill section (comma list)")
     p.add_argument("--calibrate", action="store_true",
                    help="also run a 256 MiB device copy (known HBM bytes) for counter scaling")
     return p.parse_args()
@@ -185,7 +191,8 @@ def main():
     extra = {"graph_us_per_step": round(graph_ms * 1e3, 3),
              "graph_GBs": round(step_bytes / (graph_ms * 1e-3) / 1e9, 1)}
     if not args.quick:
-        extra.update(secondary(torch, fp8lin, dev, sets, log, set(args.sections.split(","))))
+        extra.update(secondary(torch, fp8lin, dev, sets, log, set(args.sections.split(",")),
+                               [int(v) for v in args.prefill_m.split(",") if v]))
     if args.calibrate:
         extra.update(calibrate(torch, dev, log))
 
@@ -291,7 +298,7 @@ def graph_timed(torch, fn, sp, reps=20, replays=20):
     return a.elapsed_time(b) / (replays * reps)
 
 
-def secondary(torch, fp8lin, dev, sets, log, sections):
+def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(512, 1024, 4096)):
     """Per-shape and per-path figures through the C ABI with preallocated
     outputs, timed as graph replays of back-to-back launches over the rotated
     weight copies (the host's launch rate stays out of the figures)."""
@@ -309,7 +316,16 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
     # over 32 copies (554 MB) so it too streams from HBM
     cfg1 = [fp8lin.gen_weights(4096, 4096, seed=0, tag=100 + c, device=dev)
             for c in range(32)] if "gemv" in sections else []
-    gemv_cases = [(name, n, k, [ws[name] for ws in sets]) for name, n, k in SHAPES]
+    # Each shape's rotation holds at least 600 MB (the decode step's own copies
+    # plus more), so no per-shape figure is served from the Infinity Cache.
+    rot = {}
+    if sections & {"gemv", "small"}:
+        for i, (name, n, k) in enumerate(SHAPES):
+            have = [ws[name] for ws in sets]
+            need = -(-600_000_000 // (n * k + 4 * n * ((k + 127) // 128)))
+            rot[name] = have + [fp8lin.gen_weights(n, k, seed=0, tag=500 + 32 * i + c, device=dev)
+                                for c in range(max(0, need - len(have)))]
+    gemv_cases = [(name, n, k, rot.get(name, [])) for name, n, k in SHAPES]
     gemv_cases.append(("cfg1_4096", 4096, 4096, cfg1))
     for name, n, k, copies in (gemv_cases if "gemv" in sections else []):
         x = fp8lin.gen_activations(1, k, seed=0, tag=2, device=dev)
@@ -328,7 +344,7 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
     del cfg1
     # small M (config 3): GEMV and matrix-core paths on the three shapes and
     # the reference benchmark's 8240 x 5120 (in_proj_all, all FP8; 13 copies)
-    small_copies = {name: [ws[name] for ws in sets] for name, _, _ in SHAPES}
+    small_copies = dict(rot)
     if "small" in sections:
         small_copies["in_proj_all"] = [fp8lin.gen_weights(8240, 5120, seed=0, tag=400 + c, device=dev)
                                        for c in range(13)]
@@ -355,11 +371,11 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
                 gbs = algo_bytes(m, n, k) / (ms * 1e-3) / 1e9
                 extra[f"m{m}_{name}_{label}_GBs"] = round(gbs, 1)
                 log(f"M={m} {name} {label}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
-    del small_copies
+    del small_copies, rot
     # prefill GEMM with fused SwiGLU (config 4)
     n, k = 17408, 5120
     c, s = sets[0]["gate_up"]
-    for m in ((512, 1024, 4096) if "prefill" in sections else ()):
+    for m in (prefill_m if "prefill" in sections else ()):
         x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
         y = torch.empty((m, n // 2), dtype=torch.bfloat16, device=dev)
         need = L.fp8lin_linear_swiglu_workspace_bytes(m, n, k)
@@ -376,7 +392,7 @@ def secondary(torch, fp8lin, dev, sets, log, sections):
     # Practical-ceiling reference, not part of the library: the platform's
     # BF16 GEMM (torch.mm -> hipBLASLt) on the same M=4096 shape with plain
     # BF16 weights (no dequantization, no SwiGLU epilogue).
-    if "prefill" in sections:
+    if "prefill" in sections and 4096 in prefill_m:
         m = 4096
         xa = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
         wb = torch.randn(k, n, device=dev, dtype=torch.bfloat16)

@@ -346,8 +346,13 @@ int fp8lin_merge_candidates(const double* gathered, int64_t ranks, int64_t rows,
 /* The head projection and its candidates in one call: out equals
  * fp8lin_vocab_candidates(fp8lin_linear(x, W), offset), the pair of
  * src/speculative.cpp:25-27 (Engine::local_candidates with gpu_candidates).
- * The logits [M, N] and the chunk pairs go to the workspace (the bytes below,
- * 16-byte aligned).  Requirements of fp8lin_linear and fp8lin_vocab_candidates.
+ * Where fp8lin_linear runs its ring GEMV (M <= 2, 16-byte aligned x and
+ * codes, K % 16 == 0 and K <= 9216, K <= 5120 at M = 2) the GEMV's epilogue
+ * emits one {max, column} pair per workgroup and no logits are written
+ * (src/dual_path.cu:37-55 fused into the projection); otherwise the logits
+ * [M, N] and the chunk pairs go to the workspace.  Workspace: the bytes
+ * below, 16-byte aligned, any content.  Requirements of fp8lin_linear and
+ * fp8lin_vocab_candidates.
  */
 size_t fp8lin_linear_candidates_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const float* scales,
@@ -378,8 +383,10 @@ int fp8lin_linear_candidates_static(const uint16_t* x, const uint8_t* codes, con
  * Engine::local_candidates with gpu_candidates (src/speculative.cpp:25-27).
  * out equals fp8lin_vocab_candidates of fp8lin_engine_linear's output for
  * the same options (so rows 2..8 take the small-M path when the options
- * select it).  Workspace: the bytes below (the logits, the candidate pairs
- * and the branch's own workspace), 16-byte aligned.
+ * select it).  On the FP8 GEMV branch without a bias this is
+ * fp8lin_linear_candidates (no logits written).  Workspace: the bytes below
+ * (the logits, the candidate pairs and the branch's own workspace), 16-byte
+ * aligned.
  */
 size_t fp8lin_engine_linear_candidates_workspace_bytes(const fp8lin_linear_options* options,
                                                        const fp8lin_weight* weight, int64_t rows);

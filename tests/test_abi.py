@@ -144,10 +144,17 @@ def test_epilogue_validation(fp8lin):
 
 def test_linear_candidates_validation(fp8lin):
     L = fp8lin.lib()
-    # the BF16 logits [M, N] padded to 256 bytes, then one pair per chunk
-    assert L.fp8lin_linear_candidates_workspace_bytes(1, 1000, 256) == 2048 + 8
-    assert L.fp8lin_linear_candidates_workspace_bytes(16, 1000, 256) == 32000 + 16 * 8
-    assert L.fp8lin_linear_candidates_workspace_bytes(2, 75968, 5120) == 303872 + 2 * 38 * 8
+    # The larger of the two candidate forms: the BF16 logits [M, N] padded to
+    # 256 bytes, then one pair per 2048-column chunk; or, at M <= 2 (the GEMV
+    # epilogue form), the workgroup pairs, at most one per 4 columns in 8 XCD
+    # runs, padded to 256 bytes, then 16 slice pairs and a counter per row.
+    def want(m, n):
+        two_stage = (m * n * 2 + 255) // 256 * 256 + m * ((n + 2047) // 2048) * 8
+        gemv = (m * ((n + 3) // 4 + 7) * 8 + 255) // 256 * 256 + m * 16 * 8 + m * 4
+        return max(two_stage, gemv) if m <= 2 else two_stage
+    assert L.fp8lin_linear_candidates_workspace_bytes(1, 1000, 256) == want(1, 1000) == 2304 + 132
+    assert L.fp8lin_linear_candidates_workspace_bytes(16, 1000, 256) == want(16, 1000) == 32000 + 16 * 8
+    assert L.fp8lin_linear_candidates_workspace_bytes(2, 75968, 5120) == want(2, 75968) == 303872 + 2 * 38 * 8
     assert L.fp8lin_linear_candidates_workspace_bytes(0, 1000, 256) == 0
     ws = L.fp8lin_linear_candidates_workspace_bytes(2, 1000, 256)
     assert L.fp8lin_linear_candidates(P, P, P, 1, 2, 1000, 256, 0, P, P, ws - 1, None) == 4

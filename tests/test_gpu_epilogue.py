@@ -262,11 +262,13 @@ def test_linear_candidates_vs_oracle(fp8lin, gpu, oracle):
         assert lf[r].max() - lf[r, i] <= abs(lf[r].max()) * 2 ** -7
 
 
-def test_linear_candidates_ties_and_nan(fp8lin, gpu, oracle):
+@pytest.mark.parametrize("m", [2, 3])
+def test_linear_candidates_ties_and_nan(fp8lin, gpu, oracle, m):
     """Equal weight rows give exactly tied logits: the smallest row id wins,
     across row groups and across activation rows; a NaN scale makes its row
-    +inf, which the merge rejects."""
-    m, n, k = 3, 1030, 512
+    +inf, which the merge rejects.  M = 2 takes the GEMV's candidate
+    epilogue (ties across workgroups), M = 3 the two-stage kernels."""
+    n, k = 1030, 512
     rng = np.random.default_rng(12)
     codes_np = (rng.integers(0, 127, (n, k)) | (rng.integers(0, 2, (n, k)) << 7)).astype(np.uint8)
     codes_np[[5, 6, 700, 1029]] = codes_np[900]
