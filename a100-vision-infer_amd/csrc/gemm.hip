@@ -100,6 +100,20 @@ bool fp8_kernel_ok(const uint16_t* x, const void* w, int S, int64_t ldy, int M, 
     return gemm_fp8::supported(x, w, S, ldy, M, N, K);
 }
 
+// A few weight rows (N <= kSkinnyRows, as the GDN in_proj_all group's 48 BF16
+// rows): 256x256 tiles would run M/256 workgroups, so the GEMV's prefill form
+// takes them (8 activation rows per workgroup row, K split over 4 waves).
+// N counts weight rows in both forms, so the fused SwiGLU GEMM and the plain
+// GEMM of one weight take the same kernel (and give the same sums).
+bool skinny(int M, int N, bool /*swiglu*/) { return M > 8 && N <= kSkinnyRows; }
+
+hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
+                         int M, int N, int K, bool swiglu, hipStream_t stream) {
+    const bool wide = K % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(w) % 16 == 0;
+    return launch_gemv_rows(x, w, scales != nullptr, scales, S, y, ldy, M, N, K, wide, swiglu, stream);
+}
+
 }  // namespace
 
 // Compute units of the current device (cached per device), rounded down to a
@@ -119,12 +133,13 @@ int compute_units() {
 }
 
 size_t gemm_workspace_bytes(int S, int64_t ldy, int M, int N, int K, bool swiglu) {
-    if (!fp8_kernel_ok(nullptr, nullptr, S, ldy, M, N, K)) return 0;
+    if (skinny(M, N, swiglu) || !fp8_kernel_ok(nullptr, nullptr, S, ldy, M, N, K)) return 0;
     return plan_bytes(make_plan(M, N, K, swiglu, compute_units(), true));
 }
 
 hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
                           int M, int N, int K, bool swiglu, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (skinny(M, N, swiglu)) return launch_skinny(x, w, scales, S, y, ldy, M, N, K, swiglu, stream);
     const bool fp8 = scales != nullptr;
     if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
         const uint8_t* codes = static_cast<const uint8_t*>(w);
@@ -141,6 +156,7 @@ hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales,
 
 hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
                        int64_t ldy, int M, int N, int K, bool swiglu, hipStream_t stream) {
+    if (skinny(M, N, swiglu)) return launch_skinny(x, w, scales, S, y, ldy, M, N, K, swiglu, stream);
     const bool fp8 = scales != nullptr;
     if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
         const uint8_t* codes = static_cast<const uint8_t*>(w);

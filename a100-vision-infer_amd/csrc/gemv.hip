@@ -9,18 +9,18 @@
 // v_dot2_f32_bf16.
 //
 // Accumulation order: for K <= 9216 every path sums a row's steps in order
-// inside one wave (the "W = 1" order); above that, four waves split the steps
-// (W = 4).  The choice depends only on K, never on the weight type, on pointer
-// alignment or on which kernel runs, so the byte-load fallback and the
-// BF16-weight (decoded cache) variant give bit-identical results to the
-// 128-bit FP8 path, as the reference's tests require
-// (tests/optimized_test.cpp:11-12, :57-62).
+// inside one wave (the "W = 1" order); above that, and for M > 2 against at
+// most 1024 weight rows, four waves split the steps (W = 4).  The choice
+// depends only on M, N and K, never on the weight type, on pointer alignment
+// or on which kernel runs, so the byte-load fallback and the BF16-weight
+// (decoded cache) variant give bit-identical results to the 128-bit FP8 path,
+// as the reference's tests require (tests/optimized_test.cpp:11-12, :57-62).
 //
-// Kernel choice for the 128-bit FP8 path (measured on MI355X, decode shapes):
-// the unrolled ring kernel with the row group's loads all in flight, four
-// waves per workgroup -- R = 1 rows for K <= 4096, R = 2 for K <= 5120,
-// R = 1 for K <= 9216 (R = 2 for the SwiGLU form, whose rows come in
-// gate/up pairs).
+// Kernel choice for the 128-bit path, FP8 or BF16 weights (measured on
+// MI355X, decode shapes): the unrolled ring kernel with the row group's loads
+// all in flight, four waves per workgroup -- R = 1 rows for K <= 4096, R = 2
+// for K <= 5120, R = 1 for K <= 9216 (R = 2 for the SwiGLU form, whose rows
+// come in gate/up pairs); up to 1024 weight rows, one wave per workgroup.
 #include "gemv_kernel.hpp"
 #include "internal.hpp"
 
@@ -30,21 +30,34 @@ namespace {
 constexpr int kRingMaxK = 9216;  // 9 steps of 1024
 constexpr int kNT = 2;           // non-temporal weight loads (gfx950 cache policy)
 
-template <int MR, bool SWIGLU>
-hipError_t ring_fp8(const uint16_t* x, const uint8_t* w, const float* scales, int S, uint16_t* y,
-                    int64_t ldy, int M, int N, int K, hipStream_t stream) {
+// Up to this many weight rows the ring kernel runs one wave per workgroup
+// and, outside SwiGLU, one row per wave: a few rows then spread over as many
+// CUs as there are rows (the GDN in_proj_all group's 48 BF16 rows took 6 µs
+// on 12 CUs).  R and the waves per workgroup change no result: each row is
+// summed by one wave in step order either way.
+constexpr int kFewRows = 1024;
+
+template <int MR, bool FP8, bool SWIGLU>
+hipError_t ring(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy, int M,
+                int N, int K, hipStream_t stream) {
     using namespace gemv;
+    if (N <= kFewRows) {
+        constexpr int R = SWIGLU ? 2 : 1;
+        if (K <= 4096) return launch_ring<MR, R, 4, FP8, SWIGLU, kNT, 1>(x, w, scales, S, y, ldy, M, N, K, stream);
+        if (K <= 5120) return launch_ring<MR, R, 5, FP8, SWIGLU, kNT, 1>(x, w, scales, S, y, ldy, M, N, K, stream);
+        return launch_ring<MR, R, 9, FP8, SWIGLU, kNT, 1>(x, w, scales, S, y, ldy, M, N, K, stream);
+    }
     if (K <= 4096) {
         if constexpr (SWIGLU)
-            return launch_ring<MR, 2, 4, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
+            return launch_ring<MR, 2, 4, FP8, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
         else
-            return launch_ring<MR, 1, 4, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
+            return launch_ring<MR, 1, 4, FP8, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
     }
-    if (K <= 5120) return launch_ring<MR, 2, 5, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
+    if (K <= 5120) return launch_ring<MR, 2, 5, FP8, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
     if constexpr (SWIGLU)
-        return launch_ring<MR, 2, 9, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
+        return launch_ring<MR, 2, 9, FP8, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
     else
-        return launch_ring<MR, 1, 9, true, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
+        return launch_ring<MR, 1, 9, FP8, SWIGLU, kNT>(x, w, scales, S, y, ldy, M, N, K, stream);
 }
 
 // General kernel with the same W as the ring path for this K.
@@ -52,14 +65,22 @@ template <int MR, int R, bool FP8, bool SWIGLU>
 hipError_t general(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
                    int64_t ldy, int M, int N, int K, bool wide, hipStream_t stream) {
     using namespace gemv;
+    // More than 2 rows against a few weight rows: no ring form exists for
+    // these M, so the 128-bit, byte-load, FP8 and BF16 forms all run this
+    // kernel, and the four-wave step split (one row per workgroup) is free to
+    // choose: 4x the waves on a 48-row group.
+    if (M > 2 && N <= kFewRows) {
+        constexpr int R1 = SWIGLU ? 2 : 1;
+        return launch<MR, R1, 4, FP8, SWIGLU, true>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
+    }
     if (K <= kRingMaxK) return launch<MR, R, 1, FP8, SWIGLU, true>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
     return launch<MR, R, 4, FP8, SWIGLU, true>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
 }
 
-// Whether the 128-bit FP8 path runs the ring kernel (raw-buffer kernels take
+// Whether the 128-bit path runs the ring kernel (raw-buffer kernels take
 // 32-bit byte offsets).
 bool ring_path(bool fp8, bool wide, int M, int N, int K) {
-    if (!(fp8 && wide && K <= kRingMaxK && (int64_t)N * K < ((int64_t)1 << 31) &&
+    if (!(wide && K <= kRingMaxK && (int64_t)N * K * (fp8 ? 1 : 2) < ((int64_t)1 << 31) &&
           (int64_t)M * K * 2 < ((int64_t)1 << 31)))
         return false;
     return M <= 1 || (M <= 2 && K <= 5120);
@@ -69,9 +90,8 @@ template <bool FP8, bool SWIGLU>
 hipError_t dispatch(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
                     int64_t ldy, int M, int N, int K, bool wide, hipStream_t stream) {
     if (ring_path(FP8, wide, M, N, K)) {
-        const auto* codes = static_cast<const uint8_t*>(w);
-        if (M <= 1) return ring_fp8<1, SWIGLU>(x, codes, scales, S, y, ldy, M, N, K, stream);
-        return ring_fp8<2, SWIGLU>(x, codes, scales, S, y, ldy, M, N, K, stream);
+        if (M <= 1) return ring<1, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, stream);
+        return ring<2, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, stream);
     }
     if (M <= 1) return general<1, 4, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
     if (M <= 2) return general<2, 4, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
@@ -79,8 +99,8 @@ hipError_t dispatch(const uint16_t* x, const void* w, const float* scales, int S
     return general<8, 2, FP8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
 }
 
-// The ring kernel of ring_fp8<MR, false> with the candidate epilogue (the
-// same instantiation parameters, so the same per-row totals).
+// The ring kernel with the candidate epilogue (the same per-row totals as
+// ring<MR, true, false>: one wave sums each row in step order).
 template <int MR>
 hipError_t ring_cand(const uint16_t* x, const uint8_t* w, const float* scales, int S, int M, int N, int K,
                      uint32_t* part, uint32_t* counters, int64_t& chunks, hipStream_t stream) {
@@ -120,6 +140,16 @@ hipError_t launch_gemv_candidates(const uint16_t* x, const uint8_t* codes, const
                                 : ring_cand<2>(x, codes, scales, S, M, N, K, part, counters, chunks, stream);
     if (e != hipSuccess) return e;
     return launch_candidates_finish_sliced(part, M, chunks, slices, counters, offset, out, stream);
+}
+
+hipError_t launch_gemv_rows(const uint16_t* x, const void* w, bool fp8, const float* scales, int S, uint16_t* y,
+                            int64_t ldy, int M, int N, int K, bool wide, bool swiglu, hipStream_t stream) {
+    using namespace gemv;
+    if (fp8)
+        return swiglu ? launch<8, 4, 4, true, true, true>(x, w, scales, S, y, ldy, M, N, K, wide, stream)
+                      : launch<8, 4, 4, true, false, true>(x, w, scales, S, y, ldy, M, N, K, wide, stream);
+    return swiglu ? launch<8, 4, 4, false, true, true>(x, w, nullptr, 1, y, ldy, M, N, K, wide, stream)
+                  : launch<8, 4, 4, false, false, true>(x, w, nullptr, 1, y, ldy, M, N, K, wide, stream);
 }
 
 hipError_t launch_gemv(const uint16_t* x, const void* w, bool fp8, const float* scales, int S,

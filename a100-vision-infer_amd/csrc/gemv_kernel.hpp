@@ -244,10 +244,17 @@ __device__ __forceinline__ int group_count(int N, int R, bool swiglu) {
 // per workgroup (even for SWIGLU).  W: waves per workgroup.  NT: non-temporal
 // weight loads.  WIDE: 128-bit loads (K % 16 == 0, 16-byte aligned pointers),
 // else byte loads.
+// gridDim.y > 1: block y takes activation rows [y * MR, y * MR + MR) (the
+// prefill form for a few weight rows).
 template <int MR, int R, int W, bool WIDE, bool FP8, bool SWIGLU, bool NT>
 __global__ __launch_bounds__(64 * W) void gemv_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
     int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
+    if (blockIdx.y) {
+        x += (int64_t)blockIdx.y * MR * K;
+        y += (int64_t)blockIdx.y * MR * ldy;
+        M = min(MR, M - (int)blockIdx.y * MR);
+    }
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int64_t g = blockIdx.x;
@@ -333,7 +340,7 @@ template <int MR, int R, int W, bool FP8, bool SWIGLU, bool NT>
 hipError_t launch(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
                   int64_t ldy, int M, int N, int K, bool wide, hipStream_t stream) {
     const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
-    dim3 grid((unsigned)groups);
+    dim3 grid((unsigned)groups, (unsigned)((M + MR - 1) / MR));
     if (wide)
         hipLaunchKernelGGL((gemv_kernel<MR, R, W, true, FP8, SWIGLU, NT>), grid, dim3(64 * W), 0,
                            stream, x, w, scales, S, y, ldy, M, N, K);

@@ -17,6 +17,13 @@ hipError_t launch_gemv_swiglu(const uint16_t* x, const uint8_t* codes, const flo
                               uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
                               hipStream_t stream);
 
+// Any number of activation rows against a few weight rows (gemv.hip): the
+// GEMV over blocks of 8 activation rows, four waves splitting K (the prefill
+// form for N <= kSkinnyRows, where 256x256 MFMA tiles leave most CUs idle).
+constexpr int kSkinnyRows = 256;
+hipError_t launch_gemv_rows(const uint16_t* x, const void* w, bool fp8, const float* scales, int S, uint16_t* y,
+                            int64_t ldy, int M, int N, int K, bool wide, bool swiglu, hipStream_t stream);
+
 // Compute units of the current device, rounded down to a multiple of the 8
 // XCDs (cached per device): the grid of the persistent kernels (gemm.hip).
 int compute_units();

@@ -248,10 +248,11 @@ def test_engine_splitk_workspace(fp8lin):
     assert ws(17408, 5120, 1024) == 16 * 8 * SLOT        # 272 = 256 + 16: the 16 tail tiles
     assert ws(17408, 5120, 4096) == 64 * 4 * SLOT        # 1088 = 4 * 256 + 64
     assert ws(17408, 5120, 2560) == 0                    # 680 = 2 * 256 + 168: last round over a quarter
-    assert ws(256, 512, 20) == 1 * 2 * SLOT              # K / 256 = 2 caps the splits
-    assert ws(256, 256, 20) == 0                         # one 256-K chunk
-    assert ws(256, 640, 20) == 0                         # K % 256 != 0: general GEMM
+    assert ws(384, 512, 20) == 2 * 2 * SLOT              # K / 256 = 2 caps the splits
+    assert ws(384, 256, 20) == 0                         # one 256-K chunk
+    assert ws(384, 640, 20) == 0                         # K % 256 != 0: general GEMM
     assert ws(7168, 5120, 8) == 0                        # GEMV rows
+    assert ws(256, 5120, 512) == 0                       # 256 weight rows or fewer: the GEMV's prefill form
 
 
 def test_linear_swiglu_workspace(fp8lin):

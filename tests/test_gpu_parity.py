@@ -238,6 +238,33 @@ def test_gemm_bf16(fp8lin, gpu, oracle, m, n, k):
     assert_parity(bits(y), oracle.linear_bf16w(x, w), f"bf16 gemm {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 48, 5120), (9, 24, 5120), (300, 256, 8704), (77, 40, 640),
+                                   (4096, 48, 5120)])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_few_weight_rows_prefill(fp8lin, gpu, oracle, m, n, k, fp8):
+    """256 weight rows or fewer at more than 8 activation rows (the GDN
+    in_proj_all group's 48 BF16 rows at a prefill chunk): the GEMV's prefill
+    form over blocks of 8 activation rows (a ragged last block at 9, 77 and
+    300 rows), against the oracle on every output; the fused SwiGLU form
+    bit-equal to SwiGLU of the plain form."""
+    rng = np.random.default_rng(m + n + k + fp8)
+    x = rand_bf16(rng, (m, k))
+    if fp8:
+        codes = rand_codes(rng, n, k)
+        scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+        c, s = up(codes, gpu), up(scales, gpu)
+        y = fp8lin.fp8_linear(up(x, gpu), c, s)
+        ref = oracle.linear(x, codes, scales)
+        if n % 2 == 0:
+            fused = fp8lin.linear_swiglu(up(x, gpu), c, s, split=False)
+            assert torch.equal(fused, fp8lin.fused_swiglu(y))
+    else:
+        w = rand_bf16(rng, (n, k), 0.05)
+        y = fp8lin.gemm_bf16(up(x, gpu), up(w, gpu))
+        ref = oracle.linear_bf16w(x, w)
+    assert_parity(bits(y), ref, f"few rows {m}x{n}x{k} fp8={fp8}")
+
+
 # ---------------------------------------------------------------------- SwiGLU
 def test_swiglu_standalone(fp8lin, gpu, oracle):
     rng = np.random.default_rng(12)
@@ -348,7 +375,7 @@ def test_gemv_long_k(fp8lin, gpu, oracle, m, k):
 
 
 # ------------------------------------------------------------ split-K GEMM
-@pytest.mark.parametrize("m,n,k", [(300, 1040, 1024), (33, 520, 2560), (17, 256, 8704), (600, 7168, 512),
+@pytest.mark.parametrize("m,n,k", [(300, 1040, 1024), (33, 520, 2560), (17, 384, 8704), (600, 7168, 512),
                                    (512, 7168, 5120), (512, 5120, 8704)])
 def test_engine_splitk_gemm(fp8lin, gpu, oracle, m, n, k):
     """Engine::linear's FP8 GEMM branch (src/engine.cpp:222-224) with few
@@ -377,7 +404,8 @@ def test_engine_splitk_gemm(fp8lin, gpu, oracle, m, n, k):
     assert_parity(got[:, cols[0]:cols[1]], ref[:, cols[0]:cols[1]], f"split-K {m}x{n}x{k}")
     plain = bits(F.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu)))
     assert_parity(got, plain, f"split-K vs unsplit {m}x{n}x{k}", min_exact=0.99)
-    assert (ulp_distance(got, plain) <= 1).mean() >= 0.9999
+    # at most one output in 10^4 (and at least one allowed) beyond 1 ulp
+    assert (ulp_distance(got, plain) > 1).sum() <= max(1, got.size // 10000)
     # too small a workspace is an error, not a silent fallback
     if need:
         y2 = torch.empty((m, n), dtype=torch.bfloat16, device=gpu)
