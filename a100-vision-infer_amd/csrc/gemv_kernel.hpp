@@ -353,11 +353,29 @@ hipError_t launch(const uint16_t* x, const void* w, const float* scales, int S, 
 // ------------------------------------------------------ unrolled ring kernel
 // K <= 1024 * MAXSTEPS, K % 16 == 0.  Each wave owns one row group of R rows;
 // all loads of the row group are issued before the arithmetic.  WPG waves
-// share a workgroup only to cut the number of workgroups the dispatcher
-// launches (measured 3-9% faster at the decode shapes with WPG = 4); they do
-// not cooperate.
+// share a workgroup to cut the number of workgroups the dispatcher launches
+// (measured 3-9% faster at the decode shapes with WPG = 4).  For wide weights
+// (kSharedXRows) they also load the activations once per workgroup: x [M, K]
+// goes to LDS by direct-to-LDS DMA (1 KiB per instruction, spread over the
+// waves, issued before the weight loads), and each wave reads a step's
+// fragments from there when it needs them; otherwise every wave loads its own
+// x fragments, as many bytes as its weights, from L2.  Each wave still owns
+// its rows alone.  ring_lds_bytes() is the dynamic LDS the shared form needs.
+template <int MR, int WPG>
+constexpr int ring_x_dmas(int K) {  // DMAs per wave (the same count in every wave)
+    return (MR * K * 2 / 1024 + 1 + WPG - 1) / WPG;
+}
+template <int MR, int WPG, bool XS>
+size_t ring_lds_bytes(int K) { return XS ? (size_t)ring_x_dmas<MR, WPG>(K) * WPG * 1024 : 0; }
+
+__device__ __forceinline__ void ring_dma16(uint32_t m0v, uint32_t voff, rsrc_t r) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(r)
+                 : "memory", "m0");
+}
+
 // The R x MR wave-summed totals of row group g (every lane gets them).
-template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX>
+// XS: the workgroup's activations through LDS (WPG > 1).
+template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG, bool XS>
 __device__ __forceinline__ void ring_group(const Buffers& b, int S, int M, int N, int K, int64_t g, int lane,
                                            int64_t (&rows)[R], bool (&row_ok)[R], float (&acc)[R][MR]) {
 #pragma unroll
@@ -367,21 +385,73 @@ __device__ __forceinline__ void ring_group(const Buffers& b, int S, int M, int N
 
     Chunk<FP8> ring[MAXSTEPS][R];
     uint32_t xv[MAXSTEPS][MR][8];
+    extern __shared__ __align__(16) uint8_t xs[];  // [M][K] BF16, rows packed
+    static_assert(!XS || WPG > 1, "shared activations need several waves");
+    if constexpr (XS) {
+        // x by DMA: instruction d of wave w moves bytes [1024 (w + WPG d), +1024)
+        // of x (past M*K*2 the buffer returns zeros).
+        const int wave = threadIdx.x / kWave;
+        const int nd = ring_x_dmas<MR, WPG>(K);
+        for (int d = 0; d < nd; ++d) {
+            const uint32_t blk = (uint32_t)(wave + WPG * d);
+            ring_dma16(__builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)xs + blk * 1024u),
+                       blk * 1024u + (uint32_t)lane * 16u, b.x);
+        }
 #pragma unroll
-    for (int j = 0; j < MAXSTEPS; ++j) {
-        const int c = lane + j * kWave;
+        for (int j = 0; j < MAXSTEPS; ++j) {
+            const int c = lane + j * kWave;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            load_chunk_buf<FP8, AUX>(ring[j][r], b, S, rows[r], K, c << 4, row_ok[r] && c < chunks);
+            for (int r = 0; r < R; ++r)
+                load_chunk_buf<FP8, AUX>(ring[j][r], b, S, rows[r], K, c << 4, row_ok[r] && c < chunks);
+        }
+        // this wave's DMAs are older than its 2 R MAXSTEPS weight loads
+        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * R * MAXSTEPS) : "memory");
+        __syncthreads();
+    } else {
 #pragma unroll
-        for (int m = 0; m < MR; ++m) load_x_buf(xv[j][m], b, m < M ? m : M - 1, K, c << 4, c < chunks);
+        for (int j = 0; j < MAXSTEPS; ++j) {
+            const int c = lane + j * kWave;
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                load_chunk_buf<FP8, AUX>(ring[j][r], b, S, rows[r], K, c << 4, row_ok[r] && c < chunks);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) load_x_buf(xv[j][m], b, m < M ? m : M - 1, K, c << 4, c < chunks);
+        }
     }
+    // a step's activation fragments from LDS (XS)
+    auto x_step = [&](int j) __attribute__((always_inline)) {
+        if constexpr (XS) {
+            const int c = lane + j * kWave;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const int mm = m < M ? m : M - 1;
+                u32x4 lo{0u, 0u, 0u, 0u}, hi{0u, 0u, 0u, 0u};
+                if (c < chunks) {
+                    const u32x4* p = reinterpret_cast<const u32x4*>(xs + ((int64_t)mm * K + (c << 4)) * 2);
+                    lo = p[0];
+                    hi = p[1];
+                }
+                xv[j][m][0] = lo.x; xv[j][m][1] = lo.y; xv[j][m][2] = lo.z; xv[j][m][3] = lo.w;
+                xv[j][m][4] = hi.x; xv[j][m][5] = hi.y; xv[j][m][6] = hi.z; xv[j][m][7] = hi.w;
+            }
+        }
+    };
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
 #pragma unroll
     for (int j = 0; j < MAXSTEPS; ++j) {
+        // keep each step's LDS reads in its step (hoisted, all steps'
+        // fragments would be live at once): the previous step's sums are
+        // finished before this step's reads issue
+        if constexpr (XS) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) asm volatile("" : "+v"(acc[r][m])::"memory");
+        }
+        x_step(j);
         // Steps past the end leave acc untouched (a select, not a branch).
         float nxt[R][MR];
 #pragma unroll
@@ -401,7 +471,7 @@ __device__ __forceinline__ void ring_group(const Buffers& b, int S, int M, int N
         for (int m = 0; m < MR; ++m) acc[r][m] = wave_sum(acc[r][m]);
 }
 
-template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG>
+template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG, bool XS>
 __global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
     int S, uint16_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
@@ -411,7 +481,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
     int64_t rows[R];
     bool row_ok[R];
     float acc[R][MR];
-    ring_group<MR, R, MAXSTEPS, FP8, SWIGLU, AUX>(b, S, M, N, K, g, lane, rows, row_ok, acc);
+    ring_group<MR, R, MAXSTEPS, FP8, SWIGLU, AUX, WPG, XS>(b, S, M, N, K, g, lane, rows, row_ok, acc);
     if (lane == 0) store_group<R, MR, SWIGLU>(y, ldy, M, rows, row_ok, acc);
 }
 
@@ -425,7 +495,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
 // no workgroup writes.  A finishing launch reduces the pairs of a row; its
 // per-row arrival counters are cleared here (workgroup 0), so they start at
 // zero whatever the workspace held.
-template <int MR, int R, int MAXSTEPS, int AUX, int WPG>
+template <int MR, int R, int MAXSTEPS, int AUX, int WPG, bool XS>
 __global__ __launch_bounds__(64 * WPG) void gemv_ring_cand_kernel(
     const uint16_t* __restrict__ x, const void* __restrict__ w, const float* __restrict__ scales,
     int S, int M, int N, int K, uint32_t* __restrict__ part, uint32_t* __restrict__ counters) {
@@ -439,7 +509,7 @@ __global__ __launch_bounds__(64 * WPG) void gemv_ring_cand_kernel(
     int64_t rows[R];
     bool row_ok[R];
     float acc[R][MR];
-    ring_group<MR, R, MAXSTEPS, true, false, AUX>(b, S, M, N, K, g, lane, rows, row_ok, acc);
+    ring_group<MR, R, MAXSTEPS, true, false, AUX, WPG, XS>(b, S, M, N, K, g, lane, rows, row_ok, acc);
     if (lane == 0) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
@@ -469,14 +539,31 @@ __global__ __launch_bounds__(64 * WPG) void gemv_ring_cand_kernel(
     }
 }
 
+// Activations through LDS from this many weight rows on (measured at the
+// decode shapes: 75968- and 17408-row weights gain, 5120 and 4096 rows at
+// K = 8704 and 4096 lose to the workgroup barrier).
+constexpr int kSharedXRows = 16384;
+
+template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG, bool XS>
+hipError_t launch_ring_xs(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
+                          int M, int N, int K, hipStream_t stream) {
+    const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
+    const int64_t blocks = (groups + WPG - 1) / WPG;
+    const size_t lds = ring_lds_bytes<MR, WPG, XS>(K);
+    hipLaunchKernelGGL((gemv_ring_kernel<MR, R, MAXSTEPS, FP8, SWIGLU, AUX, WPG, XS>), dim3((unsigned)blocks),
+                       dim3(64 * WPG), lds, stream, x, w, scales, S, y, ldy, M, N, K);
+    return hipGetLastError();
+}
+
 template <int MR, int R, int MAXSTEPS, bool FP8, bool SWIGLU, int AUX, int WPG = 4>
 hipError_t launch_ring(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y,
                        int64_t ldy, int M, int N, int K, hipStream_t stream) {
-    const int64_t groups = SWIGLU ? ((N >> 1) + R / 2 - 1) / (R / 2) : ((int64_t)N + R - 1) / R;
-    const int64_t blocks = (groups + WPG - 1) / WPG;
-    hipLaunchKernelGGL((gemv_ring_kernel<MR, R, MAXSTEPS, FP8, SWIGLU, AUX, WPG>), dim3((unsigned)blocks),
-                       dim3(64 * WPG), 0, stream, x, w, scales, S, y, ldy, M, N, K);
-    return hipGetLastError();
+    if constexpr (WPG > 1) {
+        if (N >= kSharedXRows)
+            return launch_ring_xs<MR, R, MAXSTEPS, FP8, SWIGLU, AUX, WPG, true>(x, w, scales, S, y, ldy, M, N, K,
+                                                                              stream);
+    }
+    return launch_ring_xs<MR, R, MAXSTEPS, FP8, SWIGLU, AUX, WPG, false>(x, w, scales, S, y, ldy, M, N, K, stream);
 }
 
 template <int MR, int R, int MAXSTEPS, int AUX, int WPG = 4>
@@ -484,13 +571,22 @@ int64_t ring_cand_blocks(int N) {
     return ((int64_t)N + (int64_t)R * WPG - 1) / ((int64_t)R * WPG);
 }
 
+template <int MR, int R, int MAXSTEPS, int AUX, int WPG, bool XS>
+hipError_t launch_ring_cand_xs(const uint16_t* x, const void* w, const float* scales, int S, int M, int N, int K,
+                               uint32_t* part, uint32_t* counters, hipStream_t stream) {
+    const int64_t blocks = ring_cand_blocks<MR, R, MAXSTEPS, AUX, WPG>(N);
+    const size_t lds = ring_lds_bytes<MR, WPG, XS>(K);
+    hipLaunchKernelGGL((gemv_ring_cand_kernel<MR, R, MAXSTEPS, AUX, WPG, XS>), dim3((unsigned)blocks),
+                       dim3(64 * WPG), lds, stream, x, w, scales, S, M, N, K, part, counters);
+    return hipGetLastError();
+}
+
 template <int MR, int R, int MAXSTEPS, int AUX, int WPG = 4>
 hipError_t launch_ring_cand(const uint16_t* x, const void* w, const float* scales, int S, int M, int N, int K,
                             uint32_t* part, uint32_t* counters, hipStream_t stream) {
-    const int64_t blocks = ring_cand_blocks<MR, R, MAXSTEPS, AUX, WPG>(N);
-    hipLaunchKernelGGL((gemv_ring_cand_kernel<MR, R, MAXSTEPS, AUX, WPG>), dim3((unsigned)blocks), dim3(64 * WPG), 0,
-                       stream, x, w, scales, S, M, N, K, part, counters);
-    return hipGetLastError();
+    if (N >= kSharedXRows)
+        return launch_ring_cand_xs<MR, R, MAXSTEPS, AUX, WPG, true>(x, w, scales, S, M, N, K, part, counters, stream);
+    return launch_ring_cand_xs<MR, R, MAXSTEPS, AUX, WPG, false>(x, w, scales, S, M, N, K, part, counters, stream);
 }
 
 }  // namespace gemv
