@@ -24,10 +24,10 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 METRIC = "FP8 GEMV HBM GB/s (% peak) at M=1; prefill GEMM TFLOP/s (% MFMA peak)"
 # HBM bytes per launch of the roofline kernel (gate/up GEMV, M=1), from two
-# rocprofv3 --pmc passes: 2.000 x FETCH_SIZE (45 231.5 KiB) + 1.000 x WRITE_SIZE
-# (272.0 KiB); the factors are what the counters read for a 256 MiB device copy
+# rocprofv3 --pmc passes: 2.000 x FETCH_SIZE (44 962.1 KiB) + 1.000 x WRITE_SIZE
+# (68.0 KiB); the factors are what the counters read for a 256 MiB device copy
 # (`bench.py --calibrate`).  Re-measure when the kernel changes.
-GATE_UP_TRAFFIC_BYTES = 92_912_640
+GATE_UP_TRAFFIC_BYTES = 92_152_013
 # MFMA busy fraction of the prefill kernel over its whole dispatch (M=4096
 # gate/up+SwiGLU), one --pmc pass: SQ_VALU_MFMA_BUSY_CYCLES summed over the
 # 1024 SIMDs, per SIMD, over the dispatch's cycles.  GRBM_GUI_ACTIVE comes back
@@ -226,7 +226,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_ring_kernel<1,2,5,fp8> (gate/up 17408x5120, M=1)",
+            "kernel": "gemv_ring_kernel<1,2,5,fp8,x in LDS> (gate/up 17408x5120, M=1)",
             "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
