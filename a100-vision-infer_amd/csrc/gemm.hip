@@ -37,9 +37,11 @@ hipError_t run(const uint16_t* x, const void* w, const float* scales, int S, uin
 //  - fewer tiles than half the CUs (e.g. the prefill QKV-gate and down
 //    projections at M = 512): every tile, into min(G / T, K / 256, 8)
 //    ranges;
-//  - otherwise a last round of at most a quarter of the CUs (M = 1024: 16 of
-//    272 tiles; M = 4096: 64 of 1088): those tiles, into min(G / R, K / 256, 8)
-//    ranges, so the last round covers at least half the CUs.
+//  - otherwise a last round of at most half the CUs (M = 1024: 16 of 272
+//    tiles; M = 4096: 64 of 1088; the M = 512 output head: 82 of 594): those
+//    tiles, into min(G / R, K / 256, 8) ranges.  A last round over more than
+//    half the CUs stays whole: splitting it would not shorten the CUs that
+//    run an unsplit tile.
 gemm_fp8::Plan make_plan(int M, int N, int K, bool swiglu, int G, bool split) {
     using namespace gemm_fp8;
     Plan p;
@@ -58,7 +60,7 @@ gemm_fp8::Plan make_plan(int M, int N, int K, bool swiglu, int G, bool split) {
                 p.rtiles = T;
                 p.splits = s;
             }
-        } else if (T > G && T % G != 0 && 4 * (T % G) <= G) {
+        } else if (T > G && T % G != 0 && 2 * (T % G) <= G) {
             const int R = T % G;
             const int s = std::min(std::min(G / R, chunks), kMaxSplits);
             if (s > 1) {

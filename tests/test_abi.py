@@ -235,7 +235,7 @@ def test_engine_splitk_workspace(fp8lin):
     """FP8 GEMM branch on a 256-CU device: K-split partials (one 256x256 FP32
     slot per split tile and K range) when the tiles number at most half the
     CUs (every tile, min(256 / T, K / 256, 8) ranges) or leave a last round
-    on at most a quarter of them (those tiles, min(256 / R, K / 256, 8))."""
+    on at most half of them (those tiles, min(256 / R, K / 256, 8))."""
     F, O = fp8lin, fp8lin.LinearOptions
 
     def ws(n, k, rows, **kw):
@@ -247,7 +247,9 @@ def test_engine_splitk_workspace(fp8lin):
     assert ws(17408, 5120, 512) == 0                     # 136 tiles: no split
     assert ws(17408, 5120, 1024) == 16 * 8 * SLOT        # 272 = 256 + 16: the 16 tail tiles
     assert ws(17408, 5120, 4096) == 64 * 4 * SLOT        # 1088 = 4 * 256 + 64
-    assert ws(17408, 5120, 2560) == 0                    # 680 = 2 * 256 + 168: last round over a quarter
+    assert ws(17408, 5120, 2560) == 0                    # 680 = 2 * 256 + 168: last round over half
+    assert ws(75968, 5120, 512) == 82 * 3 * SLOT         # output head: 594 = 2 * 256 + 82
+    assert ws(22784, 512, 1024) == 100 * 2 * SLOT        # 356 = 256 + 100, K / 256 = 2
     assert ws(384, 512, 20) == 2 * 2 * SLOT              # K / 256 = 2 caps the splits
     assert ws(384, 256, 20) == 0                         # one 256-K chunk
     assert ws(384, 640, 20) == 0                         # K % 256 != 0: general GEMM

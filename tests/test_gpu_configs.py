@@ -131,6 +131,20 @@ def test_head_m512(fp8lin, gpu, oracle, head):
     tail = (75776, n)
     ref = oracle.linear(xb, c_np, s_np, rows=tail)
     assert_parity(y[:, tail[0]:], ref[:, tail[0]:], "head M=512 column tail")
+    # Through Engine::linear (with a workspace): 594 tiles = 2 rounds of 256
+    # + 82, whose tiles (weight rows 65536..75967 of both row tiles) split K
+    # three ways; only their FP32 summation order differs from fp8_linear.
+    eng = fp8lin.LinearEngine()
+    eng.add("lm_head.weight", codes, scales)
+    ys, path = eng.linear(x, "lm_head", return_path=True)
+    assert path == fp8lin.PATH_FP8_GEMM
+    ys = bits(ys)
+    split = (65536, n)
+    assert np.array_equal(ys[:, :split[0]], y[:, :split[0]])
+    ref = oracle.linear(xb[rows], c_np, s_np, rows=split)
+    assert_parity(ys[rows, split[0]:], ref[:, split[0]:], "head M=512 split tiles")
+    assert_parity(ys, y, "head M=512 split vs unsplit", min_exact=0.99)
+    assert (ulp_distance(ys, y) > 1).sum() <= max(1, ys.size // 10000)
 
 
 @pytest.mark.parametrize("m", [1, 4, 512])
