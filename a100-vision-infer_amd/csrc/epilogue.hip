@@ -583,6 +583,159 @@ __global__ __launch_bounds__(64 * kRopeWaves) void qk_norm_rope_kernel(
     }
 }
 
+// Token-major form of qk_norm_rope_kernel for long inputs: one wave per
+// token takes all of its query and key heads, so the token's cos/sin pairs
+// are computed once per wave and no workgroup barrier is needed.
+//  - Normalisation: a head of D = 8 * LPH values spans LPH lanes (8 values
+//    each), so one 16-byte load per lane covers 64 / LPH heads; up to 8 such
+//    loads (a chunk) are issued before any arithmetic.  The arithmetic is that
+//    of qk_norm_rope_kernel, value for value: lane li of a head adds the
+//    squares of its 8 values in order, the LPH-lane butterfly (xor LPH/2 .. 1)
+//    is that kernel's wave butterfly without the steps that add zeros, then
+//    the same normalisation and weight.  Lanes past the rotary part (li >= R/8)
+//    store their BF16 results; the others leave them in the wave's LDS.
+//  - Rotation: 8 pairs (f, f + R/2) per lane, for all heads of the chunk, from
+//    LDS; rope_finish's arithmetic, with bf16(-x2 * s) = -bf16(x2 * s) (round
+//    to nearest even is symmetric), so bf16(bf16(x1 c) + bf16(-x2 s)) is
+//    computed as bf16(bf16(x1 c) - bf16(x2 s)).
+// Requires the VEC conditions of qk_norm_rope_kernel, D in {64, ..., 512}
+// and R / 16 a power of two (a lane's pairs then have the same f for every
+// head: f = 8 (lane mod R/16) + [0, 8)).
+template <int LPH>
+__global__ __launch_bounds__(256) void qk_norm_rope_token_kernel(
+    const uint16_t* __restrict__ p, int64_t ld, const uint16_t* __restrict__ qw, const uint16_t* __restrict__ kw,
+    const int64_t* __restrict__ pos, uint16_t* __restrict__ q, uint16_t* __restrict__ k, int T, int H, int HK,
+    int R, double log2t, int hs, int ws, float eps, int centered) {
+    constexpr int D = 8 * LPH, HPI = 64 / LPH, G = 8, CH = G * HPI;  // heads per chunk
+    // per wave: the token's cos/sin pairs, then the chunk's rotary values
+    // (CH heads x R BF16, at most 8 KiB since R <= D)
+    __shared__ float2 tab[4][D / 2];
+    __shared__ __align__(16) uint16_t rot_lds[4][CH * D];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= T) return;  // the whole wave: no workgroup barrier follows
+    const int li = lane % LPH, sub = lane / LPH;
+    const int heads = H + HK, groups = (heads + HPI - 1) / HPI;
+    const uint16_t* src = p + (int64_t)t * ld + 8 * li;
+    auto head_dst = [&](int hh) __attribute__((always_inline)) -> uint16_t* {
+        return hh < H ? q + ((int64_t)t * H + hh) * D : k + ((int64_t)t * HK + (hh - H)) * D;
+    };
+    auto load_group = [&](int g) __attribute__((always_inline)) -> u32x4 {
+        const int hh = g * HPI + sub;
+        if (g >= groups || hh >= heads) return u32x4{0, 0, 0, 0};
+        return load_u32x4(src + (hh < H ? (int64_t)hh * 2 * D : (int64_t)H * 2 * D + (int64_t)(hh - H) * D));
+    };
+    u32x4 pre[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) pre[j] = load_group(j);
+    const u32x4 wqv = load_u32x4(qw + 8 * li), wkv = load_u32x4(kw + 8 * li);
+    // the token's table, under the loads' latency (the wave's own LDS writes,
+    // read back by the same wave: a wave-level fence orders them)
+    for (int f = lane; f < R / 2; f += 64) tab[wave][f] = rope_cos_sin(pos, T, t, f, R, log2t, hs, ws);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int r16 = R / 16;  // lanes (8 pairs each) per head in the rotation
+    float co[8], si[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float2 cs = tab[wave][8 * (lane & (r16 - 1)) + e];
+        co[e] = cs.x;
+        si[e] = cs.y;
+    }
+    const float c = centered ? 1.0f : 0.0f;
+    float wq[8], wk[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        wq[2 * e] = bf16_bits_to_f32(wqv[e] & 0xffffu) + c;
+        wq[2 * e + 1] = bf16_bits_to_f32(wqv[e] >> 16) + c;
+        wk[2 * e] = bf16_bits_to_f32(wkv[e] & 0xffffu) + c;
+        wk[2 * e + 1] = bf16_bits_to_f32(wkv[e] >> 16) + c;
+    }
+    const bool rot = li < 2 * r16;
+    uint16_t* rl = rot_lds[wave];
+    for (int g0 = 0; g0 < groups; g0 += G) {
+        // ---- normalisation of the chunk's heads
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int g = g0 + j;
+            if (g >= groups) break;  // uniform over the wave
+            const int hh = g * HPI + sub;
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[2 * e] = bf16_bits_to_f32(pre[j][e] & 0xffffu);
+                v[2 * e + 1] = bf16_bits_to_f32(pre[j][e] >> 16);
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
+#pragma unroll
+            for (int d = LPH / 2; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, kWave);
+            const float inv = rsqrtf(ss / (float)D + eps);
+            const bool is_q = hh < H;
+            uint32_t pk[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                f32x2 n{v[2 * e] * inv, v[2 * e + 1] * inv};
+                if (!centered) {
+                    const uint32_t r = pack_bf16x2(n);
+                    n = f32x2{bf16_bits_to_f32(r & 0xffffu), bf16_bits_to_f32(r >> 16)};
+                }
+                pk[e] = pack_bf16x2(f32x2{n[0] * (is_q ? wq[2 * e] : wk[2 * e]),
+                                          n[1] * (is_q ? wq[2 * e + 1] : wk[2 * e + 1])});
+            }
+            const u32x4 out{pk[0], pk[1], pk[2], pk[3]};
+            if (hh < heads) {
+                if (rot)
+                    *reinterpret_cast<u32x4*>(rl + (j * HPI + sub) * R + 8 * li) = out;
+                else
+                    *reinterpret_cast<u32x4*>(head_dst(hh) + 8 * li) = out;
+            }
+        }
+        // the next chunk's loads before this chunk's rotation
+        const int nheads = min(heads - g0 * HPI, CH);
+        if (g0 + G < groups) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) pre[j] = load_group(g0 + G + j);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // ---- rotation: unit u = (head u / r16, pairs 8 (u mod r16) + [0, 8))
+        for (int u = lane; u < nheads * r16; u += 64) {
+            const int hl = u / r16, fb = 8 * (u & (r16 - 1));
+            uint16_t* base = rl + hl * R + fb;
+            const u32x4 a = *reinterpret_cast<const u32x4*>(base);
+            const u32x4 b = *reinterpret_cast<const u32x4*>(base + R / 2);
+            uint32_t o1[4], o2[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float n1[2], n2[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float x1 = bf16_bits_to_f32(h ? a[e] >> 16 : a[e] & 0xffffu);
+                    const float x2 = bf16_bits_to_f32(h ? b[e] >> 16 : b[e] & 0xffffu);
+                    const float cc = co[2 * e + h], sn = si[2 * e + h];
+                    const uint32_t p1 = pack_bf16x2(f32x2{x1 * cc, x2 * sn});  // bf16(x1 c), bf16(x2 s)
+                    const uint32_t p2 = pack_bf16x2(f32x2{x2 * cc, x1 * sn});  // bf16(x2 c), bf16(x1 s)
+                    n1[h] = bf16_bits_to_f32(p1 & 0xffffu) - bf16_bits_to_f32(p1 >> 16);
+                    n2[h] = bf16_bits_to_f32(p2 & 0xffffu) + bf16_bits_to_f32(p2 >> 16);
+                }
+                o1[e] = pack_bf16x2(f32x2{n1[0], n1[1]});
+                o2[e] = pack_bf16x2(f32x2{n2[0], n2[1]});
+            }
+            uint16_t* dst = head_dst(g0 * HPI + hl) + fb;
+            *reinterpret_cast<u32x4*>(dst) = u32x4{o1[0], o1[1], o1[2], o1[3]};
+            *reinterpret_cast<u32x4*>(dst + R / 2) = u32x4{o2[0], o2[1], o2[2], o2[3]};
+        }
+        // this chunk's LDS reads before the next chunk's writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 }  // namespace
 
 hipError_t launch_rms(const uint16_t* x, const uint16_t* update, const uint16_t* w, uint16_t* residual,
@@ -665,6 +818,12 @@ hipError_t launch_merge_candidates(const double* gathered, int ranks, int64_t ro
 
 // Head groups of 4 per workgroup: all of a token's heads from T = 1024 on
 // (enough workgroups to fill the chip, one table per token), else one.
+// From this many tokens on, the Q/K epilogue runs token-major (one wave per
+// token) where its shape allows (measured at H = 12, HK = 2, D = 256: equal
+// at T = 512, 1.3x faster at 1024, 1.8x at 4096; slower below 512, where
+// T / 4 workgroups leave CUs idle).
+constexpr int kRopeTokenMajor = 512;
+
 int rope_iters(int T, int heads) { return T >= 1024 ? (heads + kRopeWaves - 1) / kRopeWaves : 1; }
 dim3 rope_grid(int T, int heads, int iters) {
     const int per = kRopeWaves * iters;
@@ -695,6 +854,28 @@ hipError_t launch_qk_norm_rope(const uint16_t* p, int64_t ld, const uint16_t* qw
     const int c = centered ? 1 : 0;
     const int iters = rope_iters(T, H + HK);
     const double log2t = std::log2((double)theta);
+    if (vec && T >= kRopeTokenMajor && R % 16 == 0 && ((R / 16) & (R / 16 - 1)) == 0 &&
+        (D == 64 || D == 128 || D == 256 || D == 512)) {
+        const dim3 grid((unsigned)((T + 3) / 4)), block(256);
+        switch (D) {
+            case 64:
+                hipLaunchKernelGGL(qk_norm_rope_token_kernel<8>, grid, block, 0, stream, p, ld, qw, kw, pos, q, k, T,
+                                   H, HK, R, log2t, hs, ws, eps, c);
+                break;
+            case 128:
+                hipLaunchKernelGGL(qk_norm_rope_token_kernel<16>, grid, block, 0, stream, p, ld, qw, kw, pos, q, k,
+                                   T, H, HK, R, log2t, hs, ws, eps, c);
+                break;
+            case 256:
+                hipLaunchKernelGGL(qk_norm_rope_token_kernel<32>, grid, block, 0, stream, p, ld, qw, kw, pos, q, k,
+                                   T, H, HK, R, log2t, hs, ws, eps, c);
+                break;
+            default:
+                hipLaunchKernelGGL(qk_norm_rope_token_kernel<64>, grid, block, 0, stream, p, ld, qw, kw, pos, q, k,
+                                   T, H, HK, R, log2t, hs, ws, eps, c);
+        }
+        return hipGetLastError();
+    }
     if (vec)
         hipLaunchKernelGGL(qk_norm_rope_kernel<true>, rope_grid(T, H + HK, iters), dim3(64 * kRopeWaves), lds,
                            stream, p, ld, qw, kw, pos, q, k, T, H, HK, D, R, log2t, hs, ws, eps, c, iters);

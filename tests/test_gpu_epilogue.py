@@ -411,8 +411,13 @@ QK_CASES = [
     (3, 2, 1, 512, 512, 8),      # 256 pairs: the idle fourth wave still fills its part of the table
     (4, 3, 1, 128, 30, 0),       # odd pair count with 16-byte rows
     (2, 5, 3, 64, 64, 3),        # row stride not a multiple of 8 (scalar path), full rotation
-    (1100, 12, 2, 256, 64, 0),   # long prefill: each workgroup loops over all 14 heads of its token
-    (1030, 5, 3, 100, 30, 3),    # the same loop on the scalar path
+    (1100, 12, 2, 256, 64, 0),   # long prefill: one wave per token, all 14 heads
+    (1030, 5, 3, 100, 30, 3),    # long input on the scalar path: workgroups loop over a token's heads
+    (520, 16, 4, 256, 64, 0),    # one wave per token, 20 heads: two rounds of 8 loads
+    (513, 7, 3, 64, 16, 0),      # 8 heads per load, the second load half past the last head; T % 4 != 0
+    (512, 3, 1, 128, 32, 8),     # 4 heads per load, two rotary lanes per half
+    (516, 2, 2, 512, 512, 0),    # one head per load, full rotation (32 lanes per half)
+    (600, 2, 2, 128, 48, 0),     # long input, R / 16 not a power of two: the head-parallel kernel
 ]
 
 
