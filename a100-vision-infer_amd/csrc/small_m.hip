@@ -289,7 +289,7 @@ hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, 
 // ---- persistent row-range form -------------------------------------------
 //
 // Workgroup b owns rows [b * per, min(N, (b + 1) * per)) and walks them in
-// pieces of 16 rows.  Its 8 waves split K block-wise: wave w owns the 128-K
+// pieces of pr <= 16 rows, as equal as the range allows (33 rows: 3 x 11).  Its 8 waves split K block-wise: wave w owns the 128-K
 // blocks w + 8j, j < NB, of every piece, so its activation fragments (the
 // MFMA A operand of those blocks, 16 VGPRs per block) are loaded once and stay
 // in registers for the whole kernel.  Per step (piece p, own block j) a wave
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
                                                                           const uint8_t* __restrict__ codes,
                                                                           const float* __restrict__ scales,
                                                                           uint16_t* __restrict__ y, int64_t ldy,
-                                                                          int M, int N, int K, int per) {
+                                                                          int M, int N, int K, int per, int pr) {
     constexpr int W = kStreamWaves;
     constexpr int SC = stream_scale_dmas<NB>();
     static_assert(D <= NB, "the prologue matches the steady-state issue order only for D <= NB");
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     const int KB = K >> 7;
     const int r0 = (int)blockIdx.x * per;
     const int r1 = min(N, r0 + per);
-    const int np = r1 > r0 ? (r1 - r0 + 15) >> 4 : 0;
+    const int np = r1 > r0 ? (r1 - r0 + pr - 1) / pr : 0;
     // piece order starts at blockIdx % np, so the short last piece of each
     // range does not come at the same time on every compute unit
     const int rot = np ? (int)blockIdx.x % np : 0;
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     auto piece = [&](int p) __attribute__((always_inline)) -> int {  // first row of piece p
         int q = p + rot;
         if (q >= np) q -= np;
-        return r0 + 16 * q;
+        return r0 + pr * q;
     };
     // Code DMA lanes: instruction q, lane -> row 8q + lane/8, LDS position
     // lane%8 <- 16-byte chunk (lane%8) ^ sw(row) of the block's 128 codes.
@@ -378,7 +378,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int n = base + crow[q];
-            dma16(m0 + q * 1024, ok && n < r1 ? (uint32_t)(n * K + blk * 128) + cvoff[q] : kBufferOob, dw, 0);
+            dma16(m0 + q * 1024, ok && crow[q] < pr && n < r1 ? (uint32_t)(n * K + blk * 128) + cvoff[q] : kBufferOob,
+                  dw, 0);
         }
     };
     // scales of piece p into buffer p % 3 as [j][row]
@@ -389,7 +390,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         for (int i = 0; i < SC; ++i) {
             const int e = 64 * i + lane;
             const int j = e >> 4, n = base + (e & 15), blk = wave + W * j;
-            const bool ok = p < np && j < NB && blk < KB && n < r1;
+            const bool ok = p < np && j < NB && blk < KB && (e & 15) < pr && n < r1;
             dma4(__builtin_amdgcn_readfirstlane(m0 + i * 256), ok ? (uint32_t)((n * KB + blk) * 4) : kBufferOob,
                  ds);
         }
@@ -478,7 +479,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
                 float t = rb[m * 16 + row];
 #pragma unroll
                 for (int w = 1; w < W; ++w) t = t + rb[w * 128 + m * 16 + row];
-                if (m < M && n0 + row < r1) out[m * per + (n0 - r0) + row] = f32_to_bf16_bits(t);
+                if (m < M && row < pr && n0 + row < r1) out[m * per + (n0 - r0) + row] = f32_to_bf16_bits(t);
             }
         }
     }
@@ -502,8 +503,11 @@ hipError_t launch_stream(const uint16_t* x, const uint8_t* codes, const float* s
     if (attr != hipSuccess) return attr;
     const int groups = (N + per - 1) / per;
     const size_t lds = (size_t)stream_lds_fixed<NB, D>() + (size_t)per * M * 2;
+    // pieces of at most 16 rows, as equal as the range allows
+    const int pieces = (per + 15) / 16;
+    const int pr = (per + pieces - 1) / pieces;
     hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kStreamWaves), lds, stream, x, codes, scales, y, ldy, M, N, K,
-                       per);
+                       per, pr);
     return hipGetLastError();
 }
 
@@ -528,13 +532,16 @@ int stream_nb(int K) {
 //
 // The stream kernel serves N >= 32 rows per compute unit (measured on MI355X
 // at M = 2, 4, 8: 17408 x 5120 gate/up 16-18% faster, the 75968-row head
-// 7-21%, the 8240-row in_proj_all 3-10%; at 7168 and 5120 rows the 16-row
-// workgroups stay faster).
+// 7-21%, the 8240-row in_proj_all 5-13%).  At 7168 and 5120 rows (28 and 20
+// per CU) the 16-row workgroups stay faster, also against equal pieces of 14
+// and 10 rows (6-12% slower: fewer code bytes in flight per CU).
+constexpr int kStreamRowsPerCu = 32;
+
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                           int64_t ldy, int M, int N, int K, int /*split*/, hipStream_t stream) {
     const int cus = compute_units();
     const int nb = stream_nb(K);
-    if (nb && N >= 32 * cus && (int64_t)N * K < ((int64_t)1 << 31)) {
+    if (nb && N >= kStreamRowsPerCu * cus && (int64_t)N * K < ((int64_t)1 << 31)) {
         const int per = (N + cus - 1) / cus;
         const int fixed = nb == 4 ? stream_lds_fixed<4, 4>() : nb == 5 ? stream_lds_fixed<5, 5>()
                                                                          : stream_lds_fixed<9, 7>();

@@ -173,12 +173,15 @@ def test_tensor_small_vs_fp64(fp8lin, gpu, oracle, m, k, n):
 
 
 @pytest.mark.parametrize("n,k,m", [(8192, 4096, 2), (8200, 3584, 8), (9000, 8704, 5), (8240, 5120, 3),
-                                   (12000, 4224, 7), (8192, 5120, 8)])
+                                   (12000, 4224, 7), (8192, 5120, 8), (5120, 8704, 8), (7168, 5120, 4),
+                                   (4100, 4096, 3), (4352, 5120, 2)])
 def test_tensor_small_wide(fp8lin, gpu, oracle, n, k, m):
-    """Wide weights (32 or more rows per compute unit) take the persistent
-    row-range kernel: ranges of ceil(N / CUs) rows walked in 16-row pieces,
-    with a short last piece (33 rows: 16 + 16 + 1; 36: 16 + 16 + 4), each K
-    band (4096, 5120, 9216) and a K with one block in the last step (4224).
+    """Weights of 32 or more rows per compute unit take the persistent
+    row-range kernel: ranges of ceil(N / CUs) rows walked in pieces of at
+    most 16 rows, as equal as the range allows (33 rows: 11 + 11 + 11; 36:
+    12 x 3; 47: 16 + 16 + 15; 32: 16 + 16), each K band (4096, 5120, 9216)
+    and a K with one block in the last step (4224); the decode down and
+    QKV-gate shapes and two of 17 rows per CU run the 16-row workgroups.
     Every row against the FP64 oracle; split 1 and 4 bit-equal."""
     rng = np.random.default_rng(n + k + m)
     codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
