@@ -20,7 +20,8 @@
 // MI355X, decode shapes): the unrolled ring kernel with the row group's loads
 // all in flight, four waves per workgroup -- R = 1 rows for K <= 4096, R = 2
 // for K <= 5120, R = 1 for K <= 9216 (R = 2 for the SwiGLU form, whose rows
-// come in gate/up pairs); up to 1024 weight rows, one wave per workgroup.
+// come in gate/up pairs); below 16384 rows with K <= 5120, R = 2 and two
+// waves per workgroup; up to 1024 weight rows, one wave per workgroup.
 #include "gemv_kernel.hpp"
 #include "internal.hpp"
 
@@ -46,6 +47,14 @@ hipError_t ring(const uint16_t* x, const void* w, const float* scales, int S, ui
         if (K <= 4096) return launch_ring<MR, R, 4, FP8, SWIGLU, kNT, 1>(x, w, scales, S, y, ldy, M, N, K, stream);
         if (K <= 5120) return launch_ring<MR, R, 5, FP8, SWIGLU, kNT, 1>(x, w, scales, S, y, ldy, M, N, K, stream);
         return launch_ring<MR, R, 9, FP8, SWIGLU, kNT, 1>(x, w, scales, S, y, ldy, M, N, K, stream);
+    }
+    // Up to kSharedXRows rows with K <= 5120 (the 7168-row QKV-gate, the
+    // 8192-row in_proj_all group, config 1's 4096 rows): two rows per wave and
+    // two waves per workgroup, about 3% faster than one row per wave or
+    // four-wave workgroups at those shapes (graph-replayed medians).
+    if (N < gemv::kSharedXRows && K <= 5120) {
+        if (K <= 4096) return launch_ring<MR, 2, 4, FP8, SWIGLU, kNT, 2>(x, w, scales, S, y, ldy, M, N, K, stream);
+        return launch_ring<MR, 2, 5, FP8, SWIGLU, kNT, 2>(x, w, scales, S, y, ldy, M, N, K, stream);
     }
     if (K <= 4096) {
         if constexpr (SWIGLU)
