@@ -118,9 +118,30 @@ void check_scales(const float* scales, int64_t scale_cols, int64_t K) {
             "Invalid FP8 scales: scale_cols must be 1 or ceil(K/128)");
 }
 
+// Whether fp8lin_linear's 2..8-row call runs the small-M matrix-core kernel
+// instead of the multi-row GEMV.  The reference's fp8_linear sends these rows
+// to its GEMV, one pass over the weights per activation row
+// (src/optimized.cu:62-68), and asks for no particular summation order there:
+// its only bit-equality checks are the shared GEMV's FP8 vs decoded-BF16
+// weights and the vector vs scalar GEMV on an unaligned one-row view
+// (tests/optimized_test.cpp:7-14, :57-62), which stay on the GEMV kernels.
+// The matrix-core kernel reads the weights once for all rows and
+// dequantizes each code once (measured 1.4-2.2x faster than the 4- and
+// 8-row GEMV at the decode shapes).  It takes block scales [N, K/128],
+// K % 128 == 0, 16-byte aligned x and codes and 16 K < 2^31; weights of at
+// most 1024 rows keep the GEMV (16-row workgroups would leave most CUs idle),
+// and so do two rows at K <= 5120, where the two-row ring GEMV is faster.
+bool linear_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t M, int64_t N, int64_t K) {
+    return M >= 2 && M <= 8 && (M > 2 || K > 5120) && N > 1024 && K % 128 == 0 && S == K / 128 &&
+           aligned16(x) && aligned16(codes) && 16 * K < kMaxDim && N * S * 4 < kMaxDim;
+}
+
 void linear_impl(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S,
                  uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
-    if (M <= 8) {
+    if (linear_small_m(x, codes, S, M, N, K)) {
+        check_hip(fp8lin::launch_small_m(x, codes, scales, y, ldy, (int)M, (int)N, (int)K, 1, false, stream),
+                  "fp8 small-M launch");
+    } else if (M <= 8) {
         const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
         check_hip(fp8lin::launch_gemv(x, codes, true, scales, (int)S, y, ldy, (int)M, (int)N, (int)K,
                                       wide, stream),
@@ -130,6 +151,21 @@ void linear_impl(const uint16_t* x, const uint8_t* codes, const float* scales, i
                                       false, stream),
                   "fp8 gemm launch");
     }
+}
+
+// Gate/up + SwiGLU for M <= 8 rows: the kernel fp8lin_linear runs for the
+// same (M, N, K) and pointers, with the SwiGLU epilogue, so the output is
+// fused_swiglu of fp8lin_linear's bit for bit.
+void decode_swiglu(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S, uint16_t* y, int64_t M,
+                   int64_t N, int64_t K, hipStream_t stream) {
+    if (linear_small_m(x, codes, S, M, N, K)) {
+        check_hip(fp8lin::launch_small_m(x, codes, scales, y, N / 2, (int)M, (int)N, (int)K, 1, true, stream),
+                  "fp8 small-M+swiglu launch");
+        return;
+    }
+    const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
+    check_hip(fp8lin::launch_gemv_swiglu(x, codes, scales, (int)S, y, N / 2, (int)M, (int)N, (int)K, wide, stream),
+              "fp8 gemv+swiglu launch");
 }
 
 // fp8lin_linear(x, W) followed by its vocabulary candidates, in `ws`
@@ -180,7 +216,7 @@ void tensor_small_impl(const uint16_t* x, const uint8_t* codes, const float* sca
                   "fp8 small-M fallback gemv launch");
         return;
     }
-    check_hip(fp8lin::launch_small_m(x, codes, scales, y, ldy, (int)M, (int)N, (int)K, split, stream),
+    check_hip(fp8lin::launch_small_m(x, codes, scales, y, ldy, (int)M, (int)N, (int)K, split, false, stream),
               "fp8 small-M launch");
 }
 
@@ -454,10 +490,7 @@ int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* s
         check_scales(scales, scale_cols, K);
         ensure_device();
         if (M <= 8) {
-            const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
-            check_hip(fp8lin::launch_gemv_swiglu(x, codes, scales, (int)scale_cols, y, N / 2, (int)M,
-                                                 (int)N, (int)K, wide, as_stream(stream)),
-                      "fp8 gemv+swiglu launch");
+            decode_swiglu(x, codes, scales, scale_cols, y, M, N, K, as_stream(stream));
         } else {
             check_hip(fp8lin::launch_gemm(x, codes, scales, (int)scale_cols, y, N / 2, (int)M,
                                           (int)N, (int)K, true, as_stream(stream)),
@@ -495,10 +528,7 @@ int fp8lin_linear_swiglu_ws(const uint16_t* x, const uint8_t* codes, const float
         check_workspace(workspace, workspace_bytes, need, "linear+SwiGLU: workspace too small");
         ensure_device();
         if (M <= 8) {
-            const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
-            check_hip(fp8lin::launch_gemv_swiglu(x, codes, scales, (int)scale_cols, y, N / 2, (int)M, (int)N, (int)K,
-                                                 wide, as_stream(stream)),
-                      "fp8 gemv+swiglu launch");
+            decode_swiglu(x, codes, scales, scale_cols, y, M, N, K, as_stream(stream));
         } else {
             check_hip(fp8lin::launch_gemm_ws(x, codes, scales, (int)scale_cols, y, N / 2, (int)M, (int)N, (int)K,
                                              true, need ? workspace : nullptr, need, as_stream(stream)),

@@ -31,8 +31,10 @@ int compute_units();
 // Small-M matrix-core kernel, 2 <= M <= 8, K % 128 == 0, block scales
 // (small_m.hip).  The K partition is the kernel's own, so split 1 and 4 give
 // the same bits; no workspace.  M * K * 2 and 16 * K must be below 2^31.
+// swiglu: N weight rows (gate [0, N/2), up [N/2, N)), y is [M, N/2], bit-equal
+// to fused_swiglu of the plain form's output; also needs N * K / 32 < 2^31.
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales,
-                          uint16_t* y, int64_t ldy, int M, int N, int K, int split,
+                          uint16_t* y, int64_t ldy, int M, int N, int K, int split, bool swiglu,
                           hipStream_t stream);
 
 // MFMA GEMM (gemm.hip).  B is E4M3FN codes (scales != nullptr, dequantized

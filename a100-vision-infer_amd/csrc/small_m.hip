@@ -107,13 +107,20 @@ struct SmallCfg {
 
 // Requirements (checked by the host): 2 <= M <= 8, K % 128 == 0,
 // 32 * K < 2^31.
-template <int W, int D, int NBW, int XA>
+// SW: gate/up + SwiGLU (N weight rows, gate [0, N/2), up [N/2, N); y is
+// [M, N/2]).  Workgroup b then holds gate rows 8b..8b+7 in its slots 0..7
+// and the matching up rows in slots 8..15; a row's sum does not depend on
+// its slot, so the outputs are fused_swiglu of the plain kernel's, bit for
+// bit.  Also requires N * K / 32 < 2^31 (scale offsets over the whole
+// matrix).
+template <int W, int D, int NBW, int XA, bool SW>
 __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restrict__ x,
                                                          const uint8_t* __restrict__ codes,
                                                          const float* __restrict__ scales,
                                                          uint16_t* __restrict__ y, int64_t ldy, int M, int N,
                                                          int K) {
     using C = SmallCfg<W, D, NBW, XA>;
+    static_assert(!SW || C::KSPLIT, "the SwiGLU form pairs the 16 rows of one workgroup");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -122,6 +129,11 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     const int nchunks = (KB + 3) >> 2;
     const int64_t nw = (int64_t)blockIdx.x * C::ROWS + (C::KSPLIT ? 0 : 16 * wave);  // this wave's first row
     const int rows_here = (int)max((int64_t)0, min((int64_t)16, (int64_t)N - nw));
+    // SW: output pairs pb..pb+pairs-1 (gate row pb + r in slot r, up row
+    // half + pb + r in slot 8 + r)
+    const int half = N >> 1;
+    const int64_t pb = (int64_t)blockIdx.x * 8;
+    const int pairs = (int)max((int64_t)0, min((int64_t)8, (int64_t)half - pb));
     const int xbuf = (M + 1) * kRowX;
     const uint32_t o_codes = (uint32_t)(wave * D * 2048);
     const uint32_t o_x = (uint32_t)(W * D * 2048);
@@ -135,8 +147,18 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
         *reinterpret_cast<u32x4*>(lds + o_x + (e >> 6) * xbuf + M * kRowX + (e & 63) * 16) = u32x4{0, 0, 0, 0};
     __syncthreads();
 
-    const i32x4 dw = make_desc(codes + (rows_here ? nw * K : 0), (uint32_t)(rows_here * K));
-    const i32x4 ds = make_desc(scales + (rows_here ? nw * KB : 0), (uint32_t)(rows_here * KB * 4));
+    // Code DMA instruction q fills slots 8q..8q+7 from descriptor dwq[q]:
+    // the workgroup's rows (plain), or its 8 gate rows (q = 0) and 8 up rows
+    // (q = 1).
+    i32x4 dwq[2];
+    if constexpr (SW) {
+        dwq[0] = make_desc(codes + (pairs ? pb * K : 0), (uint32_t)(pairs * K));
+        dwq[1] = make_desc(codes + (pairs ? (half + pb) * K : 0), (uint32_t)(pairs * K));
+    } else {
+        dwq[0] = dwq[1] = make_desc(codes + (rows_here ? nw * K : 0), (uint32_t)(rows_here * K));
+    }
+    const i32x4 ds = SW ? make_desc(scales, (uint32_t)((int64_t)N * KB * 4))
+                        : make_desc(scales + (rows_here ? nw * KB : 0), (uint32_t)(rows_here * KB * 4));
     const i32x4 dx = make_desc(x, (uint32_t)(M * K * 2));
 
     // Own block j of this wave -> global block index.
@@ -150,16 +172,25 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int r = 8 * q + (lane >> 3);
-        cvoff[q] = (uint32_t)(r * K + 16 * ((lane & 7) ^ sw(r)));
+        const int lr = SW ? (lane >> 3) : r;  // row within the descriptor
+        cvoff[q] = (uint32_t)(lr * K + 16 * ((lane & 7) ^ sw(r)));
     }
-    // Scales of chunk c: lane -> row lane/4, block 4c + lane%4 (LDS [row][4]).
-    const uint32_t svoff = (uint32_t)((lane >> 2) * KB * 4 + 4 * (lane & 3));
+    // Scales of chunk c: lane -> slot lane/4, block 4c + lane%4 (LDS [slot][4]).
+    uint32_t svoff = (uint32_t)((lane >> 2) * KB * 4 + 4 * (lane & 3));
+    bool sok = true;
+    if constexpr (SW) {
+        const int r = lane >> 2, pr_ = r & 7;
+        sok = pr_ < pairs;
+        const int64_t n = (r < 8 ? 0 : half) + pb + pr_;
+        svoff = sok ? (uint32_t)(n * KB * 4 + 4 * (lane & 3)) : 0u;
+    }
     auto dma_codes = [&](int j) __attribute__((always_inline)) {
         const int blk = gblk(j);
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + o_codes + (uint32_t)(j % D) * 2048u);
         const bool ok = blk < KB;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) dma16(m0 + q * 1024, ok ? cvoff[q] + (uint32_t)blk * 128u : kBufferOob, dw, 0);
+        for (int q = 0; q < 2; ++q)
+            dma16(m0 + q * 1024, ok ? cvoff[q] + (uint32_t)blk * 128u : kBufferOob, dwq[q], 0);
     };
     auto dma_chunk = [&](int c) __attribute__((always_inline)) {
         const uint32_t xb = lds0 + o_x + (uint32_t)((c % C::XBUFS) * xbuf);
@@ -172,7 +203,7 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
             dma16(__builtin_amdgcn_readfirstlane(xb + (uint32_t)(m < M ? m : M) * kRowX), off, dx, 0);
         }
         const uint32_t sb = lds0 + o_sc + (uint32_t)((c % C::XBUFS) * 256);
-        const bool ok = 4 * c + (lane & 3) < KB;
+        const bool ok = sok && 4 * c + (lane & 3) < KB;
         dma4(__builtin_amdgcn_readfirstlane(sb), ok ? svoff + (uint32_t)(16 * c) : kBufferOob, ds);
     };
 
@@ -262,7 +293,21 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
 #pragma unroll
         for (int i = 0; i < 4; ++i) total[i] = acc[i];
     }
-    if (row < rows_here) {
+    if constexpr (SW) {
+        // slot row + 8 holds the up row of slot row's gate row
+        float up[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) up[i] = __shfl_down(total[i], 8, kWave);
+        if (row < 8 && row < pairs) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 4 * g + i;
+                if (m < M)
+                    y[(int64_t)m * ldy + pb + row] =
+                        swiglu_bf16_bits(f32_to_bf16_bits(total[i]), f32_to_bf16_bits(up[i]));
+            }
+        }
+    } else if (row < rows_here) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 4 * g + i;
@@ -271,16 +316,16 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     }
 }
 
-template <int W, int D, int NBW, int XA>
+template <int W, int D, int NBW, int XA, bool SW>
 hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy, int M,
                   int N, int K, hipStream_t stream) {
     using C = SmallCfg<W, D, NBW, XA>;
-    auto kern = small_m_kernel<W, D, NBW, XA>;
+    auto kern = small_m_kernel<W, D, NBW, XA, SW>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        (int)C::lds(kMaxM));
     if (attr != hipSuccess) return attr;
-    const int groups = (N + C::ROWS - 1) / C::ROWS;
+    const int groups = SW ? (N / 2 + 7) / 8 : (N + C::ROWS - 1) / C::ROWS;
     const size_t lds = C::lds(M);
     hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * W), lds, stream, x, codes, scales, y, ldy, M, N, K);
     return hipGetLastError();
@@ -325,7 +370,12 @@ constexpr int floordiv(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / 
 // Requirements (checked by the host): 1 <= M <= 8, K % 128 == 0,
 // 8 * (NB - 1) < K / 128 <= 8 * NB, N * K < 2^31, per * M * 2 bytes of LDS
 // beyond stream_lds_fixed.
-template <int NB, int D>
+// SW: gate/up + SwiGLU (N weight rows, gate [0, N/2), up [N/2, N); y is
+// [M, N/2]).  The units of the ranges and pieces are then output pairs: a
+// piece of pr <= 8 pairs holds its gate rows in slots 0..pr-1 and their up
+// rows in slots 8..8+pr-1.  A row's sum does not depend on its slot or
+// piece, so the outputs are fused_swiglu of the plain kernel's, bit for bit.
+template <int NB, int D, bool SW>
 __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const uint16_t* __restrict__ x,
                                                                           const uint8_t* __restrict__ codes,
                                                                           const float* __restrict__ scales,
@@ -339,8 +389,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const int KB = K >> 7;
+    const int half = N >> 1;
+    const int units = SW ? half : N;  // rows, or output pairs
     const int r0 = (int)blockIdx.x * per;
-    const int r1 = min(N, r0 + per);
+    const int r1 = min(units, r0 + per);
     const int np = r1 > r0 ? (r1 - r0 + pr - 1) / pr : 0;
     // piece order starts at blockIdx % np, so the short last piece of each
     // range does not come at the same time on every compute unit
@@ -354,7 +406,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     const i32x4 ds = make_desc(scales, (uint32_t)((int64_t)N * KB * 4));
     const i32x4 dx = make_desc(x, (uint32_t)(M * K * 2));
 
-    auto piece = [&](int p) __attribute__((always_inline)) -> int {  // first row of piece p
+    auto piece = [&](int p) __attribute__((always_inline)) -> int {  // first unit of piece p
         int q = p + rot;
         if (q >= np) q -= np;
         return r0 + pr * q;
@@ -370,6 +422,19 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         cvoff[q] = (uint32_t)(16 * ((lane & 7) ^ sw(r)));
     }
     const int row = lane & 15, g = lane >> 4;
+    // Weight row in slot sr (0..15) of the piece starting at unit base, and
+    // whether it exists.
+    auto slot_row = [&](int base, int sr, bool& ok) __attribute__((always_inline)) -> int {
+        if constexpr (SW) {
+            const int u = base + (sr & 7);
+            ok = (sr & 7) < pr && u < r1;
+            return sr < 8 ? u : half + u;
+        } else {
+            const int n = base + sr;
+            ok = sr < pr && n < r1;
+            return n;
+        }
+    };
     auto issue_codes = [&](int p, int j, int slot) __attribute__((always_inline)) {
         const int blk = wave + W * j;
         const bool ok = p < np && blk < KB;
@@ -377,9 +442,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds0 + o_codes + (uint32_t)slot * 2048u);
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            const int n = base + crow[q];
-            dma16(m0 + q * 1024, ok && crow[q] < pr && n < r1 ? (uint32_t)(n * K + blk * 128) + cvoff[q] : kBufferOob,
-                  dw, 0);
+            bool rok;
+            const int n = slot_row(base, crow[q], rok);
+            dma16(m0 + q * 1024, ok && rok ? (uint32_t)(n * K + blk * 128) + cvoff[q] : kBufferOob, dw, 0);
         }
     };
     // scales of piece p into buffer p % 3 as [j][row]
@@ -389,8 +454,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
 #pragma unroll
         for (int i = 0; i < SC; ++i) {
             const int e = 64 * i + lane;
-            const int j = e >> 4, n = base + (e & 15), blk = wave + W * j;
-            const bool ok = p < np && j < NB && blk < KB && (e & 15) < pr && n < r1;
+            const int j = e >> 4, blk = wave + W * j;
+            bool rok;
+            const int n = slot_row(base, e & 15, rok);
+            const bool ok = p < np && j < NB && blk < KB && rok;
             dma4(__builtin_amdgcn_readfirstlane(m0 + i * 256), ok ? (uint32_t)((n * KB + blk) * 4) : kBufferOob,
                  ds);
         }
@@ -471,7 +538,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         // barrier that ends piece p + 1, after which buffer p & 1 is rewritten.
         gemm_fp8::wait_lgkm<0>();
         barrier();
-        if (wave == (p & (W - 1)) && g < 2) {
+        if (wave == (p & (W - 1)) && g < 2 && (!SW || row < 8)) {
             const int n0 = piece(p);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -479,7 +546,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
                 float t = rb[m * 16 + row];
 #pragma unroll
                 for (int w = 1; w < W; ++w) t = t + rb[w * 128 + m * 16 + row];
-                if (m < M && row < pr && n0 + row < r1) out[m * per + (n0 - r0) + row] = f32_to_bf16_bits(t);
+                uint16_t v = f32_to_bf16_bits(t);
+                if constexpr (SW) {
+                    // the up row of this pair sits in slot row + 8
+                    float u = rb[m * 16 + row + 8];
+#pragma unroll
+                    for (int w = 1; w < W; ++w) u = u + rb[w * 128 + m * 16 + row + 8];
+                    v = swiglu_bf16_bits(v, f32_to_bf16_bits(u));
+                }
+                if (m < M && row < pr && n0 + row < r1) out[m * per + (n0 - r0) + row] = v;
             }
         }
     }
@@ -494,17 +569,20 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     }
 }
 
-template <int NB, int D>
+// per: rows (pairs for SW) of each workgroup's range.
+template <int NB, int D, bool SW>
 hipError_t launch_stream(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy,
                          int M, int N, int K, int per, hipStream_t stream) {
-    auto kern = small_m_stream_kernel<NB, D>;
+    auto kern = small_m_stream_kernel<NB, D, SW>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     if (attr != hipSuccess) return attr;
-    const int groups = (N + per - 1) / per;
+    const int units = SW ? N / 2 : N;
+    const int groups = (units + per - 1) / per;
     const size_t lds = (size_t)stream_lds_fixed<NB, D>() + (size_t)per * M * 2;
-    // pieces of at most 16 rows, as equal as the range allows
-    const int pieces = (per + 15) / 16;
+    // pieces of at most 16 rows (8 pairs), as equal as the range allows
+    const int cap = SW ? 8 : 16;
+    const int pieces = (per + cap - 1) / cap;
     const int pr = (per + pieces - 1) / pieces;
     hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kStreamWaves), lds, stream, x, codes, scales, y, ldy, M, N, K,
                        per, pr);
@@ -537,22 +615,35 @@ int stream_nb(int K) {
 // and 10 rows (6-12% slower: fewer code bytes in flight per CU).
 constexpr int kStreamRowsPerCu = 32;
 
+// The kernel is chosen from the weight geometry alone, the same for the plain
+// and the SwiGLU form, so the SwiGLU outputs are those of the plain form's
+// sums.
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
-                          int64_t ldy, int M, int N, int K, int /*split*/, hipStream_t stream) {
+                          int64_t ldy, int M, int N, int K, int /*split*/, bool swiglu, hipStream_t stream) {
     const int cus = compute_units();
     const int nb = stream_nb(K);
     if (nb && N >= kStreamRowsPerCu * cus && (int64_t)N * K < ((int64_t)1 << 31)) {
-        const int per = (N + cus - 1) / cus;
+        const int per_rows = (N + cus - 1) / cus;
         const int fixed = nb == 4 ? stream_lds_fixed<4, 4>() : nb == 5 ? stream_lds_fixed<5, 5>()
                                                                          : stream_lds_fixed<9, 7>();
-        if ((int64_t)fixed + (int64_t)per * M * 2 <= kMaxLds) {
-            if (nb == 4) return launch_stream<4, 4>(x, codes, scales, y, ldy, M, N, K, per, stream);
-            if (nb == 5) return launch_stream<5, 5>(x, codes, scales, y, ldy, M, N, K, per, stream);
-            return launch_stream<9, 7>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        if ((int64_t)fixed + (int64_t)per_rows * M * 2 <= kMaxLds) {
+            if (swiglu) {
+                const int per = (N / 2 + cus - 1) / cus;
+                if (nb == 4) return launch_stream<4, 4, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+                if (nb == 5) return launch_stream<5, 5, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+                return launch_stream<9, 7, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+            }
+            if (nb == 4) return launch_stream<4, 4, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
+            if (nb == 5) return launch_stream<5, 5, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
+            return launch_stream<9, 7, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
         }
     }
-    if (M <= 4) return launch<4, 4, 1, 2>(x, codes, scales, y, ldy, M, N, K, stream);
-    return launch<4, 4, 1, 3>(x, codes, scales, y, ldy, M, N, K, stream);
+    if (swiglu) {
+        if (M <= 4) return launch<4, 4, 1, 2, true>(x, codes, scales, y, ldy, M, N, K, stream);
+        return launch<4, 4, 1, 3, true>(x, codes, scales, y, ldy, M, N, K, stream);
+    }
+    if (M <= 4) return launch<4, 4, 1, 2, false>(x, codes, scales, y, ldy, M, N, K, stream);
+    return launch<4, 4, 1, 3, false>(x, codes, scales, y, ldy, M, N, K, stream);
 }
 
 }  // namespace fp8lin

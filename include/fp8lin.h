@@ -72,9 +72,16 @@ int fp8lin_decode(const uint8_t* codes, const float* scales, int64_t scale_cols,
  * `at::Tensor fp8_linear(at::Tensor x, at::Tensor codes, at::Tensor scales,
  *                        bool vector_gemv=false)`
  * (include/avi/ops.h:18, src/optimized.cu:61-70).  M <= 8 runs the decode
- * GEMV (wide 128-bit loads when vector_gemv is set and K, x and codes are
- * 16-byte aligned, otherwise byte loads with bit-identical results); M > 8
- * runs the MFMA GEMM that dequantizes FP8 tiles to BF16 in LDS.
+ * GEMV (128-bit loads when K, x and codes are 16-byte aligned, otherwise
+ * byte loads with bit-identical results; vector_gemv changes nothing), except
+ * that 3..8 rows (2 rows at K > 5120) against more than 1024 weight rows with
+ * block scales, K % 128 == 0 and 16-byte aligned x and codes run the small-M
+ * matrix-core kernel of fp8lin_tensor_small (one pass over the weights for
+ * all rows; same parity bar, another FP32 summation order, so such a call and
+ * an unaligned view of the same data may differ in the last bit, which the
+ * reference allows: it checks bit-equality only on one-row views,
+ * tests/optimized_test.cpp:57-62); M > 8 runs the MFMA GEMM that dequantizes
+ * FP8 tiles to BF16 in LDS.
  * Requires M, N, K > 0 and scale_cols in {1, ceil(K/128)}.
  */
 int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales,
@@ -91,8 +98,10 @@ int fp8lin_linear_ld(const uint16_t* x, const uint8_t* codes, const float* scale
 /* ---------------------------------------------------------------------------
  * Fused gate/up projection + SwiGLU: with G = fp8lin_linear(x, W) of shape
  * [M, N] (N even, rows [0, N/2) = gate, [N/2, N) = up, the row concatenation
- * of src/engine.cpp:116,167), y[M, N/2] = fused_swiglu(G) bit for bit.
- * Replaces the pair linear(gate_up) -> fused_swiglu at src/engine.cpp:415.
+ * of src/engine.cpp:116,167), y[M, N/2] = fused_swiglu(G) bit for bit: the
+ * kernel fp8lin_linear picks for the same arguments runs with a SwiGLU
+ * epilogue.  Replaces the pair linear(gate_up) -> fused_swiglu at
+ * src/engine.cpp:415.
  */
 int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* scales,
                          int64_t scale_cols, uint16_t* y, int64_t M, int64_t N, int64_t K,

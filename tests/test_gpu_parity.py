@@ -622,3 +622,36 @@ def test_engine_workspace_under_capture(fp8lin, gpu, oracle):
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"replay {i}"
         assert torch.equal(logits, eng.linear(x, "lm_head")), f"replay {i}"
+
+
+# ------------------------------------- fp8_linear at 2..8 rows on the matrix cores
+@pytest.mark.parametrize("m,n,k", [(3, 2056, 384), (8, 2056, 384), (5, 8208, 4096), (4, 8208, 5120),
+                                   (2, 2064, 5248), (6, 1040, 8704)])
+def test_linear_small_m_rows(fp8lin, gpu, oracle, m, n, k):
+    """fp8_linear with 2..8 rows (3..8, or 2 at K > 5120) against more than
+    1024 weight rows runs the small-M matrix-core kernel: the 16-row
+    workgroups (n = 2056, 2064, 1040: ragged last group and, for SwiGLU, a
+    ragged last group of pairs) or the persistent row-range form (n = 8208:
+    32 rows per CU and more, 17 pairs per range in pieces of 6).  Every output
+    against the FP64 oracle; fp8_tensor_small bit-equal (the same kernel);
+    the fused SwiGLU bit-equal to fused_swiglu(fp8_linear); an unaligned
+    view of x runs the multi-row GEMV, at the bar."""
+    rng = np.random.default_rng(m * 100003 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"small-M rows {m}x{n}x{k}")
+    assert torch.equal(fp8lin.fp8_tensor_small(xg, c, s, 1), y)
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert torch.equal(fp8lin.linear_swiglu(xg, c, s), fused)
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+    flat = torch.empty(m * k + 1, dtype=torch.bfloat16, device=gpu)
+    xu = flat[1:].view(m, k)
+    xu.copy_(xg)
+    assert_parity(bits(fp8lin.fp8_linear(xu, c, s, True)), ref, f"unaligned x {m}x{n}x{k}")
+    assert_parity(bits(fp8lin.linear_swiglu(xu, c, s, split=False)), oracle.swiglu(ref),
+                  f"unaligned x swiglu {m}x{n}x{k}", elementwise=False)
