@@ -869,7 +869,8 @@ int fp8lin_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n, fl
 
 int fp8lin_stream_read(const void* src, size_t bytes, float* sink, fp8lin_stream_t stream) {
     return guarded([&] {
-        require(src && sink && bytes >= 16, FP8LIN_ERR_ARGUMENT, "stream_read: bad arguments");
+        require(src && sink && bytes >= 16 && bytes < ((size_t)1 << 40), FP8LIN_ERR_ARGUMENT,
+                "stream_read: bad arguments");
         require(aligned16(src), FP8LIN_ERR_ARGUMENT, "stream_read: source must be 16-byte aligned");
         ensure_device();
         check_hip(fp8lin::launch_stream_read(src, bytes, sink, as_stream(stream)),

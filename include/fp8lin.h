@@ -421,9 +421,11 @@ int fp8lin_gen_activations(uint64_t seed, uint32_t tag, int64_t M, int64_t K, ui
 int fp8lin_gen_normal(uint64_t seed, uint32_t tag, uint64_t first, int64_t n, float* out,
                       fp8lin_stream_t stream);
 
-/* Streaming-read probe (no reference counterpart): reads `bytes` bytes with
- * 128-bit loads and writes one checksum word per workgroup into sink
- * (>= 4096 floats).  Used to measure the practical HBM read ceiling. */
+/* Streaming-read probe (no reference counterpart): reads `bytes` bytes in
+ * the decode GEMV's access pattern (each wave a contiguous 10 KiB with all
+ * its 128-bit loads in flight) and may write checksum words into sink
+ * (>= 4096 floats).  Used to measure the practical HBM read ceiling;
+ * 16 <= bytes < 2^40. */
 int fp8lin_stream_read(const void* src, size_t bytes, float* sink, fp8lin_stream_t stream);
 
 /* MFMA-ceiling probe (no reference counterpart): one workgroup of 4 waves per
