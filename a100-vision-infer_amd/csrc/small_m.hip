@@ -39,6 +39,7 @@
 // so the work is balanced to a few rows instead of the 16-row workgroup
 // granularity that leaves a partial last round (1088 workgroups over 512
 // slots at the 17408-row gate/up).  See the kernel for its pipeline.
+#include <algorithm>
 #include <utility>
 
 #include "gemm_fp8.hpp"
@@ -107,6 +108,8 @@ struct SmallCfg {
 
 // Requirements (checked by the host): 2 <= M <= 8, K % 128 == 0,
 // 32 * K < 2^31.
+// per (KSPLIT form): rows of each workgroup, 1..16 (pairs for SW, 1..8); a
+// row's sum does not depend on which workgroup or slot holds it.
 // SW: gate/up + SwiGLU (N weight rows, gate [0, N/2), up [N/2, N); y is
 // [M, N/2]).  Workgroup b then holds gate rows 8b..8b+7 in its slots 0..7
 // and the matching up rows in slots 8..15; a row's sum does not depend on
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
                                                          const uint8_t* __restrict__ codes,
                                                          const float* __restrict__ scales,
                                                          uint16_t* __restrict__ y, int64_t ldy, int M, int N,
-                                                         int K) {
+                                                         int K, int per) {
     using C = SmallCfg<W, D, NBW, XA>;
     static_assert(!SW || C::KSPLIT, "the SwiGLU form pairs the 16 rows of one workgroup");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -127,13 +130,14 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const int KB = K >> 7;
     const int nchunks = (KB + 3) >> 2;
-    const int64_t nw = (int64_t)blockIdx.x * C::ROWS + (C::KSPLIT ? 0 : 16 * wave);  // this wave's first row
-    const int rows_here = (int)max((int64_t)0, min((int64_t)16, (int64_t)N - nw));
+    // this wave's first row and its row count
+    const int64_t nw = C::KSPLIT ? (int64_t)blockIdx.x * per : (int64_t)blockIdx.x * C::ROWS + 16 * wave;
+    const int rows_here = (int)max((int64_t)0, min((int64_t)(C::KSPLIT ? per : 16), (int64_t)N - nw));
     // SW: output pairs pb..pb+pairs-1 (gate row pb + r in slot r, up row
     // half + pb + r in slot 8 + r)
     const int half = N >> 1;
-    const int64_t pb = (int64_t)blockIdx.x * 8;
-    const int pairs = (int)max((int64_t)0, min((int64_t)8, (int64_t)half - pb));
+    const int64_t pb = (int64_t)blockIdx.x * per;
+    const int pairs = (int)max((int64_t)0, min((int64_t)per, (int64_t)half - pb));
     const int xbuf = (M + 1) * kRowX;
     const uint32_t o_codes = (uint32_t)(wave * D * 2048);
     const uint32_t o_x = (uint32_t)(W * D * 2048);
@@ -316,18 +320,20 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     }
 }
 
+// per: rows (pairs for SW) of each workgroup.
 template <int W, int D, int NBW, int XA, bool SW>
 hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy, int M,
-                  int N, int K, hipStream_t stream) {
+                  int N, int K, int per, hipStream_t stream) {
     using C = SmallCfg<W, D, NBW, XA>;
     auto kern = small_m_kernel<W, D, NBW, XA, SW>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
                                                        (int)C::lds(kMaxM));
     if (attr != hipSuccess) return attr;
-    const int groups = SW ? (N / 2 + 7) / 8 : (N + C::ROWS - 1) / C::ROWS;
+    static_assert(C::KSPLIT, "rows per workgroup are set at run time only in the K-split form");
+    const int groups = SW ? (N / 2 + per - 1) / per : (N + per - 1) / per;
     const size_t lds = C::lds(M);
-    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * W), lds, stream, x, codes, scales, y, ldy, M, N, K);
+    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * W), lds, stream, x, codes, scales, y, ldy, M, N, K, per);
     return hipGetLastError();
 }
 
@@ -638,12 +644,18 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
             return launch_stream<9, 7, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
         }
     }
+    // Rows per workgroup: about two workgroups per CU, 8..16 rows (4..8
+    // pairs), so every CU streams about the same number of rows in one round
+    // (16-row workgroups left the 5120-row down projection at 1.25 per CU,
+    // a quarter of the CUs streaming a second workgroup alone).
+    const int units = swiglu ? N / 2 : N;
+    const int per = std::clamp((units + 2 * cus - 1) / (2 * cus), swiglu ? 4 : 8, swiglu ? 8 : 16);
     if (swiglu) {
-        if (M <= 4) return launch<4, 4, 1, 2, true>(x, codes, scales, y, ldy, M, N, K, stream);
-        return launch<4, 4, 1, 3, true>(x, codes, scales, y, ldy, M, N, K, stream);
+        if (M <= 4) return launch<4, 4, 1, 2, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        return launch<4, 4, 1, 3, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
     }
-    if (M <= 4) return launch<4, 4, 1, 2, false>(x, codes, scales, y, ldy, M, N, K, stream);
-    return launch<4, 4, 1, 3, false>(x, codes, scales, y, ldy, M, N, K, stream);
+    if (M <= 4) return launch<4, 4, 1, 2, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    return launch<4, 4, 1, 3, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
 }
 
 }  // namespace fp8lin
