@@ -34,9 +34,9 @@ GATE_UP_TRAFFIC_BYTES = 92_152_013
 # summed over the 8 XCDs (8 x the dispatch's cycles at the shader clock), so
 # rocprofv3's own MfmaUtil formula reads 8x low on this part.  Re-measure when
 # the kernel changes.
-PREFILL_MFMA_BUSY = 0.736
-PREFILL_MFMA_BUSY_SOURCE = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE: 715.65e6 busy cycles "
-                            "/ 1024 SIMDs over GRBM_GUI_ACTIVE / 8 XCDs = 0.95e6 cycles (1.61 GHz)")
+PREFILL_MFMA_BUSY = 0.732
+PREFILL_MFMA_BUSY_SOURCE = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE: 715.7e6 busy cycles "
+                            "/ 1024 SIMDs over GRBM_GUI_ACTIVE / 8 XCDs = 0.955e6 cycles (1.60 GHz)")
 SHAPES = [("gate_up", 17408, 5120), ("down", 5120, 8704), ("qkv_gate", 7168, 5120)]
 
 
