@@ -42,10 +42,11 @@ hipError_t run(const uint16_t* x, const void* w, const float* scales, int S, uin
 //    tiles, into min(G / R, K / 256, 8) ranges.  A last round over more than
 //    half the CUs stays whole: splitting it would not shorten the CUs that
 //    run an unsplit tile.
-gemm_fp8::Plan make_plan(int M, int N, int K, bool swiglu, int G, bool split) {
+gemm_fp8::Plan plan_for(int bm, int M, int N, int K, bool swiglu, int G, bool split) {
     using namespace gemm_fp8;
     Plan p;
-    p.mtiles = (M + BM - 1) / BM;
+    p.bm = bm;
+    p.mtiles = (M + bm - 1) / bm;
     p.ntiles = swiglu ? ((N >> 1) + BN / 2 - 1) / (BN / 2) : (N + BN - 1) / BN;
     const int T = p.mtiles * p.ntiles;
     p.full = T;
@@ -76,25 +77,44 @@ gemm_fp8::Plan make_plan(int M, int N, int K, bool swiglu, int G, bool split) {
 }
 
 size_t plan_bytes(const gemm_fp8::Plan& p) {
-    return (size_t)p.rtiles * p.splits * gemm_fp8::kSlotFloats * sizeof(float);
+    return (size_t)p.rtiles * p.splits * p.bm * gemm_fp8::BN * sizeof(float);
+}
+
+// The plan of a launch.  M <= 128 (one tile row) takes 128-row tiles: the
+// same outputs at half the MFMA work of a 256-row tile that is at least half
+// padding.  Above that the 256-row tile stays: measured on MI355X, a 128-row
+// tile costs 0.62 (whole chip) to 0.77 (one partial round) of a 256-row tile
+// (its K loop issues 4 dequant VALU per MFMA instead of 2, with the same
+// per-step waits), so two of them cost more than the one they replace.
+// Both heights give each output the same FP32 sum over a K range.
+gemm_fp8::Plan make_plan(int M, int N, int K, bool swiglu, int G, bool split) {
+    return plan_for(M <= 128 ? 128 : 256, M, N, K, swiglu, G, split);
+}
+
+template <int MT, bool SWIGLU>
+hipError_t run_fp8_mt(const uint16_t* x, const uint8_t* w, const float* scales, int S, uint16_t* y, int64_t ldy,
+                      int M, int N, int K, const gemm_fp8::Plan& plan, int G, float* part, hipStream_t stream) {
+    using namespace gemm_fp8;
+    using Gm = Geo<MT>;
+    auto kern = gemm_fp8_kernel<MT, SWIGLU>;
+    static const hipError_t attr = gemm::allow_lds(reinterpret_cast<const void*>(kern), Gm::LDS_BYTES);
+    if (attr != hipSuccess) return attr;
+    const int grid = std::min(plan.units, G);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), Gm::LDS_BYTES, stream, x, w, scales, S, y, (int)ldy, M, N,
+                       K, plan, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || plan.rtiles == 0) return e;
+    const int64_t threads = (int64_t)plan.rtiles * Gm::BM * (SWIGLU ? 32 : 64);
+    hipLaunchKernelGGL((tail_reduce_kernel<MT, SWIGLU>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       stream, part, plan, M, N, y, ldy);
+    return hipGetLastError();
 }
 
 template <bool SWIGLU>
 hipError_t run_fp8(const uint16_t* x, const uint8_t* w, const float* scales, int S, uint16_t* y, int64_t ldy,
                    int M, int N, int K, const gemm_fp8::Plan& plan, int G, float* part, hipStream_t stream) {
-    using namespace gemm_fp8;
-    auto kern = gemm_fp8_kernel<SWIGLU>;
-    static const hipError_t attr = gemm::allow_lds(reinterpret_cast<const void*>(kern), LDS_BYTES);
-    if (attr != hipSuccess) return attr;
-    const int grid = std::min(plan.units, G);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(THREADS), LDS_BYTES, stream, x, w, scales, S, y, (int)ldy, M, N, K,
-                       plan, part);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || plan.rtiles == 0) return e;
-    const int64_t threads = (int64_t)plan.rtiles * BM * (SWIGLU ? 32 : 64);
-    hipLaunchKernelGGL(tail_reduce_kernel<SWIGLU>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                       part, plan, M, N, y, ldy);
-    return hipGetLastError();
+    return plan.bm == 128 ? run_fp8_mt<4, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, plan, G, part, stream)
+                          : run_fp8_mt<8, SWIGLU>(x, w, scales, S, y, ldy, M, N, K, plan, G, part, stream);
 }
 
 // Shapes and alignments the FP8 kernel takes.

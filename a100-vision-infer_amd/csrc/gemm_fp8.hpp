@@ -4,8 +4,9 @@
 // of src/optimized.cu:32), optionally with the gate/up + SwiGLU epilogue
 // (src/engine.cpp:415).
 //
-// Workgroup: 4 waves, one per SIMD, 256 (M) x 256 (weight rows) tile.  Each
-// wave owns all 256 rows of M and 64 weight rows: 8 x 2 accumulators of
+// Workgroup: 4 waves, one per SIMD, 256 (M) x 256 (weight rows) tile (128 x
+// 256 for M <= 128, see Geo).  Each wave owns all 256 rows of M and 64 weight
+// rows: 8 x 2 accumulators of
 // v_mfma_f32_32x32x16_bf16 held in AGPRs.  Owning the whole M extent makes the
 // dequantization cost per MFMA minimal (every code is converted once per
 // workgroup, 2 VALU per MFMA), and the 64-row width keeps the A-fragment LDS
@@ -43,14 +44,40 @@ namespace gemm_fp8 {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 256, WN = 64, BN = 256, BK = 64;
-constexpr int MT = 8, NT = 2;
+constexpr int WN = 64, BN = 256, BK = 64;
+constexpr int NT = 2;
 constexpr int THREADS = 256;
-constexpr int A_STAGE = BM * 128;               // 32 KiB: 256 rows x 64 BF16
-constexpr int A_BYTES = 3 * A_STAGE;
-constexpr int B_SLOT = WN * 64;                 // 4 KiB: 64 rows x 64 codes
+constexpr int B_SLOT = WN * 64;  // 4 KiB: 64 rows x 64 codes
 constexpr int B_WAVE = 3 * B_SLOT;
-constexpr int LDS_BYTES = A_BYTES + 4 * B_WAVE;  // 144 KiB of the 160 KiB
+
+// The tile's M extent: MT fragments of 32 rows.  MT = 8 (256 rows) is the
+// tile described above; MT = 4 (128 rows) serves launches of M <= 128 rows,
+// where a 256-row tile is at least half padding: the same K loop with half
+// the MFMAs per sub-step, so each code's dequantization (still once per
+// workgroup) costs 4 VALU per MFMA instead of 2.
+template <int MT>
+struct Geo {
+    static_assert(MT == 4 || MT == 8, "tile heights of 128 or 256 rows");
+    static constexpr int BM = 32 * MT;
+    static constexpr int A_STAGE = BM * 128;  // BM rows x 64 BF16
+    static constexpr int A_BYTES = 3 * A_STAGE;
+    static constexpr int LDS_BYTES = A_BYTES + 4 * B_WAVE;  // 144 KiB (MT 8) or 96 KiB (MT 4)
+    static constexpr int SLOT_FLOATS = BM * BN;             // one split partial
+    static constexpr int MFMAS = 2 * MT;                    // per sub-step
+    static constexpr int DQ = 16 / MT;                      // dequant instructions per MFMA
+    // Sub-step-0 slots of the 4 B DMAs (the 2 scale loads of odd steps sit
+    // in slots MT + 1 and MT + 3, after that slot's DMA).
+    static constexpr bool b_dma_at(int m) { return MT >= 8 ? (m >= MT && ((m - MT) & 1) == 0) : m >= MT; }
+    static constexpr int b_dma_index(int m) { return MT >= 8 ? (m - MT) >> 1 : m - MT; }
+    // Vector-memory operations issued after a step's last scale load: the
+    // B DMAs in later slots of sub-step 0 and the MT A DMAs of sub-step 2.
+    static constexpr int VM_AFTER_SCALE = (MT >= 8 ? 2 : 0) + MT;
+    // Sub-step of the 4 code reads of B(kt+2): the last with at least 4
+    // MFMAs after them before the next step's first wait (that DMA is
+    // complete from sub-step 1's wait on).
+    static constexpr int BRAW_SUB = MT >= 8 ? 3 : 2;
+};
+constexpr int kBMMax = Geo<8>::BM;
 
 // Chunk swizzles: A rows hold 8 chunks of 16 B (slot = chunk ^ ga(row)), B
 // rows 4 chunks (slot = chunk ^ gb(row)).  For any 16 consecutive rows read
@@ -117,17 +144,29 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 
 // Waits that also redefine the registers their loads filled (see header).
 template <int N>
-__device__ __forceinline__ void wait_lgkm8(u32x4 (&a)[MT]) {
+__device__ __forceinline__ void wait_lgkm_a(u32x4 (&a)[8]) {
     asm volatile("s_waitcnt lgkmcnt(%8)"
                  : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7])
                  : "i"(N)
                  : "memory");
 }
 template <int N>
-__device__ __forceinline__ void wait_lgkm12(u32x4 (&a)[MT], u32x4 (&b)[NT][2]) {
+__device__ __forceinline__ void wait_lgkm_a(u32x4 (&a)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : "i"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm_ab(u32x4 (&a)[8], u32x4 (&b)[NT][2]) {
     asm volatile("s_waitcnt lgkmcnt(%12)"
                  : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
                    "+v"(b[0][0]), "+v"(b[0][1]), "+v"(b[1][0]), "+v"(b[1][1])
+                 : "i"(N)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm_ab(u32x4 (&a)[4], u32x4 (&b)[NT][2]) {
+    asm volatile("s_waitcnt lgkmcnt(%8)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0][0]), "+v"(b[0][1]), "+v"(b[1][0]),
+                   "+v"(b[1][1])
                  : "i"(N)
                  : "memory");
 }
@@ -148,6 +187,7 @@ __device__ __forceinline__ void wait_vm4(float (&v)[NT], float (&u)[NT]) {
     asm volatile("s_waitcnt vmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(u[0]), "+v"(u[1]) : "i"(N) : "memory");
 }
 
+template <int MT>
 struct State {
     f32x16 acc[MT][NT];
     u32x4 af[2][MT];       // A fragments of two sub-steps
@@ -162,8 +202,8 @@ struct State {
 // sub-step ss), two code words of 4 each:
 //   v_cvt_pk_f32_fp8 lo, hi  ->  4 x v_mul_f32 by the scale  ->  2 x
 //   v_cvt_pk_bf16_f32 (round to nearest even): bf16(decode(c) * s).
-template <int K, int RB, int BD>
-__device__ __forceinline__ void dequant_op(State& st, const float (&sc)[NT]) {
+template <int K, int RB, int BD, int MT>
+__device__ __forceinline__ void dequant_op(State<MT>& st, const float (&sc)[NT]) {
     constexpr int unit = K / 16, r = K % 16;
     constexpr int j = unit / 4, ss = unit % 4;
     constexpr int wi = r / 8, q = r % 8;
@@ -183,9 +223,10 @@ __device__ __forceinline__ void dequant_op(State& st, const float (&sc)[NT]) {
     }
 }
 
+template <int MT>
 struct Ctx {
     i32x4 dx, dw, ds;
-    uint32_t aoff[8];   // A DMA lane offsets (k = 0)
+    uint32_t aoff[MT];  // A DMA lane offsets (k = 0)
     uint32_t boff[4];   // B DMA lane offsets (k = 0)
     uint32_t soff[NT];  // scale row offsets
     uint32_t ard[4];    // A fragment read address per sub-step, stage 0
@@ -212,11 +253,18 @@ struct Ring {
 //   A: read stage kt%3; after the mid-step barrier DMA A(kt+2) into stage
 //      (kt+2)%3; in sub-step 3 read step kt+1's first fragments.
 //   B: DMA B(kt+3) into slot kt%3; dequantize B(kt+1) from braw[(kt+1)&1];
-//      in sub-step 3 read B(kt+2) from slot (kt+2)%3 into braw[kt&1].
+//      in sub-step 3 (2 for 128-row tiles) read B(kt+2) from slot (kt+2)%3 into braw[kt&1].
 //   Scales: odd steps load block (kt+3)/2 into bsc[block&1]; step kt
 //      dequantizes with block (kt+1)/2.
-template <int T>
-__device__ __forceinline__ void kstep(State& st, const Ctx& c, const Ring& rg, int kt) {
+// Per sub-step, slot m (one MFMA, then DQ dequant instructions) also carries:
+//   m < MT: the next sub-step's A fragment m (LDS read);
+//   sub-step 0: the 4 B DMAs (Geo::b_dma_at), and on odd steps the 2 scale
+//     loads in slots MT + 1, MT + 3;
+//   sub-step 2, m >= MT: A DMA m - MT;
+//   sub-step BRAW_SUB, MT <= m < MT + 4: the 4 code reads of B(kt+2).
+template <int MT, int T>
+__device__ __forceinline__ void kstep(State<MT>& st, const Ctx<MT>& c, const Ring& rg, int kt) {
+    using Gm = Geo<MT>;
     constexpr int RB_DQ = (T + 1) & 1, RB_RD = T & 1;
     constexpr int BC = T & 1, BD = BC ^ 1;
     constexpr int SB_DQ = ((T + 1) / 2) & 1;
@@ -239,34 +287,37 @@ __device__ __forceinline__ void kstep(State& st, const Ctx& c, const Ring& rg, i
         ([&]() __attribute__((always_inline)) {
             constexpr int s = S;
             if constexpr (s == 0)
-                wait_lgkm12<0>(st.af[0], st.braw[RB_DQ]);
+                wait_lgkm_ab<0>(st.af[0], st.braw[RB_DQ]);
             else
-                wait_lgkm8<0>(st.af[s & 1]);
+                wait_lgkm_a<0>(st.af[s & 1]);
             [&]<int... M>(std::integer_sequence<int, M...>) __attribute__((always_inline)) {
                 ([&]() __attribute__((always_inline)) {
                     constexpr int m = M;
                     constexpr int i = m >> 1, j = m & 1;
                     mfma(st.acc[i][j], st.af[s & 1][i], st.bf[BC][j][s]);
-                    dequant_op<(s * 16 + m) * 2, RB_DQ, BD>(st, st.bsc[SB_DQ]);
-                    dequant_op<(s * 16 + m) * 2 + 1, RB_DQ, BD>(st, st.bsc[SB_DQ]);
-                    if constexpr (m < 8) {
+                    [&]<int... D>(std::integer_sequence<int, D...>) __attribute__((always_inline)) {
+                        (dequant_op<(s * Gm::MFMAS + m) * Gm::DQ + D, RB_DQ, BD>(st, st.bsc[SB_DQ]), ...);
+                    }(std::make_integer_sequence<int, Gm::DQ>{});
+                    if constexpr (m < MT) {
                         if constexpr (s < 3)
                             ds_read<m * 4096>(st.af[(s + 1) & 1][m], ard[s + 1]);
                         else
                             ds_read<m * 4096>(st.af[0][m], ard[0]);
                     }
-                    if constexpr (s == 0 && m >= 8 && (m & 1) == 0)
-                        dma16(m0b + ((m - 8) >> 1) * 1024, c.boff[(m - 8) >> 1], c.dw, kB);
-                    if constexpr (SLOAD && s == 0 && (m == 9 || m == 11))
-                        buf_load1(st.bsc[SB_LD][(m - 9) >> 1], c.soff[(m - 9) >> 1], c.ds, sS);
-                    if constexpr (s == 2 && m >= 8)
-                        dma16(m0a + (m - 8) * 1024, c.aoff[m - 8], c.dx, kA);
-                    if constexpr (s == 3 && m >= 8 && m < 12) {
-                        constexpr int jj = (m - 8) >> 1, cp = (m - 8) & 1;
+                    if constexpr (s == 0 && Gm::b_dma_at(m)) {
+                        constexpr int g = Gm::b_dma_index(m);
+                        dma16(m0b + g * 1024, c.boff[g], c.dw, kB);
+                    }
+                    if constexpr (SLOAD && s == 0 && (m == MT + 1 || m == MT + 3))
+                        buf_load1(st.bsc[SB_LD][(m - MT - 1) >> 1], c.soff[(m - MT - 1) >> 1], c.ds, sS);
+                    if constexpr (s == 2 && m >= MT)
+                        dma16(m0a + (m - MT) * 1024, c.aoff[m - MT], c.dx, kA);
+                    if constexpr (s == Gm::BRAW_SUB && m >= MT && m < MT + 4) {
+                        constexpr int jj = (m - MT) >> 1, cp = (m - MT) & 1;
                         ds_read<jj * 2048>(st.braw[RB_RD][jj][cp], cp ? brd1 : brd0);
                     }
                 }(), ...);
-            }(std::make_integer_sequence<int, 16>{});
+            }(std::make_integer_sequence<int, Gm::MFMAS>{});
             if constexpr (s == 1) {
                 // A(kt+1), the previous step's last DMA, has landed (issued
                 // after it: this step's 4 B DMA and NS scale loads).
@@ -280,7 +331,7 @@ __device__ __forceinline__ void kstep(State& st, const Ctx& c, const Ring& rg, i
     }(std::make_integer_sequence<int, 4>{});
 }
 
-// Work decomposition.  The output is cut into 256 x 256 tiles (L = 0..T-1,
+// Work decomposition.  The output is cut into BM x 256 tiles (L = 0..T-1,
 // walked GROUP_M tile rows at a time so that tiles running together on one
 // XCD share A and B slices in its L2).  The grid is persistent: G workgroups
 // (one per CU, G a multiple of 8) loop over work units u = bid, bid + G, ...
@@ -291,17 +342,18 @@ __device__ __forceinline__ void kstep(State& st, const Ctx& c, const Ring& rg, i
 //    whose L >= full do nothing);
 //  - units [fpad, fpad + rtiles * splits) cover the tail tiles full..T-1, each
 //    cut into `splits` K ranges (whole 256-K chunks, spread evenly).  Their
-//    FP32 sums go to partial slot r * splits + s (256 x 256 floats each, in
+//    FP32 sums go to partial slot r * splits + s (BM x 256 floats each, in
 //    the tile's own row/column order) and tail_reduce_kernel adds the splits
 //    in order, rounds once and applies the epilogue.
-// The host picks full = T and rtiles = 0 when splitting would not pay (see
-// gemm.hip), so most launches write every tile directly.
+// The host picks the tile height BM (plan.bm) and full = T, rtiles = 0 when
+// splitting would not pay (see gemm.hip), so most launches write every tile
+// directly.
 constexpr int kXcds = 8;
 constexpr int kGroupM = 8;
-constexpr int kSlotFloats = BM * BN;
 constexpr int kMaxSplits = 8;
 
 struct Plan {
+    int bm;              // tile height: 256 or 128 rows of M
     int mtiles, ntiles;  // tile grid (ntiles counts 256-row weight blocks, or 128 output pairs for SwiGLU)
     int full;            // whole tiles
     int fpad;            // full rounded up to a multiple of 8
@@ -366,10 +418,11 @@ __device__ __forceinline__ int64_t weight_row(int nt, int wave, int rr, int N) {
 }
 
 // Buffer descriptors and lane offsets of one unit (its tile and K range).
-template <bool SWIGLU>
-__device__ __forceinline__ void setup(Ctx& c, const Unit& w, const uint16_t* x, const uint8_t* wt, const float* scales,
+template <bool SWIGLU, int MT>
+__device__ __forceinline__ void setup(Ctx<MT>& c, const Unit& w, const uint16_t* x, const uint8_t* wt, const float* scales,
                                       int S, int M, int N, int K, int wave, int lane, uint32_t lds0) {
     const int h = lane >> 5, l32 = lane & 31;
+    constexpr int BM = Geo<MT>::BM, A_BYTES = Geo<MT>::A_BYTES;
     const int m0 = w.mtile * BM;
     const int sbeg = S == 1 ? 0 : w.kbeg / 128;
     // The buffers start at kbeg (rows keep the stride K), so the step offsets
@@ -378,16 +431,16 @@ __device__ __forceinline__ void setup(Ctx& c, const Unit& w, const uint16_t* x, 
     c.dw = make_desc(wt + w.kbeg, (uint32_t)((int64_t)N * K - w.kbeg));
     c.ds = make_desc(scales + sbeg, (uint32_t)((int64_t)N * S * 4 - (int64_t)sbeg * 4));
     c.scol = S == 1 ? 0 : 4;
-    // A DMA instruction ii of wave w fills rows 8G..8G+7 (G = 8w + ii) of a
+    // A DMA instruction ii of wave w fills rows 8G..8G+7 (G = MT w + ii) of a
     // stage: lane -> row 8G + lane/8, LDS slot lane%8 <- chunk slot ^ ga(row).
 #pragma unroll
-    for (int ii = 0; ii < 8; ++ii) {
-        const int r = 8 * (8 * wave + ii) + (lane >> 3);
+    for (int ii = 0; ii < MT; ++ii) {
+        const int r = 8 * (MT * wave + ii) + (lane >> 3);
         const int ch = (lane & 7) ^ ga(r);
         const int m = m0 + r;
         c.aoff[ii] = m < M ? (uint32_t)((int64_t)m * K * 2 + ch * 16) : kBufferOob;
     }
-    c.m0a = __builtin_amdgcn_readfirstlane(lds0 + wave * 8 * 1024);
+    c.m0a = __builtin_amdgcn_readfirstlane(lds0 + wave * MT * 1024);
     // B DMA instruction gi fills rows 16gi..16gi+15 of a slot: lane -> row
     // 16gi + lane/4, LDS slot lane%4 <- chunk slot ^ gb(row).
 #pragma unroll
@@ -415,11 +468,12 @@ __device__ __forceinline__ void setup(Ctx& c, const Unit& w, const uint16_t* x, 
 
 // Prologue loads of a unit: A(0), A(1) into stages 0, 1; B(0..2) into slots
 // 0..2; scale blocks 0, 1.
-__device__ __forceinline__ void issue_prologue(State& st, const Ctx& c) {
+template <int MT>
+__device__ __forceinline__ void issue_prologue(State<MT>& st, const Ctx<MT>& c) {
 #pragma unroll
-    for (int ii = 0; ii < 8; ++ii) dma16(c.m0a + ii * 1024, c.aoff[ii], c.dx, 0);
+    for (int ii = 0; ii < MT; ++ii) dma16(c.m0a + ii * 1024, c.aoff[ii], c.dx, 0);
 #pragma unroll
-    for (int ii = 0; ii < 8; ++ii) dma16(c.m0a + A_STAGE + ii * 1024, c.aoff[ii], c.dx, BK * 2);
+    for (int ii = 0; ii < MT; ++ii) dma16(c.m0a + Geo<MT>::A_STAGE + ii * 1024, c.aoff[ii], c.dx, BK * 2);
 #pragma unroll
     for (int p = 0; p < 3; ++p)
 #pragma unroll
@@ -434,7 +488,8 @@ __device__ __forceinline__ void issue_prologue(State& st, const Ctx& c) {
 // The rest of the prologue once those loads (and anything else in flight)
 // have landed: B(0) dequantized, B(1) codes and step 0's first A fragments
 // read; the accumulators cleared.
-__device__ __forceinline__ void finish_prologue(State& st, const Ctx& c) {
+template <int MT>
+__device__ __forceinline__ void finish_prologue(State<MT>& st, const Ctx<MT>& c) {
     wait_vm4<0>(st.bsc[0], st.bsc[1]);
     barrier();
 #pragma unroll
@@ -455,15 +510,15 @@ __device__ __forceinline__ void finish_prologue(State& st, const Ctx& c) {
     for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int j = 0; j < NT; ++j) mfma_zero(st.acc[i][j], zero);
-    wait_lgkm8<0>(st.af[0]);
+    wait_lgkm_a<0>(st.af[0]);
 }
 
 // Requirements (checked by the launcher): K % 256 == 0; x and w 16-byte
 // aligned; S == K/128 or S == 1; M*K*2, N*K, N*S*4 and (M + 256)*ldy*2
-// below 2^31.  When SWIGLU, N is the number of weight rows (gate rows
-// [0, N/2), up rows [N/2, N)) and y is [M, N/2].  part: rtiles * splits
-// partial slots of 256 x 256 floats (unused when rtiles == 0).
-template <bool SWIGLU>
+// below 2^31; plan.bm == 32 * MT.  When SWIGLU, N is the number of weight rows
+// (gate rows [0, N/2), up rows [N/2, N)) and y is [M, N/2].  part: rtiles *
+// splits partial slots of BM x 256 floats (unused when rtiles == 0).
+template <int MT, bool SWIGLU>
 __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __restrict__ x,
                                                           const uint8_t* __restrict__ w,
                                                           const float* __restrict__ scales, int S,
@@ -481,8 +536,9 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
     Unit cur;
     while (u < plan.units && !unit_of(u, plan, K, cur)) u += gridDim.x;
     if (u >= plan.units) return;
-    Ctx c;
-    State st;
+    using Gm = Geo<MT>;
+    Ctx<MT> c;
+    State<MT> st;
     setup<SWIGLU>(c, cur, x, w, scales, S, M, N, K, wave, lane, lds0);
     issue_prologue(st, c);
     finish_prologue(st, c);
@@ -491,20 +547,21 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
         // ---- K loop, 4 steps per iteration; only LDS DMA stays in flight
         // across the back edge.
         const int KT = cur.klen / BK;
-        Ring rg{0u, (uint32_t)A_STAGE, (uint32_t)(2 * A_STAGE), 0u, (uint32_t)(2 * B_SLOT)};
+        Ring rg{0u, (uint32_t)Gm::A_STAGE, (uint32_t)(2 * Gm::A_STAGE), 0u, (uint32_t)(2 * B_SLOT)};
         for (int kt = 0; kt < KT; kt += 4) {
-            kstep<0>(st, c, rg, kt);
+            kstep<MT, 0>(st, c, rg, kt);
             rg.advance();
-            kstep<1>(st, c, rg, kt + 1);
+            kstep<MT, 1>(st, c, rg, kt + 1);
             rg.advance();
-            kstep<2>(st, c, rg, kt + 2);
+            kstep<MT, 2>(st, c, rg, kt + 2);
             rg.advance();
-            kstep<3>(st, c, rg, kt + 3);
+            kstep<MT, 3>(st, c, rg, kt + 3);
             rg.advance();
             // step kt+3 read step kt+4's fragments and B(kt+5) (LDS) and loaded
-            // scale block (kt+6)/2 into bsc[1], followed by 10 DMA.
-            wait_lgkm12<0>(st.af[0], st.braw[1]);
-            wait_vm2<10>(st.bsc[1]);
+            // scale block (kt+6)/2 into bsc[1], followed by VM_AFTER_SCALE DMA
+            // (10 for 256-row tiles, 4 for 128).
+            wait_lgkm_ab<0>(st.af[0], st.braw[1]);
+            wait_vm2<Gm::VM_AFTER_SCALE>(st.bsc[1]);
         }
         // The last steps prefetched past the K range (the next K, or zeros
         // past the buffers); their LDS DMA must land before the rings are
@@ -532,7 +589,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
         // every accumulator through scratch memory.
         if (ep_slot >= 0) {
             // FP32 partial of a split tail tile: rows and columns in tile order.
-            const rsrc_t rp = make_rsrc(part + (int64_t)ep_slot * kSlotFloats, (uint32_t)(kSlotFloats * 4));
+            const rsrc_t rp = make_rsrc(part + (int64_t)ep_slot * Gm::SLOT_FLOATS, (uint32_t)(Gm::SLOT_FLOATS * 4));
             uint32_t voff[NT];
 #pragma unroll
             for (int j = 0; j < NT; ++j) voff[j] = (uint32_t)((4 * h * BN + wave * WN + 32 * j + l32) * 4);
@@ -557,7 +614,7 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
             // Stores go through a buffer bounded to the M x ldy output: rows
             // >= M fall outside it and columns past the end get an
             // out-of-range lane offset.
-            const int row0 = ep_mtile * BM + 4 * h;
+            const int row0 = ep_mtile * Gm::BM + 4 * h;
             const rsrc_t ry = make_rsrc(y, (uint32_t)((int64_t)M * ldy * 2));
             if constexpr (SWIGLU) {
                 const int D = N >> 1;
@@ -618,9 +675,10 @@ __global__ __launch_bounds__(256, 1) void gemm_fp8_kernel(const uint16_t* __rest
 // order of its partial slots) at the unsplit epilogue's rounding points, or
 // with SWIGLU y = swiglu(bf16(gate sum), bf16(up sum)), for rows < M and
 // columns inside the output.  Four tile columns per thread.
-template <bool SWIGLU>
+template <int MT, bool SWIGLU>
 __global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restrict__ part, Plan plan, int M, int N,
                                                           uint16_t* __restrict__ y, int64_t ldy) {
+    constexpr int BM = Geo<MT>::BM, SLOT = Geo<MT>::SLOT_FLOATS;
     constexpr int CG = SWIGLU ? 32 : 64;  // 4-column groups per tile row
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (int64_t)plan.rtiles * BM * CG) return;
@@ -633,10 +691,10 @@ __global__ __launch_bounds__(256) void tail_reduce_kernel(const float* __restric
     if (m >= M) return;
     // tile-local column of the first of the four (the gate column for SWIGLU)
     const int lc = SWIGLU ? (cg / 8) * WN + 4 * (cg % 8) : 4 * cg;
-    const float* p = part + (int64_t)r * plan.splits * kSlotFloats + row * BN + lc;
+    const float* p = part + (int64_t)r * plan.splits * SLOT + row * BN + lc;
     auto sum = [&](int off) __attribute__((always_inline)) -> f32x4 {
         f32x4 s = *reinterpret_cast<const f32x4*>(p + off);
-        for (int k = 1; k < plan.splits; ++k) s += *reinterpret_cast<const f32x4*>(p + (int64_t)k * kSlotFloats + off);
+        for (int k = 1; k < plan.splits; ++k) s += *reinterpret_cast<const f32x4*>(p + (int64_t)k * SLOT + off);
         return s;
     };
     const f32x4 a = sum(0);
@@ -661,7 +719,7 @@ inline bool supported(const uint16_t* x, const void* w, int S, int64_t ldy, int6
     const int64_t lim = (int64_t)1 << 31;
     return K % 256 == 0 && K > 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
            reinterpret_cast<uintptr_t>(w) % 16 == 0 && (S == 1 || S == K / 128) && M * K * 2 < lim &&
-           N * K < lim && N * (int64_t)S * 4 < lim && (M + BM) * ldy * 2 < lim;
+           N * K < lim && N * (int64_t)S * 4 < lim && (M + kBMMax) * ldy * 2 < lim;
 }
 
 }  // namespace gemm_fp8

@@ -228,12 +228,13 @@ def test_engine_decision_table(fp8lin):
     assert _path(F, O(), _weight(F, scales=False), 4) == F.PATH_BF16
 
 
-SLOT = 256 * 256 * 4  # one FP32 partial tile
+SLOT = 256 * 256 * 4  # one FP32 partial of a 256-row tile
+SLOT128 = 128 * 256 * 4  # of a 128-row tile (M <= 128)
 
 
 def test_engine_splitk_workspace(fp8lin):
-    """FP8 GEMM branch on a 256-CU device: K-split partials (one 256x256 FP32
-    slot per split tile and K range) when the tiles number at most half the
+    """FP8 GEMM branch on a 256-CU device: K-split partials (one BM x 256 FP32
+    slot per split tile and K range; BM = 128 rows for M <= 128, else 256) when the tiles number at most half the
     CUs (every tile, min(256 / T, K / 256, 8) ranges) or leave a last round
     on at most half of them (those tiles, min(256 / R, K / 256, 8))."""
     F, O = fp8lin, fp8lin.LinearOptions
@@ -250,7 +251,9 @@ def test_engine_splitk_workspace(fp8lin):
     assert ws(17408, 5120, 2560) == 0                    # 680 = 2 * 256 + 168: last round over half
     assert ws(75968, 5120, 512) == 82 * 3 * SLOT         # output head: 594 = 2 * 256 + 82
     assert ws(22784, 512, 1024) == 100 * 2 * SLOT        # 356 = 256 + 100, K / 256 = 2
-    assert ws(384, 512, 20) == 2 * 2 * SLOT              # K / 256 = 2 caps the splits
+    assert ws(384, 512, 20) == 2 * 2 * SLOT128           # K / 256 = 2 caps the splits; 128-row tiles
+    assert ws(7168, 5120, 128) == 28 * 8 * SLOT128       # M <= 128: one row of 128-row tiles
+    assert ws(7168, 5120, 129) == 28 * 8 * SLOT          # M > 128: 256-row tiles
     assert ws(384, 256, 20) == 0                         # one 256-K chunk
     assert ws(384, 640, 20) == 0                         # K % 256 != 0: general GEMM
     assert ws(7168, 5120, 8) == 0                        # GEMV rows
@@ -265,7 +268,7 @@ def test_linear_swiglu_workspace(fp8lin):
     assert L.fp8lin_linear_swiglu_workspace_bytes(1024, 17408, 5120) == 16 * 8 * SLOT
     assert L.fp8lin_linear_swiglu_workspace_bytes(4096, 17408, 5120) == 64 * 4 * SLOT
     assert L.fp8lin_linear_swiglu_workspace_bytes(3913, 17408, 5120) == 64 * 4 * SLOT
-    assert L.fp8lin_linear_swiglu_workspace_bytes(64, 512, 512) == 2 * 2 * SLOT
+    assert L.fp8lin_linear_swiglu_workspace_bytes(64, 512, 512) == 2 * 2 * SLOT128
     assert L.fp8lin_linear_swiglu_workspace_bytes(64, 511, 512) == 0          # odd N
     n = L.fp8lin_linear_swiglu_workspace_bytes(1024, 17408, 5120)
     assert L.fp8lin_linear_swiglu_ws(P, P, P, 40, P, 1024, 17408, 5120, P, n - 16, None) == 4

@@ -232,6 +232,38 @@ def test_gemm_fp8(fp8lin, gpu, oracle, m, n, k):
     assert_parity(bits(y), oracle.linear(x, codes, scales), f"gemm {m}x{n}x{k}")
 
 
+@pytest.mark.parametrize("n,k,swiglu", [(520, 512, False), (2056, 1024, False), (1040, 768, True),
+                                        (17408, 5120, True)])
+def test_gemm_tile_heights_agree(fp8lin, gpu, oracle, n, k, swiglu):
+    """The FP8 GEMM runs 128-row tiles for M <= 128 and 256-row tiles above.
+    Unsplit, both give every output the same FP32 sum (same K order, same
+    accumulator position), so an M = 128 call equals rows 0..127 of an
+    M = 129 call on the same rows bit for bit; the M = 128 call also holds
+    the oracle bar (plain: a column sample, SwiGLU: all outputs of a row
+    sample)."""
+    rng = np.random.default_rng(n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (129, k))
+    c, s = up(codes, gpu), up(scales, gpu)
+    xg = up(x, gpu)
+    if swiglu:
+        small = fp8lin.linear_swiglu(xg[:128].contiguous(), c, s, split=False)
+        big = fp8lin.linear_swiglu(xg, c, s, split=False)
+    else:
+        small = fp8lin.fp8_linear(xg[:128].contiguous(), c, s)
+        big = fp8lin.fp8_linear(xg, c, s)
+    assert torch.equal(small, big[:128])
+    if swiglu:
+        rows = [0, 1, 63, 64, 127]
+        ref = oracle.swiglu(oracle.linear(x[rows], codes, scales))
+        assert_parity(bits(small)[rows], ref, f"swiglu tiles {n}x{k}", elementwise=False)
+    else:
+        cols = (max(0, n - 300), n)
+        ref = oracle.linear(x[:128], codes, scales, rows=cols)
+        assert_parity(bits(small)[:, cols[0]:cols[1]], ref[:, cols[0]:cols[1]], f"gemm tiles {n}x{k}")
+
+
 @pytest.mark.parametrize("m,n,k", [(17, 137, 257), (300, 520, 640)])
 def test_gemm_bf16(fp8lin, gpu, oracle, m, n, k):
     rng = np.random.default_rng(m * n)
@@ -379,16 +411,18 @@ def test_gemv_long_k(fp8lin, gpu, oracle, m, k):
 
 # ------------------------------------------------------------ split-K GEMM
 def splitk_bytes(m, n, k, cus=256):
-    """Split-K workspace of the FP8 GEMM plan on a device of `cus` CUs: every
-    tile split when the tiles number at most half the CUs, else the tiles of
-    a last round on at most half the CUs; min(CUs / tiles, K / 256, 8) K
-    ranges of one 256 x 256 FP32 partial each."""
-    tiles = -(-m // 256) * -(-n // 256)
+    """Split-K workspace of the FP8 GEMM plan on a device of `cus` CUs, with
+    bm x 256 tiles (bm = 128 for m <= 128, else 256): every tile split when
+    the tiles number at most half the CUs, else the tiles of a last round on
+    at most half the CUs; min(CUs / tiles, K / 256, 8) K ranges of one
+    bm x 256 FP32 partial each."""
+    bm = 128 if m <= 128 else 256
+    tiles = -(-m // bm) * -(-n // 256)
     split = tiles if 2 * tiles <= cus else tiles % cus if tiles > cus and 2 * (tiles % cus) <= cus else 0
     if split == 0:
         return 0
     s = min(cus // split, k // 256, 8)
-    return split * s * 256 * 256 * 4 if s > 1 else 0
+    return split * s * bm * 256 * 4 if s > 1 else 0
 
 
 @pytest.mark.parametrize("m,n,k", [(300, 1040, 1024), (33, 520, 2560), (17, 384, 8704), (600, 7168, 512),
