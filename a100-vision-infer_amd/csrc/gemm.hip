@@ -136,6 +136,18 @@ hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, 
     return launch_gemv_rows(x, w, scales != nullptr, scales, S, y, ldy, M, N, K, wide, swiglu, stream);
 }
 
+// 9..16 activation rows of a block-FP8 weight of more than 1024 rows: the
+// small-M matrix-core kernel (small_m.hip), whose 16x16 MFMA tile holds all
+// of them, streams the codes once with each dequantized once; a GEMM tile
+// would be at least seven eighths padding.  Its geometry limits are those of
+// the decode routing (block scales [N, K/128], 16-byte aligned x and codes).
+bool mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K) {
+    const int64_t lim = (int64_t)1 << 31;
+    return M > 8 && M <= 16 && N > 1024 && K % 128 == 0 && S == K / 128 &&
+           reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 && 16 * K < lim &&
+           N * S * 4 < lim && M * K * 2 < lim;
+}
+
 }  // namespace
 
 // Compute units of the current device (cached per device), rounded down to a
@@ -155,7 +167,9 @@ int compute_units() {
 }
 
 size_t gemm_workspace_bytes(int S, int64_t ldy, int M, int N, int K, bool swiglu) {
-    if (skinny(M, N, swiglu) || !fp8_kernel_ok(nullptr, nullptr, S, ldy, M, N, K)) return 0;
+    if (skinny(M, N, swiglu) || mid_rows(nullptr, nullptr, S, M, N, K) ||
+        !fp8_kernel_ok(nullptr, nullptr, S, ldy, M, N, K))
+        return 0;
     return plan_bytes(make_plan(M, N, K, swiglu, compute_units(), true));
 }
 
@@ -163,6 +177,8 @@ hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales,
                           int M, int N, int K, bool swiglu, void* ws, size_t ws_bytes, hipStream_t stream) {
     if (skinny(M, N, swiglu)) return launch_skinny(x, w, scales, S, y, ldy, M, N, K, swiglu, stream);
     const bool fp8 = scales != nullptr;
+    if (fp8 && mid_rows(x, w, S, M, N, K))
+        return launch_small_m(x, static_cast<const uint8_t*>(w), scales, y, ldy, M, N, K, 1, swiglu, stream);
     if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
         const uint8_t* codes = static_cast<const uint8_t*>(w);
         const int G = compute_units();
@@ -180,6 +196,8 @@ hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, in
                        int64_t ldy, int M, int N, int K, bool swiglu, hipStream_t stream) {
     if (skinny(M, N, swiglu)) return launch_skinny(x, w, scales, S, y, ldy, M, N, K, swiglu, stream);
     const bool fp8 = scales != nullptr;
+    if (fp8 && mid_rows(x, w, S, M, N, K))
+        return launch_small_m(x, static_cast<const uint8_t*>(w), scales, y, ldy, M, N, K, 1, swiglu, stream);
     if (fp8 && fp8_kernel_ok(x, w, S, ldy, M, N, K)) {
         const uint8_t* codes = static_cast<const uint8_t*>(w);
         const int G = compute_units();

@@ -1,4 +1,4 @@
-// Small-M (2..8 activation rows) block-FP8 linear on the matrix cores.
+// Small-M (2..16 activation rows) block-FP8 linear on the matrix cores.
 //
 // Contract of fp8_tensor_small (src/fp8_tensor.cu:18-71): K % 128 == 0, block
 // scales [N, K/128], each weight is decoded to BF16 with the reference
@@ -7,8 +7,8 @@
 // (src/fp8_tensor.cu:41-51); here the K partition is the kernel's own and the
 // same for both values, so both give the same bits.
 //
-// MI355X design: the path is an HBM stream of FP8 codes (M <= 8 rows reuse
-// each code at most 8 times), so the kernel is built around keeping enough
+// MI355X design: the path is an HBM stream of FP8 codes (M <= 16 rows reuse
+// each code at most 16 times), so the kernel is built around keeping enough
 // bytes in flight with coalesced loads, and holds no load data in registers
 // across steps:
 //   - a workgroup owns 16 weight rows; its 4 waves split K: wave w takes block
@@ -55,7 +55,7 @@ using gemm_fp8::make_desc;
 using gemm_fp8::wait_vm;
 
 constexpr int kRowX = 1040;  // LDS stride of an activation row (1 KiB + 16 B)
-constexpr int kMaxM = 8;
+constexpr int kMaxM = 16;    // rows of the 16x16x32 MFMA tile's activation side
 constexpr int kMaxLds = 160 * 1024;
 
 __device__ __forceinline__ int sw(int r) { return (r >> 1) & 7; }
@@ -91,12 +91,14 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, 
 //   NBW == 4 / W: the waves share 16 rows and split every chunk's 4 blocks
 //     (wave w takes blocks w, w + W, ...); their partial sums are added in
 //     LDS in wave order.
-template <int W, int D, int NBW, int XA>
+// MX (8 or 16) bounds the activation rows a launch may have.
+template <int W, int D, int NBW, int XA, int MX>
 struct SmallCfg {
+    static_assert(MX == 8 || MX == 16, "8 or 16 activation rows");
     static constexpr bool KSPLIT = NBW < 4;
     static constexpr int ROWS = KSPLIT ? 16 : 16 * W;
     static constexpr int XBUFS = XA + 1;
-    static constexpr int XQ = kMaxM / W;  // activation rows DMA'd per wave per chunk
+    static constexpr int XQ = MX / W;  // activation rows DMA'd per wave per chunk
     static constexpr int CS = XQ + 1;
     static constexpr int W0 = wait0(D, CS, NBW, XA), W1 = wait1(D, CS, NBW, XA);
     static_assert(W * NBW == 4 || NBW == 4, "a chunk's blocks are split evenly");
@@ -106,7 +108,7 @@ struct SmallCfg {
     }
 };
 
-// Requirements (checked by the host): 2 <= M <= 8, K % 128 == 0,
+// Requirements (checked by the host): 2 <= M <= MX, K % 128 == 0,
 // 32 * K < 2^31.
 // per (KSPLIT form): rows of each workgroup, 1..16 (pairs for SW, 1..8); a
 // row's sum does not depend on which workgroup or slot holds it.
@@ -116,13 +118,13 @@ struct SmallCfg {
 // its slot, so the outputs are fused_swiglu of the plain kernel's, bit for
 // bit.  Also requires N * K / 32 < 2^31 (scale offsets over the whole
 // matrix).
-template <int W, int D, int NBW, int XA, bool SW>
+template <int W, int D, int NBW, int XA, int MX, bool SW>
 __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restrict__ x,
                                                          const uint8_t* __restrict__ codes,
                                                          const float* __restrict__ scales,
                                                          uint16_t* __restrict__ y, int64_t ldy, int M, int N,
                                                          int K, int per) {
-    using C = SmallCfg<W, D, NBW, XA>;
+    using C = SmallCfg<W, D, NBW, XA, MX>;
     static_assert(!SW || C::KSPLIT, "the SwiGLU form pairs the 16 rows of one workgroup");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -321,14 +323,14 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
 }
 
 // per: rows (pairs for SW) of each workgroup.
-template <int W, int D, int NBW, int XA, bool SW>
+template <int W, int D, int NBW, int XA, int MX, bool SW>
 hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy, int M,
                   int N, int K, int per, hipStream_t stream) {
-    using C = SmallCfg<W, D, NBW, XA>;
-    auto kern = small_m_kernel<W, D, NBW, XA, SW>;
+    using C = SmallCfg<W, D, NBW, XA, MX>;
+    auto kern = small_m_kernel<W, D, NBW, XA, MX, SW>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       (int)C::lds(kMaxM));
+                                                       (int)C::lds(MX));
     if (attr != hipSuccess) return attr;
     static_assert(C::KSPLIT, "rows per workgroup are set at run time only in the K-split form");
     const int groups = SW ? (N / 2 + per - 1) / per : (N + per - 1) / per;
@@ -363,7 +365,7 @@ hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, 
 // wave partials in wave order.  It depends on K only (not on the row range),
 // so split 1 and 4 and every workgroup count give the same bits.
 constexpr int kStreamWaves = 8;
-constexpr int kStreamRed = 2 * kStreamWaves * 512;  // two buffers of 8 waves x 8 x 16 floats
+constexpr int kStreamRed = 2 * kStreamWaves * 1024;  // two buffers of 8 waves x 16 x 16 floats
 
 template <int NB>
 constexpr int stream_scale_dmas() { return (16 * NB + 63) / 64; }
@@ -373,7 +375,7 @@ constexpr int stream_lds_fixed() {
 }
 constexpr int floordiv(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 
-// Requirements (checked by the host): 1 <= M <= 8, K % 128 == 0,
+// Requirements (checked by the host): 1 <= M <= 16, K % 128 == 0,
 // 8 * (NB - 1) < K / 128 <= 8 * NB, N * K < 2^31, per * M * 2 bytes of LDS
 // beyond stream_lds_fixed.
 // SW: gate/up + SwiGLU (N weight rows, gate [0, N/2), up [N/2, N); y is
@@ -534,30 +536,30 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         }(std::make_integer_sequence<int, NB>{});
         sbase += NB % D;
         sbase = sbase >= D ? sbase - D : sbase;
-        // acc[i] = C[m = 4g + i][n = row]; lanes g < 2 hold the rows m < 8
-        float* rb = red + (p & 1) * (W * 128);
-        if (g < 2) {
+        // acc[i] = C[m = 4g + i][n = row]; lanes with 4g < M hold rows m < M
+        float* rb = red + (p & 1) * (W * 256);
+        if (4 * g < M) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) rb[wave * 128 + (4 * g + i) * 16 + row] = acc[i];
+            for (int i = 0; i < 4; ++i) rb[wave * 256 + (4 * g + i) * 16 + row] = acc[i];
         }
         // Two buffers: wave (p % 8) reads buffer p & 1 before it reaches the
         // barrier that ends piece p + 1, after which buffer p & 1 is rewritten.
         gemm_fp8::wait_lgkm<0>();
         barrier();
-        if (wave == (p & (W - 1)) && g < 2 && (!SW || row < 8)) {
+        if (wave == (p & (W - 1)) && 4 * g < M && (!SW || row < 8)) {
             const int n0 = piece(p);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 4 * g + i;
                 float t = rb[m * 16 + row];
 #pragma unroll
-                for (int w = 1; w < W; ++w) t = t + rb[w * 128 + m * 16 + row];
+                for (int w = 1; w < W; ++w) t = t + rb[w * 256 + m * 16 + row];
                 uint16_t v = f32_to_bf16_bits(t);
                 if constexpr (SW) {
                     // the up row of this pair sits in slot row + 8
                     float u = rb[m * 16 + row + 8];
 #pragma unroll
-                    for (int w = 1; w < W; ++w) u = u + rb[w * 128 + m * 16 + row + 8];
+                    for (int w = 1; w < W; ++w) u = u + rb[w * 256 + m * 16 + row + 8];
                     v = swiglu_bf16_bits(v, f32_to_bf16_bits(u));
                 }
                 if (m < M && row < pr && n0 + row < r1) out[m * per + (n0 - r0) + row] = v;
@@ -606,7 +608,7 @@ int stream_nb(int K) {
 }  // namespace
 
 // Four waves share 16 weight rows and split every chunk's 4 blocks, with a
-// 4-block ring each.  Activations are prefetched 3 chunks ahead for M > 4
+// 4-block ring each.  Activations are prefetched 3 chunks ahead for 4 < M <= 8
 // (73 KiB of LDS at M = 8, two workgroups per CU) and 2 chunks ahead for
 // M <= 4, which brings the LDS under 54 KiB and fits three workgroups per CU:
 // 7% faster on the 75968-row head at M = 2 and 4, the same elsewhere.  The
@@ -650,12 +652,21 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
     // a quarter of the CUs streaming a second workgroup alone).
     const int units = swiglu ? N / 2 : N;
     const int per = std::clamp((units + 2 * cus - 1) / (2 * cus), swiglu ? 4 : 8, swiglu ? 8 : 16);
+    // 9..16 rows: activations 2 chunks ahead while two workgroups still fit
+    // per CU (M <= 13), else 1 (measured at M = 16: 13.3 against 16.9 us at
+    // QKV-gate, 17.9 against 21.9 at down; at M = 9 two chunks ahead are 3%
+    // faster).
+    const bool xa2 = 2 * SmallCfg<4, 4, 1, 2, 16>::lds(M) <= (size_t)kMaxLds;
     if (swiglu) {
-        if (M <= 4) return launch<4, 4, 1, 2, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-        return launch<4, 4, 1, 3, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        if (M <= 4) return launch<4, 4, 1, 2, 8, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        if (M <= 8) return launch<4, 4, 1, 3, 8, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        if (xa2) return launch<4, 4, 1, 2, 16, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        return launch<4, 4, 1, 1, 16, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
     }
-    if (M <= 4) return launch<4, 4, 1, 2, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
-    return launch<4, 4, 1, 3, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    if (M <= 4) return launch<4, 4, 1, 2, 8, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    if (M <= 8) return launch<4, 4, 1, 3, 8, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    if (xa2) return launch<4, 4, 1, 2, 16, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    return launch<4, 4, 1, 1, 16, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
 }
 
 }  // namespace fp8lin

@@ -689,3 +689,43 @@ def test_linear_small_m_rows(fp8lin, gpu, oracle, m, n, k):
     assert_parity(bits(fp8lin.fp8_linear(xu, c, s, True)), ref, f"unaligned x {m}x{n}x{k}")
     assert_parity(bits(fp8lin.linear_swiglu(xu, c, s, split=False)), oracle.swiglu(ref),
                   f"unaligned x swiglu {m}x{n}x{k}", elementwise=False)
+
+
+# ------------------------------------ fp8_linear at 9..16 rows on the matrix cores
+@pytest.mark.parametrize("m,n,k", [(9, 2056, 384), (16, 2056, 384), (12, 8208, 5120), (16, 8208, 4096),
+                                   (13, 1040, 8704), (16, 8240, 8704)])
+def test_linear_mid_rows(fp8lin, gpu, oracle, m, n, k):
+    """fp8_linear with 9..16 rows against more than 1024 weight rows runs the
+    small-M matrix-core kernel, whose 16x16 MFMA tile holds every row (the
+    16-row workgroups at n = 2056 and 1040, the row-range form at n = 8208 and
+    8240), instead of a mostly-padding GEMM tile.  Every output against the
+    FP64 oracle; the fused SwiGLU bit-equal to fused_swiglu(fp8_linear), with
+    or without a workspace (none is needed); Engine::linear's FP8 GEMM branch
+    asks for no workspace and gives the same bits; an unaligned view of x
+    runs the GEMM, at the bar."""
+    import ctypes
+    F = fp8lin
+    rng = np.random.default_rng(m * 100019 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = F.fp8_linear(xg, c, s)
+    assert_parity(bits(y), ref, f"mid rows {m}x{n}x{k}")
+    assert F.lib().fp8lin_linear_swiglu_workspace_bytes(m, n, k) == 0
+    fused = F.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, F.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert torch.equal(F.linear_swiglu(xg, c, s), fused)
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+    eng = F.LinearEngine()
+    eng.add("w.weight", c, s)
+    rec = eng._record("w")
+    assert F.lib().fp8lin_engine_linear_workspace_bytes(ctypes.byref(eng.options), ctypes.byref(rec), m) == 0
+    ye, path = eng.linear(xg, "w", return_path=True)
+    assert path == F.PATH_FP8_GEMM
+    assert torch.equal(ye, y)
+    flat = torch.empty(m * k + 1, dtype=torch.bfloat16, device=gpu)
+    xu = flat[1:].view(m, k)
+    xu.copy_(xg)
+    assert_parity(bits(F.fp8_linear(xu, c, s)), ref, f"unaligned x {m}x{n}x{k}")
