@@ -34,9 +34,9 @@ GATE_UP_TRAFFIC_BYTES = 92_152_013
 # summed over the 8 XCDs (8 x the dispatch's cycles at the shader clock), so
 # rocprofv3's own MfmaUtil formula reads 8x low on this part.  Re-measure when
 # the kernel changes.
-PREFILL_MFMA_BUSY = 0.732
+PREFILL_MFMA_BUSY = 0.730
 PREFILL_MFMA_BUSY_SOURCE = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE: 715.7e6 busy cycles "
-                            "/ 1024 SIMDs over GRBM_GUI_ACTIVE / 8 XCDs = 0.955e6 cycles (1.60 GHz)")
+                            "/ 1024 SIMDs over GRBM_GUI_ACTIVE / 8 XCDs = 0.957e6 cycles (1.60 GHz)")
 SHAPES = [("gate_up", 17408, 5120), ("down", 5120, 8704), ("qkv_gate", 7168, 5120)]
 
 
@@ -58,7 +58,7 @@ def parse():
     p.add_argument("--sections", default="gemv,small,prefill,chain,inproj,head,stream,ceiling",
                    help="secondary measurements to run (comma list of gemv, small, prefill, "
                         "chain, inproj, head, stream, ceiling)")
-    p.add_argument("--prefill-m", default="512,1024,4096",
+    p.add_argument("--prefill-m", default="128,512,1024,4096",
                    help="prefill row counts of the prefill section (comma list)")
     p.add_argument("--calibrate", action="store_true",
                    help="also run a 256 MiB device copy (known HBM bytes) for counter scaling")
@@ -243,7 +243,7 @@ def main():
         tf = extra["prefill_swiglu_m4096_TFLOPs"]
         out["roofline_prefill"] = {
             "bound": "mfma",
-            "kernel": "gemm_fp8_kernel<true> + tail_reduce_kernel<true> (gate/up+SwiGLU 17408x5120, M=4096)",
+            "kernel": "gemm_fp8_kernel<8, true> + tail_reduce_kernel<8, true> (gate/up+SwiGLU 17408x5120, M=4096)",
             "achieved": tf,
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
@@ -298,7 +298,7 @@ def graph_timed(torch, fn, sp, reps=20, replays=20):
     return a.elapsed_time(b) / (replays * reps)
 
 
-def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(512, 1024, 4096)):
+def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(128, 512, 1024, 4096)):
     """Per-shape and per-path figures through the C ABI with preallocated
     outputs, timed as graph replays of back-to-back launches over the rotated
     weight copies (the host's launch rate stays out of the figures)."""
