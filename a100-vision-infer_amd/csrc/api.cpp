@@ -194,6 +194,11 @@ void gemm_bf16_impl(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t l
 // The split-4 partials are summed inside each workgroup (small_m.hip).
 size_t tensor_small_ws(int64_t, int64_t, int) { return 0; }
 
+// Whether fp8_tensor_small runs the matrix-core kernel (else the GEMV).
+bool tensor_small_matrix_core(const uint16_t* x, const uint8_t* codes, int64_t K) {
+    return aligned16(x) && aligned16(codes) && 16 * K < kMaxDim;
+}
+
 void tensor_small_impl(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                        int64_t ldy, int64_t M, int64_t N, int64_t K, int split, void* ws,
                        size_t ws_bytes, hipStream_t stream) {
@@ -210,7 +215,7 @@ void tensor_small_impl(const uint16_t* x, const uint8_t* codes, const float* sca
     // (src/fp8_tensor.cu:54-59), so an unaligned view or a K too large for
     // those offsets runs the multi-row GEMV instead: same operator, same
     // parity bar, only the FP32 summation order differs.
-    if (!aligned16(x) || !aligned16(codes) || 16 * K >= kMaxDim) {
+    if (!tensor_small_matrix_core(x, codes, K)) {
         check_hip(fp8lin::launch_gemv(x, codes, true, scales, (int)(K / 128), y, ldy, (int)M, (int)N, (int)K,
                                       K % 16 == 0 && aligned16(x) && aligned16(codes), stream),
                   "fp8 small-M fallback gemv launch");
@@ -410,10 +415,19 @@ size_t vocab_ws(int64_t M, int64_t N) { return (size_t)(M * fp8lin::vocab_chunks
 // Output head: the logits (padded to 256 bytes), then the chunk partials.
 int64_t logits_bytes(int64_t M, int64_t N) { return (M * N * 2 + 255) / 256 * 256; }
 // Either candidate form: the logits and chunk pairs of the two-stage form, or
-// the GEMV candidate form's pairs, slices and counters (no logits).
+// the ring GEMV's candidate pairs, slices and counters (M <= 2; no logits).
+// The small-M row-range kernel's candidate pairs (M x at most CUs) fit in the
+// two-stage form's logits (M x N BF16, N >= 32 CUs there).
 size_t linear_candidates_ws(int64_t M, int64_t N) {
     const size_t two_stage = (size_t)logits_bytes(M, N) + vocab_ws(M, N);
     return M <= 2 ? std::max(two_stage, fp8lin::gemv_candidates_ws_bytes((int)M, (int)N)) : two_stage;
+}
+
+// Whether fp8lin_linear runs the small-M matrix-core kernel for this call
+// (3..8 rows, or 2 at K > 5120, through linear_small_m; 9..16 rows through
+// the GEMM dispatch's mid-rows rule).
+bool linear_runs_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t M, int64_t N, int64_t K) {
+    return linear_small_m(x, codes, S, M, N, K) || fp8lin::gemm_mid_rows(x, codes, (int)S, M, N, K);
 }
 
 void linear_candidates_impl(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S, int64_t M,
@@ -423,6 +437,19 @@ void linear_candidates_impl(const uint16_t* x, const uint8_t* codes, const float
         check_hip(fp8lin::launch_gemv_candidates(x, codes, scales, (int)S, (int)M, (int)N, (int)K, offset, ws, out,
                                                  stream),
                   "fp8 gemv candidates launch");
+        return;
+    }
+    // where fp8lin_linear runs the small-M row-range kernel: its candidate
+    // form (the same logits, never stored; at most CUs pairs per row) and one
+    // finishing workgroup per row
+    if (M <= 16 && linear_runs_small_m(x, codes, S, M, N, K) &&
+        fp8lin::small_m_candidates_supported((int)M, (int)N, (int)K)) {
+        auto* part = static_cast<uint32_t*>(ws);
+        int64_t groups = 0;
+        check_hip(fp8lin::launch_small_m_candidates(x, codes, scales, (int)M, (int)N, (int)K, part, groups, stream),
+                  "fp8 small-M candidates launch");
+        check_hip(fp8lin::launch_candidates_finish(part, (int)M, groups, offset, out, stream),
+                  "candidates finish launch");
         return;
     }
     auto* logits = static_cast<uint16_t*>(ws);
@@ -820,10 +847,24 @@ int fp8lin_engine_linear_candidates(const fp8lin_linear_options* options, const 
         ensure_device();
         const hipStream_t s = as_stream(stream);
         int path = engine_path(*options, *weight, rows);
+        const auto* codes = static_cast<const uint8_t*>(weight->data);
         if (path == FP8LIN_PATH_FP8_GEMV && !weight->bias) {
             // the FP8 GEMV branch is fp8lin_linear: its candidate form
-            linear_candidates_impl(x, static_cast<const uint8_t*>(weight->data), weight->scales, weight->scale_cols,
-                                   rows, weight->N, weight->K, offset, base, out, s);
+            linear_candidates_impl(x, codes, weight->scales, weight->scale_cols, rows, weight->N, weight->K, offset,
+                                   base, out, s);
+        } else if (path == FP8LIN_PATH_TENSOR_SMALL && !weight->bias && tensor_small_matrix_core(x, codes, weight->K) &&
+                   fp8lin::small_m_candidates_supported((int)rows, (int)weight->N, (int)weight->K)) {
+            // the tensor-small branch runs the small-M row-range kernel here:
+            // its candidate form gives the candidates of the same logits; its
+            // pairs (rows x at most CUs) go where the logits would (rows x N
+            // BF16, N >= 32 CUs on this path)
+            auto* pairs = reinterpret_cast<uint32_t*>(base);
+            int64_t groups = 0;
+            check_hip(fp8lin::launch_small_m_candidates(x, codes, weight->scales, (int)rows, (int)weight->N,
+                                                        (int)weight->K, pairs, groups, s),
+                      "fp8 small-M candidates launch");
+            check_hip(fp8lin::launch_candidates_finish(pairs, (int)rows, groups, offset, out, s),
+                      "candidates finish launch");
         } else {
             path = engine_impl(*options, *weight, x, rows, logits, weight->N, base + head, workspace_bytes - head, s);
             check_hip(fp8lin::launch_vocab_candidates(logits, (int)rows, (int)weight->N, offset, part, out, s),

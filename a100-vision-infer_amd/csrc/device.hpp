@@ -70,6 +70,16 @@ __device__ __forceinline__ void pick(float& v, uint32_t& id, float ov, uint32_t 
     }
 }
 
+// The best pair of the 64 lanes of a wave (every lane gets it).
+__device__ __forceinline__ void wave_pick(float& v, uint32_t& id) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+        const float ov = __shfl_xor(v, d, kWave);
+        const uint32_t oid = __shfl_xor(id, d, kWave);
+        pick(v, id, ov, oid);
+    }
+}
+
 // NaN counts as +inf: the row's candidate becomes non-finite and the merge
 // rejects it, as torch.max's NaN propagation does in the reference.
 __device__ __forceinline__ void pick_bf16(float& v, uint32_t& id, uint32_t bits, uint32_t i) {

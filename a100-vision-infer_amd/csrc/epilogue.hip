@@ -168,15 +168,6 @@ __global__ __launch_bounds__(kNormMaxThreads) void rms_kernel(const uint16_t* __
 constexpr int kVocabChunk = 2048;
 constexpr int kVocabThreads = kVocabChunk / 8;
 
-__device__ __forceinline__ void wave_pick(float& v, uint32_t& id) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-        const float ov = __shfl_xor(v, d, kWave);
-        const uint32_t oid = __shfl_xor(id, d, kWave);
-        pick(v, id, ov, oid);
-    }
-}
-
 template <bool VEC>
 __global__ __launch_bounds__(kVocabThreads) void vocab_partial_kernel(const uint16_t* __restrict__ logits, int N,
                                                                       int chunks, uint32_t* __restrict__ part) {
@@ -778,8 +769,6 @@ hipError_t launch_reduce_rms(const uint16_t* x, const uint16_t* partials, int ra
 
 int64_t vocab_chunks(int64_t N) { return (N + kVocabChunk - 1) / kVocabChunk; }
 
-static hipError_t launch_candidates_finish(const uint32_t* part, int M, int64_t chunks, int64_t offset,
-                                          double* out, hipStream_t stream);
 
 hipError_t launch_vocab_candidates(const uint16_t* logits, int M, int N, int64_t offset, uint32_t* part,
                                    double* out, hipStream_t stream) {
@@ -803,8 +792,8 @@ hipError_t launch_candidates_finish_sliced(const uint32_t* part, int M, int64_t 
     return hipGetLastError();
 }
 
-static hipError_t launch_candidates_finish(const uint32_t* part, int M, int64_t chunks, int64_t offset,
-                                          double* out, hipStream_t stream) {
+hipError_t launch_candidates_finish(const uint32_t* part, int M, int64_t chunks, int64_t offset, double* out,
+                                    hipStream_t stream) {
     hipLaunchKernelGGL((vocab_finish_kernel<64, 4>), dim3(M), dim3(64), 0, stream, part, (int)chunks, offset, out);
     return hipGetLastError();
 }

@@ -150,6 +150,10 @@ bool mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int
 
 }  // namespace
 
+bool gemm_mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K) {
+    return mid_rows(x, w, S, M, N, K);
+}
+
 // Compute units of the current device (cached per device), rounded down to a
 // multiple of the 8 XCDs: the persistent kernels' grid size.
 int compute_units() {

@@ -36,6 +36,18 @@ int compute_units();
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales,
                           uint16_t* y, int64_t ldy, int M, int N, int K, int split, bool swiglu,
                           hipStream_t stream);
+// The output head's candidates where launch_small_m (plain form) runs its
+// row-range kernel (small_m_candidates_supported): the same logits, reduced
+// per workgroup and activation row to one {value bits, column} pair, part
+// [M][groups] pairs (groups <= CUs), for launch_candidates_finish.  No logits
+// written.
+bool small_m_candidates_supported(int M, int N, int K);
+hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
+                                     int K, uint32_t* part, int64_t& groups, hipStream_t stream);
+// out[2m] = value, out[2m + 1] = column + offset of the best of the `chunks`
+// pairs of row m in part [M][chunks] (epilogue.hip; one workgroup per row).
+hipError_t launch_candidates_finish(const uint32_t* part, int M, int64_t chunks, int64_t offset, double* out,
+                                    hipStream_t stream);
 
 // MFMA GEMM (gemm.hip).  B is E4M3FN codes (scales != nullptr, dequantized
 // to BF16 in LDS) or BF16 (scales == nullptr).  When swiglu, N is the number
@@ -49,6 +61,9 @@ hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, in
 // (0 when nothing splits); a smaller or unaligned workspace, unaligned x or
 // w, or another kernel's shape run unsplit.
 size_t gemm_workspace_bytes(int S, int64_t ldy, int M, int N, int K, bool swiglu);
+// Whether the GEMM dispatch sends this FP8 call (9..16 rows) to the small-M
+// matrix-core kernel instead of a GEMM tile.
+bool gemm_mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K);
 hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
                           int M, int N, int K, bool swiglu, void* ws, size_t ws_bytes, hipStream_t stream);
 

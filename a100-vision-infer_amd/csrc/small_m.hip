@@ -383,13 +383,20 @@ constexpr int floordiv(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / 
 // piece of pr <= 8 pairs holds its gate rows in slots 0..pr-1 and their up
 // rows in slots 8..8+pr-1.  A row's sum does not depend on its slot or
 // piece, so the outputs are fused_swiglu of the plain kernel's, bit for bit.
-template <int NB, int D, bool SW>
+// CAND: the output head's vocabulary candidates instead of y.  Per activation
+// row m the workgroup writes the best {BF16 logit as float bits, column} of
+// its row range (the logits fp8lin_linear would store; larger value, then
+// smaller column, NaN as +inf) to pair m * gridDim + blockIdx of part, the
+// layout of the two-stage candidates' chunk pairs.
+template <int NB, int D, bool SW, bool CAND>
 __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const uint16_t* __restrict__ x,
                                                                           const uint8_t* __restrict__ codes,
                                                                           const float* __restrict__ scales,
                                                                           uint16_t* __restrict__ y, int64_t ldy,
-                                                                          int M, int N, int K, int per, int pr) {
+                                                                          int M, int N, int K, int per, int pr,
+                                                                          uint32_t* __restrict__ part) {
     constexpr int W = kStreamWaves;
+    static_assert(!(SW && CAND), "candidates of a plain projection only");
     constexpr int SC = stream_scale_dmas<NB>();
     static_assert(D <= NB, "the prologue matches the steady-state issue order only for D <= NB");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -571,17 +578,32 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     gemm_fp8::wait_lgkm<0>();
     __syncthreads();
     const int rows = r1 - r0;
-    for (int e = threadIdx.x; e < M * rows; e += 64 * W) {
-        const int m = e / rows, r = e - m * rows;
-        y[(int64_t)m * ldy + r0 + r] = out[m * per + r];
+    if constexpr (CAND) {
+        for (int m = wave; m < M; m += W) {
+            float best = -__builtin_inff();
+            uint32_t id = 0xffffffffu;
+            for (int r = lane; r < rows; r += 64) pick_bf16(best, id, out[m * per + r], (uint32_t)(r0 + r));
+            wave_pick(best, id);
+            if (lane == 0) {
+                uint32_t* pp = part + ((int64_t)m * gridDim.x + blockIdx.x) * 2;
+                pp[0] = __builtin_bit_cast(uint32_t, best);
+                pp[1] = id;
+            }
+        }
+    } else {
+        for (int e = threadIdx.x; e < M * rows; e += 64 * W) {
+            const int m = e / rows, r = e - m * rows;
+            y[(int64_t)m * ldy + r0 + r] = out[m * per + r];
+        }
     }
 }
 
-// per: rows (pairs for SW) of each workgroup's range.
-template <int NB, int D, bool SW>
+// per: rows (pairs for SW) of each workgroup's range.  CAND: part as
+// small_m_stream_kernel describes (y unused).
+template <int NB, int D, bool SW, bool CAND = false>
 hipError_t launch_stream(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy,
-                         int M, int N, int K, int per, hipStream_t stream) {
-    auto kern = small_m_stream_kernel<NB, D, SW>;
+                         int M, int N, int K, int per, hipStream_t stream, uint32_t* part = nullptr) {
+    auto kern = small_m_stream_kernel<NB, D, SW, CAND>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     if (attr != hipSuccess) return attr;
@@ -593,7 +615,7 @@ hipError_t launch_stream(const uint16_t* x, const uint8_t* codes, const float* s
     const int pieces = (per + cap - 1) / cap;
     const int pr = (per + pieces - 1) / pieces;
     hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kStreamWaves), lds, stream, x, codes, scales, y, ldy, M, N, K,
-                       per, pr);
+                       per, pr, part);
     return hipGetLastError();
 }
 
@@ -623,28 +645,56 @@ int stream_nb(int K) {
 // and 10 rows (6-12% slower: fewer code bytes in flight per CU).
 constexpr int kStreamRowsPerCu = 32;
 
+namespace {
+
+// Whether launch_small_m runs the row-range kernel for this geometry (its
+// blocks per wave in nb, rows per workgroup for the plain form in per_rows).
+bool stream_form(int M, int N, int K, int& nb, int& per_rows) {
+    const int cus = compute_units();
+    nb = stream_nb(K);
+    if (!nb || N < kStreamRowsPerCu * cus || (int64_t)N * K >= ((int64_t)1 << 31)) return false;
+    per_rows = (N + cus - 1) / cus;
+    const int fixed = nb == 4 ? stream_lds_fixed<4, 4>() : nb == 5 ? stream_lds_fixed<5, 5>()
+                                                                     : stream_lds_fixed<9, 7>();
+    return (int64_t)fixed + (int64_t)per_rows * M * 2 <= kMaxLds;
+}
+
+}  // namespace
+
+bool small_m_candidates_supported(int M, int N, int K) {
+    int nb = 0, per = 0;
+    return M >= 1 && M <= kMaxM && stream_form(M, N, K, nb, per);
+}
+
+hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
+                                     int K, uint32_t* part, int64_t& groups, hipStream_t stream) {
+    int nb = 0, per = 0;
+    if (M < 1 || M > kMaxM || !stream_form(M, N, K, nb, per)) return hipErrorNotSupported;
+    groups = (N + per - 1) / per;
+    if (nb == 4)
+        return launch_stream<4, 4, false, true>(x, codes, scales, nullptr, 0, M, N, K, per, stream, part);
+    if (nb == 5)
+        return launch_stream<5, 5, false, true>(x, codes, scales, nullptr, 0, M, N, K, per, stream, part);
+    return launch_stream<9, 7, false, true>(x, codes, scales, nullptr, 0, M, N, K, per, stream, part);
+}
+
 // The kernel is chosen from the weight geometry alone, the same for the plain
 // and the SwiGLU form, so the SwiGLU outputs are those of the plain form's
 // sums.
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                           int64_t ldy, int M, int N, int K, int /*split*/, bool swiglu, hipStream_t stream) {
     const int cus = compute_units();
-    const int nb = stream_nb(K);
-    if (nb && N >= kStreamRowsPerCu * cus && (int64_t)N * K < ((int64_t)1 << 31)) {
-        const int per_rows = (N + cus - 1) / cus;
-        const int fixed = nb == 4 ? stream_lds_fixed<4, 4>() : nb == 5 ? stream_lds_fixed<5, 5>()
-                                                                         : stream_lds_fixed<9, 7>();
-        if ((int64_t)fixed + (int64_t)per_rows * M * 2 <= kMaxLds) {
-            if (swiglu) {
-                const int per = (N / 2 + cus - 1) / cus;
-                if (nb == 4) return launch_stream<4, 4, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-                if (nb == 5) return launch_stream<5, 5, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-                return launch_stream<9, 7, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-            }
-            if (nb == 4) return launch_stream<4, 4, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
-            if (nb == 5) return launch_stream<5, 5, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
-            return launch_stream<9, 7, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
+    int nb = 0, per_rows = 0;
+    if (stream_form(M, N, K, nb, per_rows)) {
+        if (swiglu) {
+            const int per = (N / 2 + cus - 1) / cus;
+            if (nb == 4) return launch_stream<4, 4, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+            if (nb == 5) return launch_stream<5, 5, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+            return launch_stream<9, 7, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
         }
+        if (nb == 4) return launch_stream<4, 4, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
+        if (nb == 5) return launch_stream<5, 5, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
+        return launch_stream<9, 7, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
     }
     // Rows per workgroup: about two workgroups per CU, 8..16 rows (4..8
     // pairs), so every CU streams about the same number of rows in one round

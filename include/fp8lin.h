@@ -360,7 +360,10 @@ int fp8lin_merge_candidates(const double* gathered, int64_t ranks, int64_t rows,
  * Where fp8lin_linear runs its ring GEMV (M <= 2, 16-byte aligned x and
  * codes, K % 16 == 0 and K <= 9216, K <= 5120 at M = 2) the GEMV's epilogue
  * emits one {max, column} pair per workgroup and no logits are written
- * (src/dual_path.cu:37-55 fused into the projection); otherwise the logits
+ * (src/dual_path.cu:37-55 fused into the projection); where it runs the
+ * small-M matrix-core kernel's row-range form (3..16 rows, or 2 at
+ * K > 5120, against at least 32 weight rows per compute unit) that kernel
+ * does the same, one pair per workgroup and row; otherwise the logits
  * [M, N] and the chunk pairs go to the workspace.  Workspace: the bytes
  * below, 16-byte aligned, any content.  Requirements of fp8lin_linear and
  * fp8lin_vocab_candidates.
@@ -395,7 +398,9 @@ int fp8lin_linear_candidates_static(const uint16_t* x, const uint8_t* codes, con
  * out equals fp8lin_vocab_candidates of fp8lin_engine_linear's output for
  * the same options (so rows 2..8 take the small-M path when the options
  * select it).  On the FP8 GEMV branch without a bias this is
- * fp8lin_linear_candidates (no logits written).  Workspace: the bytes below
+ * fp8lin_linear_candidates, and the tensor-small branch without a bias takes
+ * the small-M kernel's candidate form where its row-range form runs (no
+ * logits written in either).  Workspace: the bytes below
  * (the logits, the candidate pairs and the branch's own workspace), 16-byte
  * aligned.
  */

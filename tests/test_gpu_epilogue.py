@@ -232,7 +232,7 @@ def _head(fp8lin, gpu, m, n, k, seed):
     return x, codes, scales
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 9, 64])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 9, 16, 64])
 @pytest.mark.parametrize("n,k", [(1000, 256), (4097, 5120), (31040, 4096), (777, 10240), (300, 6144)])
 def test_linear_candidates_equals_unfused(fp8lin, gpu, oracle, m, n, k):
     """The head in one call (src/speculative.cpp:25-27) is bit-identical to
@@ -290,9 +290,54 @@ def test_linear_candidates_ties_and_nan(fp8lin, gpu, oracle, m):
     assert (fp8lin.merge_candidates(got.unsqueeze(0).contiguous()) == -1).all()
 
 
-def test_linear_candidates_graph_replay(fp8lin, gpu):
-    """Captured head: every replay matches the eager call on the new input."""
-    x, codes, scales = _head(fp8lin, gpu, 1, 31040, 4096, seed=21)
+@pytest.mark.parametrize("m", [3, 8, 16])
+def test_small_m_candidates_ties_and_nan(fp8lin, gpu, oracle, m):
+    """3..16 rows against a wide head (8208 rows: the small-M row-range
+    kernel, 33 rows per workgroup in pieces of 11) take that kernel's candidate
+    form: per workgroup and activation row one pair, then one finishing
+    workgroup per row.
+    Equal weight rows in different workgroups give tied logits and the
+    smallest row id wins; the result equals vocabulary_candidates of
+    fp8_linear and the oracle's candidates; a NaN scale makes every row's
+    candidate +inf.  Engine::local_candidates on the tensor-small branch
+    (3 and 8 rows) takes the same candidate form."""
+    n, k = 8208, 4096
+    rng = np.random.default_rng(40 + m)
+    codes_np = (rng.integers(0, 127, (n, k)) | (rng.integers(0, 2, (n, k)) << 7)).astype(np.uint8)
+    tied = [7, 3300, 6001, 8207]
+    codes_np[tied] = codes_np[4500]
+    scales_np = (rng.random((n, k // 128)) * 0.01 + 0.001).astype(np.float32)
+    scales_np[tied] = scales_np[4500] = 1.0
+    x_np = rand_bf16(rng, (m, k))
+    x_np[1] = x_np[0] ^ 0x8000          # one of rows 0 and 1 sees the tied rows as its maximum
+    x = up(x_np, gpu)
+    codes, scales = up(codes_np, gpu), up(scales_np, gpu)
+    assert fp8lin.lib().fp8lin_linear_candidates_workspace_bytes(m, n, k) > 0
+    want = fp8lin.vocabulary_candidates(fp8lin.fp8_linear(x, codes, scales), 0)
+    got = fp8lin.linear_candidates(x, codes, scales, 0)
+    assert torch.equal(got, want)
+    assert 7 in got[:2, 1].long().tolist()
+    logits = oracle.linear(bits(x), codes_np, scales_np)
+    assert np.array_equal(got.cpu().numpy(), oracle.vocab_candidates(logits, 0))
+    if m <= 8:
+        # Engine::local_candidates on the tensor-small branch: the same kernel's
+        # candidate form, the same result
+        eng = fp8lin.LinearEngine(fp8lin.LinearOptions(fp8_tensor_small=True))
+        eng.add("lm_head.weight", codes, scales)
+        ec, path = eng.local_candidates(x, "lm_head", 0, return_path=True)
+        assert path == fp8lin.PATH_TENSOR_SMALL
+        assert torch.equal(ec, got)
+        assert torch.equal(ec, fp8lin.vocabulary_candidates(eng.linear(x, "lm_head"), 0))
+    scales_np[5000, 3] = np.nan
+    got = fp8lin.linear_candidates(x, codes, up(scales_np, gpu), 0)
+    assert torch.isinf(got[:, 0]).all()
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_linear_candidates_graph_replay(fp8lin, gpu, m):
+    """Captured head: every replay matches the eager call on the new input
+    (M = 1: the GEMV candidate form; M = 4: the small-M row-range form)."""
+    x, codes, scales = _head(fp8lin, gpu, m, 31040, 4096, seed=21)
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
@@ -303,7 +348,7 @@ def test_linear_candidates_graph_replay(fp8lin, gpu):
             out = fp8lin.linear_candidates(x, codes, scales, 62080)
     for i in range(4):
         if i:
-            x.copy_(fp8lin.gen_activations(1, 4096, seed=100 + i, tag=2, device=gpu))
+            x.copy_(fp8lin.gen_activations(m, 4096, seed=100 + i, tag=2, device=gpu))
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
