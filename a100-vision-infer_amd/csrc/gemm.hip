@@ -123,14 +123,18 @@ bool fp8_kernel_ok(const uint16_t* x, const void* w, int S, int64_t ldy, int M, 
 }
 
 // A few weight rows (N <= kSkinnyRows, as the GDN in_proj_all group's 48 BF16
-// rows): 256x256 tiles would run M/256 workgroups, so the GEMV's prefill form
-// takes them (8 activation rows per workgroup row, K split over 4 waves).
-// N counts weight rows in both forms, so the fused SwiGLU GEMM and the plain
-// GEMM of one weight take the same kernel (and give the same sums).
+// rows): 256x256 tiles would run M/256 workgroups, so the skinny MFMA kernel
+// takes them (16 x 16 output tiles, K split over 4 waves; skinny.hip), or,
+// for K % 32 != 0 or unaligned operands, the GEMV's prefill form (8
+// activation rows per workgroup row).  N counts weight rows in both forms, so
+// the fused SwiGLU GEMM and the plain GEMM of one weight take the same kernel
+// (and give the same sums).
 bool skinny(int M, int N, bool /*swiglu*/) { return M > 8 && N <= kSkinnyRows; }
 
 hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,
                          int M, int N, int K, bool swiglu, hipStream_t stream) {
+    if (skinny_mfma_supported(x, w, scales != nullptr, S, M, N, K))
+        return launch_skinny_mfma(x, w, scales != nullptr, scales, S, y, ldy, M, N, K, swiglu, stream);
     const bool wide = K % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                       reinterpret_cast<uintptr_t>(w) % 16 == 0;
     return launch_gemv_rows(x, w, scales != nullptr, scales, S, y, ldy, M, N, K, wide, swiglu, stream);

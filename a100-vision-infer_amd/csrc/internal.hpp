@@ -21,6 +21,11 @@ hipError_t launch_gemv_swiglu(const uint16_t* x, const uint8_t* codes, const flo
 // GEMV over blocks of 8 activation rows, four waves splitting K (the prefill
 // form for N <= kSkinnyRows, where 256x256 MFMA tiles leave most CUs idle).
 constexpr int kSkinnyRows = 256;
+// MFMA form for few weight rows (skinny.hip): 16 x 16 output tiles, K split
+// over 4 waves; the requirements in skinny_mfma_supported.
+bool skinny_mfma_supported(const uint16_t* x, const void* w, bool fp8, int S, int64_t M, int64_t N, int64_t K);
+hipError_t launch_skinny_mfma(const uint16_t* x, const void* w, bool fp8, const float* scales, int S, uint16_t* y,
+                              int64_t ldy, int M, int N, int K, bool swiglu, hipStream_t stream);
 hipError_t launch_gemv_rows(const uint16_t* x, const void* w, bool fp8, const float* scales, int S, uint16_t* y,
                             int64_t ldy, int M, int N, int K, bool wide, bool swiglu, hipStream_t stream);
 
