@@ -424,7 +424,7 @@ size_t linear_candidates_ws(int64_t M, int64_t N) {
 }
 
 // Whether fp8lin_linear runs the small-M matrix-core kernel for this call
-// (3..8 rows, or 2 at K > 5120, through linear_small_m; 9..16 rows through
+// (3..8 rows, or 2 at K > 5120, through linear_small_m; 9..32 rows through
 // the GEMM dispatch's mid-rows rule).
 bool linear_runs_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t M, int64_t N, int64_t K) {
     return linear_small_m(x, codes, S, M, N, K) || fp8lin::gemm_mid_rows(x, codes, (int)S, M, N, K);
@@ -442,7 +442,7 @@ void linear_candidates_impl(const uint16_t* x, const uint8_t* codes, const float
     // where fp8lin_linear runs the small-M row-range kernel: its candidate
     // form (the same logits, never stored; at most CUs pairs per row) and one
     // finishing workgroup per row
-    if (M <= 16 && linear_runs_small_m(x, codes, S, M, N, K) &&
+    if (M <= 32 && linear_runs_small_m(x, codes, S, M, N, K) &&
         fp8lin::small_m_candidates_supported((int)M, (int)N, (int)K)) {
         auto* part = static_cast<uint32_t*>(ws);
         int64_t groups = 0;

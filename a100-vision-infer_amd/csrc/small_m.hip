@@ -56,6 +56,7 @@ using gemm_fp8::wait_vm;
 
 constexpr int kRowX = 1040;  // LDS stride of an activation row (1 KiB + 16 B)
 constexpr int kMaxM = 16;    // rows of the 16x16x32 MFMA tile's activation side
+constexpr int kStreamMaxM = 32;  // two tiles in the row-range kernel
 constexpr int kMaxLds = 160 * 1024;
 
 __device__ __forceinline__ int sw(int r) { return (r >> 1) & 7; }
@@ -365,13 +366,15 @@ hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, 
 // wave partials in wave order.  It depends on K only (not on the row range),
 // so split 1 and 4 and every workgroup count give the same bits.
 constexpr int kStreamWaves = 8;
-constexpr int kStreamRed = 2 * kStreamWaves * 1024;  // two buffers of 8 waves x 16 x 16 floats
+// Partial-sum exchange of T 16-row activation tiles: two buffers of 8 waves x
+// 16 T x 16 floats.
+constexpr int stream_red(int T) { return 2 * kStreamWaves * 1024 * T; }
 
 template <int NB>
 constexpr int stream_scale_dmas() { return (16 * NB + 63) / 64; }
-template <int NB, int D>
+template <int NB, int D, int T = 1>
 constexpr int stream_lds_fixed() {
-    return kStreamWaves * D * 2048 + kStreamWaves * 3 * stream_scale_dmas<NB>() * 256 + kStreamRed;
+    return kStreamWaves * D * 2048 + kStreamWaves * 3 * stream_scale_dmas<NB>() * 256 + stream_red(T);
 }
 constexpr int floordiv(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 
@@ -388,7 +391,7 @@ constexpr int floordiv(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / 
 // its row range (the logits fp8lin_linear would store; larger value, then
 // smaller column, NaN as +inf) to pair m * gridDim + blockIdx of part, the
 // layout of the two-stage candidates' chunk pairs.
-template <int NB, int D, bool SW, bool CAND>
+template <int NB, int D, bool SW, bool CAND, int T>
 __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const uint16_t* __restrict__ x,
                                                                           const uint8_t* __restrict__ codes,
                                                                           const float* __restrict__ scales,
@@ -415,7 +418,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     const uint32_t o_codes = (uint32_t)(wave * D * 2048);
     const uint32_t o_sc = (uint32_t)(W * D * 2048 + wave * 3 * SC * 256);
     const uint32_t o_red = (uint32_t)(W * D * 2048 + W * 3 * SC * 256);
-    const uint32_t o_out = o_red + kStreamRed;
+    const uint32_t o_out = o_red + stream_red(T);
 
     const i32x4 dw = make_desc(codes, (uint32_t)((int64_t)N * K));
     const i32x4 ds = make_desc(scales, (uint32_t)((int64_t)N * KB * 4));
@@ -478,18 +481,23 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         }
     };
 
-    // Activation fragments of the own blocks, A operand layout: lane (m = row,
-    // K sub-range g); K offset within a block 16g + 64(f/2) + 8(f%2), the same
-    // permutation as the code words the lane converts.  Rows >= M read zeros.
-    u32x4 xr[NB][4];
+    // Activation fragments of the own blocks, A operand layout of tile tt:
+    // lane (m = 16 tt + row, K sub-range g); K offset within a block 16g +
+    // 64(f/2) + 8(f%2), the same permutation as the code words the lane
+    // converts.  Rows >= M read zeros.
+    u32x4 xr[NB][4 * T];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
         const int blk = wave + W * j;
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-            const int k = blk * 128 + 16 * g + 64 * (f >> 1) + 8 * (f & 1);
-            const uint32_t off = row < M && blk < KB ? (uint32_t)((row * K + k) * 2) : kBufferOob;
-            asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(xr[j][f]) : "v"(off), "s"(dx));
+        for (int tt = 0; tt < T; ++tt) {
+            const int mr = 16 * tt + row;
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                const int k = blk * 128 + 16 * g + 64 * (f >> 1) + 8 * (f & 1);
+                const uint32_t off = mr < M && blk < KB ? (uint32_t)((mr * K + k) * 2) : kBufferOob;
+                asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(xr[j][4 * tt + f]) : "v"(off), "s"(dx));
+            }
         }
     }
     issue_scales(0);
@@ -498,13 +506,19 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
     for (int t = 0; t < D; ++t) issue_codes(t / NB, t % NB, t);
     wait_vm<2 * (D - 1)>();  // the activations, the first two scale pieces, step 0's codes
 #pragma unroll
-    for (int j = 0; j < NB; ++j) asm volatile("" : "+v"(xr[j][0]), "+v"(xr[j][1]), "+v"(xr[j][2]), "+v"(xr[j][3]));
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt)
+            asm volatile("" : "+v"(xr[j][4 * tt]), "+v"(xr[j][4 * tt + 1]), "+v"(xr[j][4 * tt + 2]),
+                         "+v"(xr[j][4 * tt + 3]));
     float* red = reinterpret_cast<float*>(lds + o_red);
     uint16_t* out = reinterpret_cast<uint16_t*>(lds + o_out);
 
     int sbase = 0;  // (p * NB) % D
     for (int p = 0; p < np; ++p) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4 acc[T];
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) acc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         const uint32_t sbuf = o_sc + (uint32_t)((p % 3) * SC * 256);
         [&]<int... J>(std::integer_sequence<int, J...>) __attribute__((always_inline)) {
             ([&]() __attribute__((always_inline)) {
@@ -528,12 +542,15 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
                     dequant4(cw.y, s, wv[2], wv[3]);
                     dequant4(cw.z, s, wv[4], wv[5]);
                     dequant4(cw.w, s, wv[6], wv[7]);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xr[j][2 * h]),
-                                                                   as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc,
-                                                                   0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xr[j][2 * h + 1]),
-                                                                   as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc,
-                                                                   0, 0, 0);
+#pragma unroll
+                    for (int tt = 0; tt < T; ++tt) {
+                        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, xr[j][4 * tt + 2 * h]), as_bf16x8(wv[0], wv[1], wv[2], wv[3]),
+                            acc[tt], 0, 0, 0);
+                        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, xr[j][4 * tt + 2 * h + 1]),
+                            as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc[tt], 0, 0, 0);
+                    }
                 }
                 // the slot's codes and the scale are in registers: refill
                 gemm_fp8::wait_lgkm<0>();
@@ -543,33 +560,41 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         }(std::make_integer_sequence<int, NB>{});
         sbase += NB % D;
         sbase = sbase >= D ? sbase - D : sbase;
-        // acc[i] = C[m = 4g + i][n = row]; lanes with 4g < M hold rows m < M
-        float* rb = red + (p & 1) * (W * 256);
-        if (4 * g < M) {
+        // acc[tt][i] = C[m = 16 tt + 4g + i][n = row]; only rows m < M are kept
+        constexpr int RW = 256 * T;  // floats per wave in a buffer
+        float* rb = red + (p & 1) * (W * RW);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) rb[wave * 256 + (4 * g + i) * 16 + row] = acc[i];
+        for (int tt = 0; tt < T; ++tt) {
+            if (16 * tt + 4 * g < M) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rb[wave * RW + (16 * tt + 4 * g + i) * 16 + row] = acc[tt][i];
+            }
         }
         // Two buffers: wave (p % 8) reads buffer p & 1 before it reaches the
         // barrier that ends piece p + 1, after which buffer p & 1 is rewritten.
         gemm_fp8::wait_lgkm<0>();
         barrier();
-        if (wave == (p & (W - 1)) && 4 * g < M && (!SW || row < 8)) {
+        if (wave == (p & (W - 1)) && (!SW || row < 8)) {
             const int n0 = piece(p);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = 4 * g + i;
-                float t = rb[m * 16 + row];
+            for (int tt = 0; tt < T; ++tt) {
+                if (16 * tt + 4 * g >= M) continue;
 #pragma unroll
-                for (int w = 1; w < W; ++w) t = t + rb[w * 256 + m * 16 + row];
-                uint16_t v = f32_to_bf16_bits(t);
-                if constexpr (SW) {
-                    // the up row of this pair sits in slot row + 8
-                    float u = rb[m * 16 + row + 8];
+                for (int i = 0; i < 4; ++i) {
+                    const int m = 16 * tt + 4 * g + i;
+                    float t = rb[m * 16 + row];
 #pragma unroll
-                    for (int w = 1; w < W; ++w) u = u + rb[w * 256 + m * 16 + row + 8];
-                    v = swiglu_bf16_bits(v, f32_to_bf16_bits(u));
+                    for (int w = 1; w < W; ++w) t = t + rb[w * RW + m * 16 + row];
+                    uint16_t v = f32_to_bf16_bits(t);
+                    if constexpr (SW) {
+                        // the up row of this pair sits in slot row + 8
+                        float u = rb[m * 16 + row + 8];
+#pragma unroll
+                        for (int w = 1; w < W; ++w) u = u + rb[w * RW + m * 16 + row + 8];
+                        v = swiglu_bf16_bits(v, f32_to_bf16_bits(u));
+                    }
+                    if (m < M && row < pr && n0 + row < r1) out[m * per + (n0 - r0) + row] = v;
                 }
-                if (m < M && row < pr && n0 + row < r1) out[m * per + (n0 - r0) + row] = v;
             }
         }
     }
@@ -600,16 +625,16 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
 
 // per: rows (pairs for SW) of each workgroup's range.  CAND: part as
 // small_m_stream_kernel describes (y unused).
-template <int NB, int D, bool SW, bool CAND = false>
+template <int NB, int D, bool SW, bool CAND, int T>
 hipError_t launch_stream(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy,
-                         int M, int N, int K, int per, hipStream_t stream, uint32_t* part = nullptr) {
-    auto kern = small_m_stream_kernel<NB, D, SW, CAND>;
+                         int M, int N, int K, int per, hipStream_t stream, uint32_t* part) {
+    auto kern = small_m_stream_kernel<NB, D, SW, CAND, T>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     if (attr != hipSuccess) return attr;
     const int units = SW ? N / 2 : N;
     const int groups = (units + per - 1) / per;
-    const size_t lds = (size_t)stream_lds_fixed<NB, D>() + (size_t)per * M * 2;
+    const size_t lds = (size_t)stream_lds_fixed<NB, D, T>() + (size_t)per * M * 2;
     // pieces of at most 16 rows (8 pairs), as equal as the range allows
     const int cap = SW ? 8 : 16;
     const int pieces = (per + cap - 1) / cap;
@@ -649,33 +674,54 @@ namespace {
 
 // Whether launch_small_m runs the row-range kernel for this geometry (its
 // blocks per wave in nb, rows per workgroup for the plain form in per_rows).
+// 17..32 activation rows take two 16-row tiles, whose activation registers
+// (8 NB dwordx4 per lane) fit beside the rest for NB <= 5 (K <= 5120).
 bool stream_form(int M, int N, int K, int& nb, int& per_rows) {
     const int cus = compute_units();
     nb = stream_nb(K);
-    if (!nb || N < kStreamRowsPerCu * cus || (int64_t)N * K >= ((int64_t)1 << 31)) return false;
+    if (!nb || M < 1 || M > kStreamMaxM || N < kStreamRowsPerCu * cus || (int64_t)N * K >= ((int64_t)1 << 31))
+        return false;
+    if (M > kMaxM && nb > 5) return false;
     per_rows = (N + cus - 1) / cus;
-    const int fixed = nb == 4 ? stream_lds_fixed<4, 4>() : nb == 5 ? stream_lds_fixed<5, 5>()
-                                                                     : stream_lds_fixed<9, 7>();
+    const int fixed = M > kMaxM ? (nb == 4 ? stream_lds_fixed<4, 4, 2>() : stream_lds_fixed<5, 5, 2>())
+                      : nb == 4 ? stream_lds_fixed<4, 4>()
+                      : nb == 5 ? stream_lds_fixed<5, 5>()
+                                : stream_lds_fixed<9, 7>();
     return (int64_t)fixed + (int64_t)per_rows * M * 2 <= kMaxLds;
+}
+
+// The row-range kernel for stream_form's geometry: per rows (pairs for SW)
+// per workgroup, one or two activation tiles.
+template <bool SW, bool CAND>
+hipError_t dispatch_stream(int nb, const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                           int64_t ldy, int M, int N, int K, int per, hipStream_t stream, uint32_t* part) {
+    if (M > kMaxM) {
+        if (nb == 4) return launch_stream<4, 4, SW, CAND, 2>(x, codes, scales, y, ldy, M, N, K, per, stream, part);
+        return launch_stream<5, 5, SW, CAND, 2>(x, codes, scales, y, ldy, M, N, K, per, stream, part);
+    }
+    if (nb == 4) return launch_stream<4, 4, SW, CAND, 1>(x, codes, scales, y, ldy, M, N, K, per, stream, part);
+    if (nb == 5) return launch_stream<5, 5, SW, CAND, 1>(x, codes, scales, y, ldy, M, N, K, per, stream, part);
+    return launch_stream<9, 7, SW, CAND, 1>(x, codes, scales, y, ldy, M, N, K, per, stream, part);
 }
 
 }  // namespace
 
+bool small_m_stream_supported(int M, int N, int K) {
+    int nb = 0, per = 0;
+    return stream_form(M, N, K, nb, per);
+}
+
 bool small_m_candidates_supported(int M, int N, int K) {
     int nb = 0, per = 0;
-    return M >= 1 && M <= kMaxM && stream_form(M, N, K, nb, per);
+    return stream_form(M, N, K, nb, per);
 }
 
 hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
                                      int K, uint32_t* part, int64_t& groups, hipStream_t stream) {
     int nb = 0, per = 0;
-    if (M < 1 || M > kMaxM || !stream_form(M, N, K, nb, per)) return hipErrorNotSupported;
+    if (!stream_form(M, N, K, nb, per)) return hipErrorNotSupported;
     groups = (N + per - 1) / per;
-    if (nb == 4)
-        return launch_stream<4, 4, false, true>(x, codes, scales, nullptr, 0, M, N, K, per, stream, part);
-    if (nb == 5)
-        return launch_stream<5, 5, false, true>(x, codes, scales, nullptr, 0, M, N, K, per, stream, part);
-    return launch_stream<9, 7, false, true>(x, codes, scales, nullptr, 0, M, N, K, per, stream, part);
+    return dispatch_stream<false, true>(nb, x, codes, scales, nullptr, 0, M, N, K, per, stream, part);
 }
 
 // The kernel is chosen from the weight geometry alone, the same for the plain
@@ -686,16 +732,12 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
     const int cus = compute_units();
     int nb = 0, per_rows = 0;
     if (stream_form(M, N, K, nb, per_rows)) {
-        if (swiglu) {
-            const int per = (N / 2 + cus - 1) / cus;
-            if (nb == 4) return launch_stream<4, 4, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-            if (nb == 5) return launch_stream<5, 5, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-            return launch_stream<9, 7, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-        }
-        if (nb == 4) return launch_stream<4, 4, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
-        if (nb == 5) return launch_stream<5, 5, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
-        return launch_stream<9, 7, false>(x, codes, scales, y, ldy, M, N, K, per_rows, stream);
+        if (swiglu)
+            return dispatch_stream<true, false>(nb, x, codes, scales, y, ldy, M, N, K, (N / 2 + cus - 1) / cus,
+                                                stream, nullptr);
+        return dispatch_stream<false, false>(nb, x, codes, scales, y, ldy, M, N, K, per_rows, stream, nullptr);
     }
+    if (M > kMaxM) return hipErrorNotSupported;
     // Rows per workgroup: about two workgroups per CU, 8..16 rows (4..8
     // pairs), so every CU streams about the same number of rows in one round
     // (16-row workgroups left the 5120-row down projection at 1.25 per CU,

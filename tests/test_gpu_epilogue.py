@@ -232,12 +232,13 @@ def _head(fp8lin, gpu, m, n, k, seed):
     return x, codes, scales
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 9, 16, 64])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 9, 16, 24, 64])
 @pytest.mark.parametrize("n,k", [(1000, 256), (4097, 5120), (31040, 4096), (777, 10240), (300, 6144)])
 def test_linear_candidates_equals_unfused(fp8lin, gpu, oracle, m, n, k):
     """The head in one call (src/speculative.cpp:25-27) is bit-identical to
     vocabulary_candidates(fp8_linear(x, W), offset) on the GEMV paths (128-bit
-    and byte loads) and the M > 8 GEMM path."""
+    and byte loads), the small-M row-range kernel's candidate form (9..32
+    rows against 31040 rows) and the M > 8 GEMM path."""
     x, codes, scales = _head(fp8lin, gpu, m, n, k, seed=m + n)
     offset = 124160
     want = fp8lin.vocabulary_candidates(fp8lin.fp8_linear(x, codes, scales, True), offset)
@@ -290,9 +291,9 @@ def test_linear_candidates_ties_and_nan(fp8lin, gpu, oracle, m):
     assert (fp8lin.merge_candidates(got.unsqueeze(0).contiguous()) == -1).all()
 
 
-@pytest.mark.parametrize("m", [3, 8, 16])
+@pytest.mark.parametrize("m", [3, 8, 16, 17, 32])
 def test_small_m_candidates_ties_and_nan(fp8lin, gpu, oracle, m):
-    """3..16 rows against a wide head (8208 rows: the small-M row-range
+    """3..32 rows against a wide head (8208 rows: the small-M row-range
     kernel, 33 rows per workgroup in pieces of 11) take that kernel's candidate
     form: per workgroup and activation row one pair, then one finishing
     workgroup per row.
