@@ -143,16 +143,16 @@ hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, 
 // 9..16 activation rows of a block-FP8 weight of more than 1024 rows: the
 // small-M matrix-core kernel (small_m.hip), whose 16x16 MFMA tile holds all
 // of them, streams the codes once with each dequantized once; a GEMM tile
-// would be at least seven eighths padding.  17..32 rows where its row-range
-// form runs with two activation tiles (at least 32 weight rows per CU, K <=
-// 5120).  Its geometry limits are those of the decode routing (block scales
-// [N, K/128], 16-byte aligned x and codes).
+// would be at least seven eighths padding.  17..32 rows in its row-range
+// form with two activation tiles (at least 32 weight rows per CU, K <=
+// 5120), else in two passes of at most 16 rows.  Its geometry limits are
+// those of the decode routing (block scales [N, K/128], 16-byte aligned x
+// and codes).
 bool mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K) {
     const int64_t lim = (int64_t)1 << 31;
-    const bool geo = M > 8 && N > 1024 && K % 128 == 0 && S == K / 128 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-                     reinterpret_cast<uintptr_t>(w) % 16 == 0 && 16 * K < lim && N * S * 4 < lim && M * K * 2 < lim;
-    if (!geo || M > 32) return false;
-    return M <= 16 || small_m_stream_supported((int)M, (int)N, (int)K);
+    return M > 8 && M <= 32 && N > 1024 && K % 128 == 0 && S == K / 128 &&
+           reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 && 16 * K < lim &&
+           N * S * 4 < lim && M * K * 2 < lim;
 }
 
 }  // namespace

@@ -33,8 +33,8 @@ hipError_t launch_gemv_rows(const uint16_t* x, const void* w, bool fp8, const fl
 // XCDs (cached per device): the grid of the persistent kernels (gemm.hip).
 int compute_units();
 
-// Small-M matrix-core kernel, 2 <= M <= 16 (<= 32 where
-// small_m_stream_supported), K % 128 == 0, block scales
+// Small-M matrix-core kernel, 2 <= M <= 32 (17..32: the two-tile row-range
+// form where small_m_candidates_supported, else two passes), K % 128 == 0, block scales
 // (small_m.hip).  The K partition is the kernel's own, so split 1 and 4 give
 // the same bits; no workspace.  M * K * 2 and 16 * K must be below 2^31.
 // swiglu: N weight rows (gate [0, N/2), up [N/2, N)), y is [M, N/2], bit-equal
@@ -47,10 +47,9 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
 // per workgroup and activation row to one {value bits, column} pair, part
 // [M][groups] pairs (groups <= CUs), for launch_candidates_finish.  No logits
 // written.
+// Supported: at least 32 weight rows per CU and K / 128 in 25..40 (or 65..72
+// for M <= 16), 1 <= M <= 32.
 bool small_m_candidates_supported(int M, int N, int K);
-// Whether launch_small_m (either form) runs the row-range kernel: at least 32
-// weight rows per CU and K / 128 in 25..40 (or 65..72 for M <= 16), M <= 32.
-bool small_m_stream_supported(int M, int N, int K);
 hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
                                      int K, uint32_t* part, int64_t& groups, hipStream_t stream);
 // out[2m] = value, out[2m + 1] = column + offset of the best of the `chunks`

@@ -706,10 +706,6 @@ hipError_t dispatch_stream(int nb, const uint16_t* x, const uint8_t* codes, cons
 
 }  // namespace
 
-bool small_m_stream_supported(int M, int N, int K) {
-    int nb = 0, per = 0;
-    return stream_form(M, N, K, nb, per);
-}
 
 bool small_m_candidates_supported(int M, int N, int K) {
     int nb = 0, per = 0;
@@ -737,7 +733,18 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
                                                 stream, nullptr);
         return dispatch_stream<false, false>(nb, x, codes, scales, y, ldy, M, N, K, per_rows, stream, nullptr);
     }
-    if (M > kMaxM) return hipErrorNotSupported;
+    if (M > kMaxM) {
+        // 17..32 rows off the row-range form: two passes over row blocks of
+        // at least 2 rows, each streaming the codes once (at M = 32, 13.4 +
+        // 13.4 us on QKV-gate and 17.9 + 17.9 on down, against 28.5 and 36
+        // in the split-K GEMM and 90 and 144 in the GEMM without workspace)
+        if (M > kStreamMaxM) return hipErrorNotSupported;
+        const int m0 = M - kMaxM >= 2 ? kMaxM : M - 2;
+        const hipError_t e = launch_small_m(x, codes, scales, y, ldy, m0, N, K, 1, swiglu, stream);
+        if (e != hipSuccess) return e;
+        return launch_small_m(x + (int64_t)m0 * K, codes, scales, y + (int64_t)m0 * ldy, ldy, M - m0, N, K, 1,
+                              swiglu, stream);
+    }
     // Rows per workgroup: about two workgroups per CU, 8..16 rows (4..8
     // pairs), so every CU streams about the same number of rows in one round
     // (16-row workgroups left the 5120-row down projection at 1.25 per CU,

@@ -349,8 +349,8 @@ def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(128, 512, 1024
         small_copies["in_proj_all"] = [fp8lin.gen_weights(8240, 5120, seed=0, tag=400 + c, device=dev)
                                        for c in range(13)]
     for name, n, k in (SHAPES + [("in_proj_all", 8240, 5120)] if "small" in sections else []):
-        # M = 16: fp8lin_linear only (fp8_tensor_small takes 2..8 rows)
-        for m in (2, 4, 8, 16):
+        # M = 16 and 32: fp8lin_linear only (fp8_tensor_small takes 2..8 rows)
+        for m in (2, 4, 8, 16, 32):
             x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
             y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
             ws = torch.empty(4 * 4 * m * n, dtype=torch.uint8, device=dev)

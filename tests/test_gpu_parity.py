@@ -694,13 +694,14 @@ def test_linear_small_m_rows(fp8lin, gpu, oracle, m, n, k):
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
 @pytest.mark.parametrize("m,n,k", [(9, 2056, 384), (16, 2056, 384), (12, 8208, 5120), (16, 8208, 4096),
                                    (13, 1040, 8704), (16, 8240, 8704), (17, 8208, 5120), (32, 8208, 4096),
-                                   (27, 8240, 3200)])
+                                   (27, 8240, 3200), (17, 5120, 8704), (32, 7168, 5120), (24, 2056, 384)])
 def test_linear_mid_rows(fp8lin, gpu, oracle, m, n, k):
     """fp8_linear with 9..16 rows against more than 1024 weight rows runs the
     small-M matrix-core kernel, whose 16x16 MFMA tile holds every row (the
     16-row workgroups at n = 2056 and 1040, the row-range form at n = 8208 and
     8240), instead of a mostly-padding GEMM tile; 17..32 rows run the
-    row-range form with two activation tiles (n >= 32 rows per CU, k <= 5120).  Every output against the
+    row-range form with two activation tiles (n >= 32 rows per CU, k <= 5120)
+    or two passes of at most 16 rows (15 + 2 at m = 17).  Every output against the
     FP64 oracle; the fused SwiGLU bit-equal to fused_swiglu(fp8_linear), with
     or without a workspace (none is needed); Engine::linear's FP8 GEMM branch
     asks for no workspace and gives the same bits; an unaligned view of x
