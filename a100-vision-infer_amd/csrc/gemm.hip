@@ -144,7 +144,7 @@ hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, 
 // small-M matrix-core kernel (small_m.hip), whose 16x16 MFMA tile holds all
 // of them, streams the codes once with each dequantized once; a GEMM tile
 // would be at least seven eighths padding.  17..32 rows in its row-range
-// form with two activation tiles (at least 32 weight rows per CU, K <=
+// form with two activation tiles (at least 24 weight rows per CU, K <=
 // 5120), else in two passes of at most 16 rows.  Its geometry limits are
 // those of the decode routing (block scales [N, K/128], 16-byte aligned x
 // and codes).

@@ -47,8 +47,8 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
 // per workgroup and activation row to one {value bits, column} pair, part
 // [M][groups] pairs (groups <= CUs), for launch_candidates_finish.  No logits
 // written.
-// Supported: at least 32 weight rows per CU and K / 128 in 25..40 (or 65..72
-// for M <= 16), 1 <= M <= 32.
+// Supported: K / 128 in 25..40 with at least 32 weight rows per CU for M <=
+// 16 (24 for 17..32 rows), or K / 128 in 65..72 with 32 rows per CU for M <= 16.
 bool small_m_candidates_supported(int M, int N, int K);
 hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
                                      int K, uint32_t* part, int64_t& groups, hipStream_t stream);

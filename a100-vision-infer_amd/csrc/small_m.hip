@@ -669,6 +669,11 @@ int stream_nb(int K) {
 // per CU) the 16-row workgroups stay faster, also against equal pieces of 14
 // and 10 rows (6-12% slower: fewer code bytes in flight per CU).
 constexpr int kStreamRowsPerCu = 32;
+// With two activation tiles every code byte feeds twice the MFMAs, and one
+// pass beats two passes of the 16-row workgroups from 24 rows per CU: the
+// 7168-row QKV-gate (28 per CU) at M = 17 / 24 / 32 in 15.2 / 16.9 / 18.8 us
+// against 22.1 / 22.4 / 23.7 (measured on MI355X).
+constexpr int kStreamRowsPerCuT2 = 24;
 
 namespace {
 
@@ -679,7 +684,8 @@ namespace {
 bool stream_form(int M, int N, int K, int& nb, int& per_rows) {
     const int cus = compute_units();
     nb = stream_nb(K);
-    if (!nb || M < 1 || M > kStreamMaxM || N < kStreamRowsPerCu * cus || (int64_t)N * K >= ((int64_t)1 << 31))
+    const int rows_per_cu = M > kMaxM ? kStreamRowsPerCuT2 : kStreamRowsPerCu;
+    if (!nb || M < 1 || M > kStreamMaxM || N < rows_per_cu * cus || (int64_t)N * K >= ((int64_t)1 << 31))
         return false;
     if (M > kMaxM && nb > 5) return false;
     per_rows = (N + cus - 1) / cus;
