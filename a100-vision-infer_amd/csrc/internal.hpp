@@ -33,8 +33,8 @@ hipError_t launch_gemv_rows(const uint16_t* x, const void* w, bool fp8, const fl
 // XCDs (cached per device): the grid of the persistent kernels (gemm.hip).
 int compute_units();
 
-// Small-M matrix-core kernel, 2 <= M <= 32 (17..32: the two-tile row-range
-// form where small_m_candidates_supported, else two passes), K % 128 == 0, block scales
+// Small-M matrix-core kernel, 2 <= M <= 32 (17..32: two 16-row MFMA tiles,
+// in the row-range form where small_m_candidates_supported), K % 128 == 0, block scales
 // (small_m.hip).  The K partition is the kernel's own, so split 1 and 4 give
 // the same bits; no workspace.  M * K * 2 and 16 * K must be below 2^31.
 // swiglu: N weight rows (gate [0, N/2), up [N/2, N)), y is [M, N/2], bit-equal

@@ -92,10 +92,12 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, 
 //   NBW == 4 / W: the waves share 16 rows and split every chunk's 4 blocks
 //     (wave w takes blocks w, w + W, ...); their partial sums are added in
 //     LDS in wave order.
-// MX (8 or 16) bounds the activation rows a launch may have.
+// MX (8, 16 or 32: one or two 16-row MFMA tiles) bounds the activation rows
+// a launch may have.
 template <int W, int D, int NBW, int XA, int MX>
 struct SmallCfg {
-    static_assert(MX == 8 || MX == 16, "8 or 16 activation rows");
+    static_assert(MX == 8 || MX == 16 || MX == 32, "8, 16 or 32 activation rows");
+    static constexpr int T = MX > 16 ? 2 : 1;  // 16-row activation tiles
     static constexpr bool KSPLIT = NBW < 4;
     static constexpr int ROWS = KSPLIT ? 16 : 16 * W;
     static constexpr int XBUFS = XA + 1;
@@ -146,7 +148,7 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     const uint32_t o_x = (uint32_t)(W * D * 2048);
     const uint32_t o_sc = o_x + C::XBUFS * xbuf + wave * (C::XBUFS * 256);
     // the partial-sum exchange reuses the code rings once every wave is done
-    static_assert(W * 1024 <= W * D * 2048, "reduction buffer fits in the code rings");
+    static_assert(W * 1024 * C::T <= W * D * 2048, "reduction buffer fits in the code rings");
     const uint32_t o_red = 0;
 
     // row M of every activation buffer stays zero: lanes for rows >= M read it
@@ -218,7 +220,10 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     const int row = lane & 15, g = lane >> 4;
     const uint32_t c0off = (uint32_t)(row * 128 + 16 * (g ^ sw(row)));
     const uint32_t c1off = (uint32_t)(row * 128 + 16 * ((4 + g) ^ sw(row)));
-    const uint32_t xrow = (uint32_t)((row < M ? row : M) * kRowX + 32 * g);
+    uint32_t xrow[C::T];
+#pragma unroll
+    for (int tt = 0; tt < C::T; ++tt)
+        xrow[tt] = (uint32_t)((16 * tt + row < M ? 16 * tt + row : M) * kRowX + 32 * g);
 
     // ---- prologue: XA chunks of activations and scales, own blocks 0..D-1
 #pragma unroll
@@ -228,7 +233,9 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     wait_vm<0>();
     barrier();
 
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[C::T];
+#pragma unroll
+    for (int tt = 0; tt < C::T; ++tt) acc[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int c = 0; c < nchunks; ++c) {
         const uint32_t xb = o_x + (uint32_t)((c % C::XBUFS) * xbuf);
         const uint32_t sb = o_sc + (uint32_t)((c % C::XBUFS) * 256);
@@ -251,11 +258,13 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
                 const u32x4 c0 = *reinterpret_cast<const u32x4*>(lds + slot + c0off);
                 const u32x4 c1 = *reinterpret_cast<const u32x4*>(lds + slot + c1off);
                 const float s = *reinterpret_cast<const float*>(lds + sb + row * 16 + b * 4);
-                u32x4 xf[4];
+                u32x4 xf[C::T][4];
 #pragma unroll
-                for (int f = 0; f < 4; ++f)
-                    xf[f] = *reinterpret_cast<const u32x4*>(lds + xb + xrow + b * 256 + (f >> 1) * 128 +
-                                                            (f & 1) * 16);
+                for (int tt = 0; tt < C::T; ++tt)
+#pragma unroll
+                    for (int f = 0; f < 4; ++f)
+                        xf[tt][f] = *reinterpret_cast<const u32x4*>(lds + xb + xrow[tt] + b * 256 +
+                                                                    (f >> 1) * 128 + (f & 1) * 16);
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const u32x4 cw = h ? c1 : c0;
@@ -264,12 +273,15 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
                     dequant4(cw.y, s, wv[2], wv[3]);
                     dequant4(cw.z, s, wv[4], wv[5]);
                     dequant4(cw.w, s, wv[6], wv[7]);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xf[2 * h]),
-                                                                   as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc,
-                                                                   0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xf[2 * h + 1]),
-                                                                   as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc,
-                                                                   0, 0, 0);
+#pragma unroll
+                    for (int tt = 0; tt < C::T; ++tt) {
+                        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, xf[tt][2 * h]), as_bf16x8(wv[0], wv[1], wv[2], wv[3]),
+                            acc[tt], 0, 0, 0);
+                        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, xf[tt][2 * h + 1]), as_bf16x8(wv[4], wv[5], wv[6], wv[7]),
+                            acc[tt], 0, 0, 0);
+                    }
                 }
                 // the slot's codes are in registers; refill it D own blocks ahead
                 gemm_fp8::wait_lgkm<0>();
@@ -280,46 +292,60 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     // DMAs past the end still target this workgroup's LDS
     wait_vm<0>();
 
-    // acc[i] = C[m = 4g + i][n = row]
-    float total[4];
+    // acc[tt][i] = C[m = 16 tt + 4g + i][n = row]
+    constexpr int T = C::T;
+    float total[T][4];
     if constexpr (C::KSPLIT) {
         float* red = reinterpret_cast<float*>(lds + o_red);
         __syncthreads();  // every wave has read its last ring slot
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave * 256 + (4 * g + i) * 16 + row] = acc[i];
+        for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave * 256 * T + (16 * tt + 4 * g + i) * 16 + row] = acc[tt][i];
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float t = red[(4 * g + i) * 16 + row];
+        for (int tt = 0; tt < T; ++tt)
 #pragma unroll
-            for (int w = 1; w < W; ++w) t = t + red[w * 256 + (4 * g + i) * 16 + row];
-            total[i] = t;
-        }
+            for (int i = 0; i < 4; ++i) {
+                const int e = (16 * tt + 4 * g + i) * 16 + row;
+                float t = red[e];
+#pragma unroll
+                for (int w = 1; w < W; ++w) t = t + red[w * 256 * T + e];
+                total[tt][i] = t;
+            }
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) total[i] = acc[i];
+        for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) total[tt][i] = acc[tt][i];
     }
     if constexpr (SW) {
         // slot row + 8 holds the up row of slot row's gate row
-        float up[4];
+        float up[T][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) up[i] = __shfl_down(total[i], 8, kWave);
+        for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) up[tt][i] = __shfl_down(total[tt][i], 8, kWave);
         if (row < 8 && row < pairs) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = 4 * g + i;
-                if (m < M)
-                    y[(int64_t)m * ldy + pb + row] =
-                        swiglu_bf16_bits(f32_to_bf16_bits(total[i]), f32_to_bf16_bits(up[i]));
-            }
+            for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = 16 * tt + 4 * g + i;
+                    if (m < M)
+                        y[(int64_t)m * ldy + pb + row] =
+                            swiglu_bf16_bits(f32_to_bf16_bits(total[tt][i]), f32_to_bf16_bits(up[tt][i]));
+                }
         }
     } else if (row < rows_here) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * g + i;
-            if (m < M) y[(int64_t)m * ldy + nw + row] = f32_to_bf16_bits(total[i]);
-        }
+        for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 16 * tt + 4 * g + i;
+                if (m < M) y[(int64_t)m * ldy + nw + row] = f32_to_bf16_bits(total[tt][i]);
+            }
     }
 }
 
@@ -739,24 +765,23 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
                                                 stream, nullptr);
         return dispatch_stream<false, false>(nb, x, codes, scales, y, ldy, M, N, K, per_rows, stream, nullptr);
     }
-    if (M > kMaxM) {
-        // 17..32 rows off the row-range form: two passes over row blocks of
-        // at least 2 rows, each streaming the codes once (at M = 32, 13.4 +
-        // 13.4 us on QKV-gate and 17.9 + 17.9 on down, against 28.5 and 36
-        // in the split-K GEMM and 90 and 144 in the GEMM without workspace)
-        if (M > kStreamMaxM) return hipErrorNotSupported;
-        const int m0 = M - kMaxM >= 2 ? kMaxM : M - 2;
-        const hipError_t e = launch_small_m(x, codes, scales, y, ldy, m0, N, K, 1, swiglu, stream);
-        if (e != hipSuccess) return e;
-        return launch_small_m(x + (int64_t)m0 * K, codes, scales, y + (int64_t)m0 * ldy, ldy, M - m0, N, K, 1,
-                              swiglu, stream);
-    }
     // Rows per workgroup: about two workgroups per CU, 8..16 rows (4..8
     // pairs), so every CU streams about the same number of rows in one round
     // (16-row workgroups left the 5120-row down projection at 1.25 per CU,
     // a quarter of the CUs streaming a second workgroup alone).
     const int units = swiglu ? N / 2 : N;
     const int per = std::clamp((units + 2 * cus - 1) / (2 * cus), swiglu ? 4 : 8, swiglu ? 8 : 16);
+    if (M > kMaxM) {
+        // 17..32 rows off the row-range form: the same workgroups with two
+        // activation tiles (32 rows staged per chunk, 1 chunk ahead; each
+        // code word feeds both tiles).  Down at M = 17 / 24 / 32: 20.7 /
+        // 29.8 / 30.5 us, against 29.2 / 30.0 / 32.1 for two passes of 16
+        // rows and 36 in the split-K GEMM (two workgroups per CU fit up to
+        // M = 21).
+        if (M > kStreamMaxM) return hipErrorNotSupported;
+        if (swiglu) return launch<4, 4, 1, 1, 32, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        return launch<4, 4, 1, 1, 32, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    }
     // 9..16 rows: activations 2 chunks ahead while two workgroups still fit
     // per CU (M <= 13), else 1 (measured at M = 16: 13.3 against 16.9 us at
     // QKV-gate, 17.9 against 21.9 at down; at M = 9 two chunks ahead are 3%

@@ -84,8 +84,7 @@ int fp8lin_decode(const uint8_t* codes, const float* scales, int64_t scale_cols,
  * FP8 tiles to BF16 (128-row tiles for M <= 128, 256-row tiles above), except
  * that 9..16 rows under the same conditions as the 3..8-row case run the
  * small-M matrix-core kernel too (its 16-row MFMA tile holds them all), and
- * 17..32 rows (two such tiles where N >= 24 rows per compute unit and
- * K / 128 is in 25..40, else two passes of at most 16 rows).
+ * 17..32 rows (two such tiles).
  * Requires M, N, K > 0 and scale_cols in {1, ceil(K/128)}.
  */
 int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales,
