@@ -91,8 +91,13 @@ at::Tensor fp8_linear(at::Tensor x, at::Tensor w, at::Tensor s, bool vector_gemv
     TORCH_CHECK(M > 0 && N > 0 && K > 0, "Empty GEMM");
     Guard guard(x.device());
     auto y = at::empty({M, N}, x.options());
-    check(fp8lin_linear(bf(x), w.data_ptr<uint8_t>(), s.data_ptr<float>(), scale_cols(s), bf_out(y), M, N, K,
-                        vector_gemv ? 1 : 0, stream_of(x)));
+    // The prefill GEMM's K-split partials, allocated by the operator on the
+    // input's stream as the reference allocates its own (src/fp8_tensor.cu:65).
+    const size_t ws = fp8lin_linear_workspace_bytes(M, N, K);
+    at::Tensor work;
+    if (ws) work = at::empty({(int64_t)ws}, x.options().dtype(at::kByte));
+    check(fp8lin_linear_ws(bf(x), w.data_ptr<uint8_t>(), s.data_ptr<float>(), scale_cols(s), bf_out(y), M, N, K,
+                           vector_gemv ? 1 : 0, ws ? work.data_ptr() : nullptr, ws, stream_of(x)));
     return y;
 }
 

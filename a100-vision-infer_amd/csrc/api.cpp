@@ -136,8 +136,20 @@ bool linear_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t 
            aligned16(x) && aligned16(codes) && 16 * K < kMaxDim && N * S * 4 < kMaxDim;
 }
 
+// K-split partials of fp8_linear's prefill GEMM (M > 8) for output row stride
+// ldy: the engine branch's plan (few tiles, or a small last round, split K);
+// 0 where nothing splits.  Block scales are assumed: per-row scales take the
+// same plan.
+size_t linear_ws(int64_t M, int64_t N, int64_t K, int64_t ldy) {
+    if (M <= 8 || M >= kMaxDim || N <= 0 || N >= kMaxDim || K <= 0 || K >= kMaxDim) return 0;
+    return fp8lin::gemm_workspace_bytes((int)ceil_div(K, 128), ldy, (int)M, (int)N, (int)K, false);
+}
+
+// ws: the K-split partials of the prefill GEMM (linear_ws bytes), or null to
+// run every GEMM tile whole.
 void linear_impl(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S,
-                 uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+                 uint16_t* y, int64_t ldy, int64_t M, int64_t N, int64_t K, hipStream_t stream,
+                 void* ws = nullptr, size_t ws_bytes = 0) {
     if (linear_small_m(x, codes, S, M, N, K)) {
         check_hip(fp8lin::launch_small_m(x, codes, scales, y, ldy, (int)M, (int)N, (int)K, 1, false, stream),
                   "fp8 small-M launch");
@@ -147,8 +159,8 @@ void linear_impl(const uint16_t* x, const uint8_t* codes, const float* scales, i
                                       wide, stream),
                   "fp8 gemv launch");
     } else {
-        check_hip(fp8lin::launch_gemm(x, codes, scales, (int)S, y, ldy, (int)M, (int)N, (int)K,
-                                      false, stream),
+        check_hip(fp8lin::launch_gemm_ws(x, codes, scales, (int)S, y, ldy, (int)M, (int)N, (int)K, false,
+                                         ws_bytes ? ws : nullptr, ws_bytes, stream),
                   "fp8 gemm launch");
     }
 }
@@ -505,6 +517,25 @@ int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales, 
                   uint16_t* y, int64_t M, int64_t N, int64_t K, int vector_gemv,
                   fp8lin_stream_t stream) {
     return fp8lin_linear_ld(x, codes, scales, scale_cols, y, N, M, N, K, vector_gemv, stream);
+}
+
+size_t fp8lin_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) { return linear_ws(M, N, K, N); }
+
+int fp8lin_linear_ws(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t scale_cols,
+                     uint16_t* y, int64_t M, int64_t N, int64_t K, int vector_gemv, void* workspace,
+                     size_t workspace_bytes, fp8lin_stream_t stream) {
+    (void)vector_gemv;
+    return guarded([&] {
+        // src/optimized.cu:62-65
+        require(x && codes && y, FP8LIN_ERR_ARGUMENT, "FP8 linear: null pointer");
+        check_dims(M, N, K);
+        check_scales(scales, scale_cols, K);
+        const size_t need = linear_ws(M, N, K, N);
+        check_workspace(workspace, workspace_bytes, need, "FP8 linear: workspace too small");
+        ensure_device();
+        linear_impl(x, codes, scales, scale_cols, y, N, M, N, K, as_stream(stream), need ? workspace : nullptr,
+                    need);
+    });
 }
 
 int fp8lin_linear_swiglu(const uint16_t* x, const uint8_t* codes, const float* scales,

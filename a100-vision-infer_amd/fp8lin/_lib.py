@@ -43,6 +43,7 @@ EXPORTED = [
     "fp8lin_add_bias",
     "fp8lin_linear_candidates_static",
     "fp8lin_linear_swiglu_workspace_bytes", "fp8lin_linear_swiglu_ws",
+    "fp8lin_linear_workspace_bytes", "fp8lin_linear_ws",
 ]
 
 
@@ -97,6 +98,8 @@ def lib():
         "fp8lin_decode": (i32, [vp, vp, i64, vp, i64, i64, vp]),
         "fp8lin_linear": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i32, vp]),
         "fp8lin_linear_ld": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i64, i32, vp]),
+        "fp8lin_linear_workspace_bytes": (sz, [i64, i64, i64]),
+        "fp8lin_linear_ws": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i32, vp, sz, vp]),
         "fp8lin_linear_swiglu": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, vp]),
         "fp8lin_swiglu": (i32, [vp, vp, i64, i64, vp]),
         "fp8lin_linear_swiglu_workspace_bytes": (sz, [i64, i64, i64]),
@@ -139,6 +142,11 @@ def lib():
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args
+    # Prepare the current device now (its properties and the device address
+    # of the library's static scratch), outside any graph capture a caller
+    # may start later.  Without a GPU (or on another architecture) this fails
+    # here without effect, and every entry point reports it when called.
+    L.fp8lin_init()
     _lib = L
     return L
 

@@ -18,7 +18,7 @@ def load():
         if not os.path.exists(ATEN_PATH):
             raise RuntimeError(f"{ATEN_PATH} is not built: run a100-vision-infer_amd/build.py --aten")
         import torch  # noqa: F401  (LibTorch must be loaded before the extension)
-        ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL).fp8lin_init()  # the current device, outside any capture
         spec = importlib.util.spec_from_file_location("avi_aten", ATEN_PATH)
         mod = importlib.util.module_from_spec(spec)
         spec.loader.exec_module(mod)

@@ -10,12 +10,13 @@ the `name.bias` vector the native call adds (src/engine.cpp:240).  The
 tensor-parallel reduce that the reference runs before the bias
 (src/engine.cpp:239) needs a second GPU and is outside this path.
 """
+import contextlib
 import ctypes
 
 import torch
 
 from ._lib import (ERR_ARGUMENT, PATH_TENSOR_SMALL, Fp8linError, LinearOptions, Weight, check, lib)
-from .ops import fp8_decode, qk_norm_rope
+from .ops import fp8_decode, fused_swiglu, qk_norm_rope
 
 
 def check_options(options):
@@ -71,15 +72,19 @@ class StoredWeight:
 
 class LinearEngine:
     """Options are the reference's `EngineOptions` linear flags
-    (`LinearOptions`) plus `cache_vision_weights` (cache fill order) and
-    `profile_kernels` (per-label event timing, `profile_report`)."""
+    (`LinearOptions`) plus `cache_vision_weights` (cache fill order),
+    `profile_kernels` (per-label event timing, `profile_report`) and
+    `reference_prefill` (`--reference-prefill`: fused weights keep views of
+    their sources, and prefill steps run unoptimized; `step_mode`)."""
 
-    def __init__(self, options=None, weight_cache_bytes=0, cache_vision_weights=False, profile_kernels=False):
+    def __init__(self, options=None, weight_cache_bytes=0, cache_vision_weights=False, profile_kernels=False,
+                 reference_prefill=False):
         self.options = options or LinearOptions()
         check_options(self.options)
         self.weight_cache_bytes = int(weight_cache_bytes)
         self.cache_vision_weights = bool(cache_vision_weights)
         self.profile_kernels = bool(profile_kernels)
+        self.reference_prefill = bool(reference_prefill)
         self.weights = {}
         self.biases = {}
         self.mixed_projections = {}
@@ -134,8 +139,18 @@ class LinearEngine:
         data = torch.cat([w.data for w in ws], 0)
         scale = torch.cat([w.scale for w in ws], 0) if scaled else None
         self.weights[dest + ".weight"] = StoredWeight(data, scale)
-        for s in sources:
-            del self.weights[s + ".weight"]
+        offset = 0
+        for s, w in zip(sources, ws):
+            rows = w.data.size(0)
+            if self.reference_prefill:
+                # src/engine.cpp:172-173: the source name stays, as a view of
+                # its rows of the fused weight (no second allocation), for the
+                # unoptimized prefill steps
+                self.weights[s + ".weight"] = StoredWeight(
+                    data.narrow(0, offset, rows), scale.narrow(0, offset, rows) if scale is not None else None)
+            else:
+                del self.weights[s + ".weight"]
+            offset += rows
 
     def cache_candidates(self):
         """The matrices the reference may cache (src/engine.cpp:130-132):
@@ -189,6 +204,37 @@ class LinearEngine:
         q, k = qk_norm_rope(projected, q_norm, k_norm, positions, heads, kv_heads, head_dim, rotary,
                             rope["rope_theta"], sections[1], sections[2], eps)
         return q, gate, k, v
+
+    # -- steps -----------------------------------------------------------------
+    @contextlib.contextmanager
+    def step_mode(self, decode=False, verifying=False):
+        """The option override of `Engine::step` (src/engine.cpp:403-405):
+        with reference_prefill, a prefill step (neither decode nor MTP
+        verification) runs with `optimized` off and restores it on exit."""
+        saved = self.options.optimized
+        if self.reference_prefill and not decode and not verifying:
+            self.options.optimized = 0
+        try:
+            yield self
+        finally:
+            self.options.optimized = saved
+
+    def mlp(self, n, prefix):
+        """The MLP of `Engine::step` (src/engine.cpp:415-416) on one rank:
+        optimized, `fused_swiglu(linear(n, gate_up))`; otherwise the unfused
+        `silu(linear(n, gate_proj)) * linear(n, up_proj)` on the source
+        weights, with the same two BF16 rounding points (the SwiGLU of the two
+        outputs side by side).  Then `linear(gated, down_proj)`; the
+        cross-rank reduce is the caller's."""
+        if self.options.optimized:
+            gated = fused_swiglu(self.linear(n, prefix + ".gate_up"))
+        else:
+            gate = self.linear(n, prefix + ".gate_proj")
+            up = self.linear(n, prefix + ".up_proj")
+            rows = gate.numel() // gate.size(-1)
+            pair = torch.cat([gate.reshape(rows, -1), up.reshape(rows, -1)], -1)
+            gated = fused_swiglu(pair).reshape(*gate.shape)
+        return self.linear(gated, prefix + ".down_proj")
 
     # -- dispatch --------------------------------------------------------------
     def _record(self, name):

@@ -23,7 +23,19 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
+_ready_devices = set()
+
+
 def _stream(t):
+    """torch's current stream on t's device, as a hipStream_t.  The first
+    time a device is seen, fp8lin_init runs with that device current, so the
+    library's one-time device queries never happen inside a graph capture
+    that starts later."""
+    idx = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    if idx not in _ready_devices:
+        with torch.cuda.device(idx):
+            check(lib().fp8lin_init())
+        _ready_devices.add(idx)
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
@@ -65,9 +77,13 @@ def fp8_decode(codes, scales):
     return y
 
 
-def fp8_linear(x, codes, scales, vector_gemv=False):
+def fp8_linear(x, codes, scales, vector_gemv=False, split=True):
     """`at::Tensor fp8_linear(x, codes, scales, bool vector_gemv=false)` --
-    src/optimized.cu:61-70."""
+    src/optimized.cu:61-70.  split: give the prefill GEMM a workspace (allocated
+    here, on the input's stream, as the reference allocates its operators'
+    partials, src/fp8_tensor.cu:65) so it may split K where whole tiles would
+    leave CUs idle (fp8lin_linear_ws); False runs every tile whole
+    (fp8lin_linear)."""
     _check_x(x, "FP8 linear expects CUDA BF16 [M,K]")
     _check_codes(codes, x)
     sc = _scale_cols(scales, codes.size(0), codes.size(1))
@@ -75,8 +91,14 @@ def fp8_linear(x, codes, scales, vector_gemv=False):
     if not (M > 0 and N > 0 and K > 0):
         _fail(ERR_SHAPE, "Empty GEMM")
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    check(lib().fp8lin_linear(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K,
-                              int(bool(vector_gemv)), _stream(x)))
+    need = lib().fp8lin_linear_workspace_bytes(M, N, K) if split else 0
+    if need:
+        ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+        check(lib().fp8lin_linear_ws(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K,
+                                     int(bool(vector_gemv)), _ptr(ws), need, _stream(x)))
+    else:
+        check(lib().fp8lin_linear(_ptr(x), _ptr(codes), _ptr(scales), sc, _ptr(y), M, N, K,
+                                  int(bool(vector_gemv)), _stream(x)))
     return y
 
 

@@ -40,6 +40,28 @@ PREFILL_MFMA_BUSY_SOURCE = ("rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_A
 SHAPES = [("gate_up", 17408, 5120), ("down", 5120, 8704), ("qkv_gate", 7168, 5120)]
 
 
+# Least bytes of weight copies each rotation holds: more than twice the
+# 256 MB Infinity Cache, so a weight is evicted before it comes round again.
+ROTATION_BYTES = 600_000_000
+
+
+def weight_bytes(n, k):
+    """Codes and row-expanded block scales of one N x K weight."""
+    return n * k + 4 * n * ((k + 127) // 128)
+
+
+def rotations(fp8lin, dev, copies):
+    """Per decode shape, at least ROTATION_BYTES of seeded weight copies (and
+    at least `copies`): copy c of shape i has Philox tag 1 + 16 c + i for the
+    first `copies`, 500 + 32 i + c after."""
+    rot = {}
+    for i, (name, n, k) in enumerate(SHAPES):
+        count = max(copies, -(-ROTATION_BYTES // weight_bytes(n, k)))
+        rot[name] = [fp8lin.gen_weights(n, k, seed=0, tag=(1 + 16 * c + i) if c < copies else (500 + 32 * i + c),
+                                        device=dev) for c in range(count)]
+    return rot
+
+
 def algo_bytes(m, n, k, n_out=None):
     """N*K codes + 4*N*ceil(K/128) scales + 2*M*K activations + 2*M*N_out output."""
     n_out = n if n_out is None else n_out
@@ -55,8 +77,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--quick", action="store_true", help="skip the secondary measurements")
-    p.add_argument("--sections", default="gemv,small,prefill,chain,inproj,head,stream,ceiling",
-                   help="secondary measurements to run (comma list of gemv, small, prefill, "
+    p.add_argument("--sections", default="gemv,small,prefill,refbench,chain,inproj,head,stream,ceiling",
+                   help="secondary measurements to run (comma list of gemv, small, prefill, refbench, "
                         "chain, inproj, head, stream, ceiling)")
     p.add_argument("--prefill-m", default="128,512,1024,4096",
                    help="prefill row counts of the prefill section (comma list)")
@@ -83,18 +105,19 @@ def main():
     assert fp8lin.lib().fp8lin_init() == 0, fp8lin.lib().fp8lin_last_error()
 
     # ---- inputs: seed 0, generated on the device ---------------------------------
-    sets = []
-    for c in range(args.copies):
-        ws = {}
-        for i, (name, n, k) in enumerate(SHAPES):
-            ws[name] = fp8lin.gen_weights(n, k, seed=0, tag=1 + 16 * c + i, device=dev)
-        sets.append(ws)
+    # Each shape's weights rotate over copies of at least ROTATION_BYTES
+    # (more than twice the 256 MB Infinity Cache), so every figure that
+    # rotates through them streams from HBM; the decode step takes the first
+    # `copies` of each.
+    rot = rotations(fp8lin, dev, args.copies)
+    sets = [{name: rot[name][c] for name, _, _ in SHAPES} for c in range(args.copies)]
     xs = {k: fp8lin.gen_activations(1, k, seed=0, tag=2, device=dev) for k in {5120, 8704}}
     ys = {name: torch.empty((1, n), dtype=torch.bfloat16, device=dev) for name, n, _ in SHAPES}
     torch.cuda.synchronize()
     step_bytes = sum(algo_bytes(1, n, k) for _, n, k in SHAPES)
-    working_set = args.copies * sum(n * k + 4 * n * ((k + 127) // 128) for _, n, k in SHAPES)
-    log(f"working set {working_set / 1e6:.1f} MB over {args.copies} weight copies")
+    working_set = args.copies * sum(weight_bytes(n, k) for _, n, k in SHAPES)
+    log(f"working set {working_set / 1e6:.1f} MB over {args.copies} weight copies; per-shape rotations " +
+        ", ".join(f"{name} {len(rot[name])} x {weight_bytes(n, k) / 1e6:.1f} MB" for name, n, k in SHAPES))
 
     L = fp8lin.lib()
     import ctypes
@@ -162,15 +185,17 @@ def main():
     torch.cuda.synchronize()
     graph_ms = r0.elapsed_time(r1) / (replays * copies)
 
-    # Dominant kernel: gate/up GEMV, back-to-back launches over the rotating
-    # copies in a graph, timed with HIP events around the replays.
+    # Dominant kernel: gate/up GEMV, back-to-back launches over its rotation
+    # (at least ROTATION_BYTES) in a graph, timed with HIP events around the
+    # replays.
     gu_graph = torch.cuda.CUDAGraph()
-    reps_in_graph = 8 * copies
+    gu_rot = rot["gate_up"]
+    reps_in_graph = 4 * len(gu_rot)
     with torch.cuda.stream(cap):
         sp_saved, sp.value = sp.value, cap.cuda_stream
         with torch.cuda.graph(gu_graph, stream=cap):
             for i in range(reps_in_graph):
-                gemv("gate_up", sets[i % copies], ys["gate_up"])
+                gemv("gate_up", {"gate_up": gu_rot[i % len(gu_rot)]}, ys["gate_up"])
         sp.value = sp_saved
     gu_graph.replay()
     torch.cuda.synchronize()
@@ -191,7 +216,7 @@ def main():
     extra = {"graph_us_per_step": round(graph_ms * 1e3, 3),
              "graph_GBs": round(step_bytes / (graph_ms * 1e-3) / 1e9, 1)}
     if not args.quick:
-        extra.update(secondary(torch, fp8lin, dev, sets, log, set(args.sections.split(",")),
+        extra.update(secondary(torch, fp8lin, dev, rot, log, set(args.sections.split(",")),
                                [int(v) for v in args.prefill_m.split(",") if v]))
     if args.calibrate:
         extra.update(calibrate(torch, dev, log))
@@ -298,10 +323,12 @@ def graph_timed(torch, fn, sp, reps=20, replays=20):
     return a.elapsed_time(b) / (replays * reps)
 
 
-def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(128, 512, 1024, 4096)):
+def secondary(torch, fp8lin, dev, rot, log, sections, prefill_m=(128, 512, 1024, 4096)):
     """Per-shape and per-path figures through the C ABI with preallocated
-    outputs, timed as graph replays of back-to-back launches over the rotated
-    weight copies (the host's launch rate stays out of the figures)."""
+    outputs, each call on the next of its shape's rotated weight copies
+    (`rot`, at least ROTATION_BYTES per shape); decode figures are graph
+    replays of back-to-back launches (the host's launch rate stays out of
+    them), prefill figures eager back-to-back calls."""
     import ctypes
     L = fp8lin.lib()
     P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
@@ -316,16 +343,7 @@ def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(128, 512, 1024
     # over 32 copies (554 MB) so it too streams from HBM
     cfg1 = [fp8lin.gen_weights(4096, 4096, seed=0, tag=100 + c, device=dev)
             for c in range(32)] if "gemv" in sections else []
-    # Each shape's rotation holds at least 600 MB (the decode step's own copies
-    # plus more), so no per-shape figure is served from the Infinity Cache.
-    rot = {}
-    if sections & {"gemv", "small"}:
-        for i, (name, n, k) in enumerate(SHAPES):
-            have = [ws[name] for ws in sets]
-            need = -(-600_000_000 // (n * k + 4 * n * ((k + 127) // 128)))
-            rot[name] = have + [fp8lin.gen_weights(n, k, seed=0, tag=500 + 32 * i + c, device=dev)
-                                for c in range(max(0, need - len(have)))]
-    gemv_cases = [(name, n, k, rot.get(name, [])) for name, n, k in SHAPES]
+    gemv_cases = [(name, n, k, rot[name]) for name, n, k in SHAPES]
     gemv_cases.append(("cfg1_4096", 4096, 4096, cfg1))
     for name, n, k, copies in (gemv_cases if "gemv" in sections else []):
         x = fp8lin.gen_activations(1, k, seed=0, tag=2, device=dev)
@@ -374,18 +392,23 @@ def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(128, 512, 1024
                 gbs = algo_bytes(m, n, k) / (ms * 1e-3) / 1e9
                 extra[f"m{m}_{name}_{label}_GBs"] = round(gbs, 1)
                 log(f"M={m} {name} {label}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
-    del small_copies, rot
-    # prefill GEMM with fused SwiGLU (config 4)
+    del small_copies
+    # prefill GEMM with fused SwiGLU (config 4), each call on the next gate/up
+    # copy of the rotation
     n, k = 17408, 5120
-    c, s = sets[0]["gate_up"]
+    gu = rot["gate_up"]
     for m in (prefill_m if "prefill" in sections else ()):
         x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
         y = torch.empty((m, n // 2), dtype=torch.bfloat16, device=dev)
         need = L.fp8lin_linear_swiglu_workspace_bytes(m, n, k)
         pws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
-        ms = timed(torch, lambda: ok(L.fp8lin_linear_swiglu_ws(P(x), P(c), P(s), s.size(1), P(y), m, n, k, P(pws),
-                                                               need, sp)),
-                   10 if m == 4096 else 20)
+        i = [0]
+
+        def call():
+            c, s = gu[i[0] % len(gu)]
+            i[0] += 1
+            ok(L.fp8lin_linear_swiglu_ws(P(x), P(c), P(s), s.size(1), P(y), m, n, k, P(pws), need, sp))
+        ms = timed(torch, call, 2 * len(gu) if m == 4096 else 4 * len(gu), warm=len(gu))
         tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         extra[f"prefill_swiglu_m{m}_TFLOPs"] = round(tflops, 1)
         extra[f"prefill_swiglu_m{m}_us"] = round(ms * 1e3, 2)
@@ -404,8 +427,34 @@ def secondary(torch, fp8lin, dev, sets, log, sections, prefill_m=(128, 512, 1024
         extra["reference_hipblaslt_bf16_m4096_TFLOPs"] = round(tflops, 1)
         log(f"reference: torch.mm BF16 (hipBLASLt) M={m} N={n} K={k}: {ms:.3f} ms {tflops:.1f} TFLOP/s")
         del xa, wb
+    # The drop-in operator (fp8_linear through fp8lin_linear_ws, as the ATen
+    # shim calls it) on the prefill projections whose tiles leave CUs idle,
+    # against the same call without a workspace (every tile whole).
+    for name, n, k in (SHAPES[1:] if "prefill" in sections else ()):
+        for m in (64, 512):
+            x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
+            y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            need = L.fp8lin_linear_workspace_bytes(m, n, k)
+            lws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+            copies = rot[name]
+            for label, split in (("linear_ws", True), ("linear", False)):
+                i = [0]
+
+                def call():
+                    c, s = copies[i[0] % len(copies)]
+                    i[0] += 1
+                    if split:
+                        ok(L.fp8lin_linear_ws(P(x), P(c), P(s), s.size(1), P(y), m, n, k, 1, P(lws), need, sp))
+                    else:
+                        ok(L.fp8lin_linear(P(x), P(c), P(s), s.size(1), P(y), m, n, k, 1, sp))
+                ms = timed(torch, call, 2 * len(copies), warm=len(copies))
+                tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+                extra[f"dropin_m{m}_{name}_{label}_us"] = round(ms * 1e3, 2)
+                log(f"fp8_linear M={m} {name} ({label}): {ms * 1e3:.2f} us {tf:.1f} TFLOP/s")
+    if "refbench" in sections:
+        extra.update(reference_benchmark_shapes(torch, fp8lin, dev, log))
     if "chain" in sections:
-        extra.update(layer_chain(torch, fp8lin, dev, sets, log))
+        extra.update(layer_chain(torch, fp8lin, dev, rot, log))
     if "inproj" in sections:
         extra.update(in_proj_all(torch, fp8lin, dev, log))
     if "head" in sections:
@@ -559,25 +608,25 @@ def head_and_epilogue(torch, fp8lin, dev, log):
     return extra
 
 
-def layer_chain(torch, fp8lin, dev, sets, log):
+def layer_chain(torch, fp8lin, dev, rot, log):
     """Config 5: QKV-gate -> gate/up+SwiGLU -> down -> vocab-sharded head
     (75968 x 5120) at M = 512 and M = 1, each link fed by the previous one's
     output where the shapes chain (QKV-gate and gate/up both read the layer
-    input; attention between them is out of scope).  The three layer links
-    rotate over the weight copies of `sets` (more than 512 MB together) and
-    the 389 MB head is one matrix, so every figure streams from HBM, for the
-    whole chain and for each link alone.  M = 1 is timed as graph replays of
-    back-to-back calls (the host's launch rate stays out), M = 512 eagerly."""
+    input; attention between them is out of scope).  Every link rotates over
+    at least ROTATION_BYTES of its own weight copies (the layer links over
+    their `rot` lists, the head over two 389 MB copies), so every figure
+    streams from HBM, for the whole chain and for each link alone.  M = 1 is
+    timed as graph replays of back-to-back calls (the host's launch rate
+    stays out), M = 512 eagerly."""
     import ctypes
     L = fp8lin.lib()
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-    head = fp8lin.gen_weights(75968, 5120, seed=0, tag=90, device=dev)
+    heads = [fp8lin.gen_weights(75968, 5120, seed=0, tag=90 + c, device=dev) for c in range(2)]
     shapes = {"qkv_gate": (7168, 5120, False), "gate_up_swiglu": (17408, 5120, True),
               "down": (5120, 8704, False), "head": (75968, 5120, False)}
-    weights = {"qkv_gate": [ws["qkv_gate"] for ws in sets], "gate_up_swiglu": [ws["gate_up"] for ws in sets],
-               "down": [ws["down"] for ws in sets], "head": [head]}
-    copies = len(sets)
+    weights = {"qkv_gate": rot["qkv_gate"], "gate_up_swiglu": rot["gate_up"], "down": rot["down"], "head": heads}
+    copies = max(len(v) for v in weights.values())
     extra = {}
 
     def ok(rc):
@@ -634,8 +683,8 @@ def layer_chain(torch, fp8lin, dev, sets, log):
 
         def time_it(fn):
             if m == 1:
-                return graph_timed(torch, rotating(fn), sp, reps=4 * copies, replays=10)
-            return timed(torch, rotating(fn), 2 * copies)
+                return graph_timed(torch, rotating(fn), sp, reps=2 * copies, replays=10)
+            return timed(torch, rotating(fn), copies, warm=copies)
         total_ms = time_it(chain)
         tot_bytes = tot_flops = 0
         for name, (n, k, sw) in shapes.items():
@@ -660,6 +709,49 @@ def layer_chain(torch, fp8lin, dev, sets, log):
             extra[f"chain_m{m}_TFLOPs"] = round(tf, 1)
             log(f"chain M={m}: {total_ms:.3f} ms, {tf:.1f} TFLOP/s ({100 * tf / BF16_PEAK_TFLOPS:.1f}% MFMA)")
         log("  " + ", ".join(f"{name} {extra[f'chain_m{m}_{name}_us']} us" for name in shapes))
+    return extra
+
+
+def reference_benchmark_shapes(torch, fp8lin, dev, log):
+    """The reference benchmark's remaining shapes (tests/linear_benchmark.cpp:
+    22-23): 5120 x 5120 and the 124160 x 5120 head at M = 2, 4, 8, through
+    fp8_linear and fp8_tensor_small with split 1 and 4, as graph replays.
+    5120 x 5120 rotates over 23 copies (613 MB); the 655 MB head is one
+    matrix, larger than twice the Infinity Cache."""
+    import ctypes
+    L = fp8lin.lib()
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    sp = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    extra = {}
+
+    def ok(rc):
+        if rc:
+            raise RuntimeError(L.fp8lin_last_error())
+    for name, n, k, count in (("5120x5120", 5120, 5120, 23), ("head124160", 124160, 5120, 1)):
+        copies = [fp8lin.gen_weights(n, k, seed=0, tag=700 + c, device=dev) for c in range(count)]
+        for m in (2, 4, 8):
+            x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
+            y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+            paths = {
+                "linear": lambda c, s: ok(L.fp8lin_linear(P(x), P(c), P(s), s.size(1), P(y), m, n, k, 1, sp)),
+                "tensor_s1": lambda c, s: ok(L.fp8lin_tensor_small(P(x), P(c), P(s), P(y), m, n, k, 1, None, 0,
+                                                                  sp)),
+                "tensor_s4": lambda c, s: ok(L.fp8lin_tensor_small(P(x), P(c), P(s), P(y), m, n, k, 4, None, 0,
+                                                                  sp)),
+            }
+            for label, fn in paths.items():
+                i = [0]
+
+                def run():
+                    c, s = copies[i[0] % len(copies)]
+                    i[0] += 1
+                    fn(c, s)
+                ms = graph_timed(torch, run, sp, reps=max(4, 2 * len(copies)), replays=10)
+                gbs = algo_bytes(m, n, k) / (ms * 1e-3) / 1e9
+                extra[f"refbench_m{m}_{name}_{label}_us"] = round(ms * 1e3, 2)
+                extra[f"refbench_m{m}_{name}_{label}_GBs"] = round(gbs, 1)
+                log(f"reference shape {name} M={m} {label}: {ms * 1e3:.2f} us {gbs:.1f} GB/s")
+        del copies
     return extra
 
 

@@ -36,7 +36,9 @@
 extern "C" {
 #endif
 
-#define FP8LIN_VERSION 110 /* 1.1.0 */
+/* 2.0.0: fp8lin_weight gained its `bias` member (a record built against a
+ * 1.x header has another size and stride) and fp8lin_linear_ws was added. */
+#define FP8LIN_VERSION 200 /* 2.0.0 */
 
 enum fp8lin_status {
     FP8LIN_OK = 0,
@@ -53,9 +55,14 @@ typedef void* fp8lin_stream_t; /* hipStream_t */
 int fp8lin_version(void);
 /* Message for the calling thread's most recent failure ("" if none). */
 const char* fp8lin_last_error(void);
-/* Checks that the current device is gfx950 and loads the kernels.  Optional:
- * every entry point calls it on first use.  TileLang plugin precedent:
- * init()/get_last_error() of src/tilelang.cpp:80-82. */
+/* Checks that the current device is gfx950 and, once per device, queries
+ * its properties and looks up the device address of the library's static
+ * scratch.  Every entry point does the same on its first call on a device,
+ * but those runtime queries must not run inside a HIP stream capture: call
+ * fp8lin_init() with each device current before the first capture that
+ * records fp8lin calls on it (the Python host mirror does so for every
+ * device it is handed).  Idempotent and thread-safe.  TileLang plugin
+ * precedent: init()/get_last_error() of src/tilelang.cpp:80-82. */
 int fp8lin_init(void);
 
 /* ---------------------------------------------------------------------------
@@ -97,6 +104,25 @@ int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales,
 int fp8lin_linear_ld(const uint16_t* x, const uint8_t* codes, const float* scales,
                      int64_t scale_cols, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
                      int64_t K, int vector_gemv, fp8lin_stream_t stream);
+
+/* fp8lin_linear with a workspace for the prefill GEMM's K-split partials:
+ * when M > 8 and the GEMM's 256x256 (128-row for M <= 128) tiles number
+ * fewer than half the CUs (e.g. the 7168-row QKV-gate and 5120-row down
+ * projections at M = 512, or the 5120-row down projection at M = 33..128),
+ * or leave a last round on at most half of them, those tiles are cut into
+ * K ranges and a second launch adds their FP32 sums in order and rounds
+ * once.  Within the parity bar of fp8lin_linear (only the FP32 summation
+ * order of the split tiles differs); every other call is fp8lin_linear bit
+ * for bit.  The workspace is what fp8lin_linear_workspace_bytes reports for
+ * (M, N, K) (0: none needed; 256 KiB per split tile and K range), 16-byte
+ * aligned, any content.  Replaces the same `fp8_linear` as fp8lin_linear;
+ * the reference allocates such partials inside its own operator
+ * (src/fp8_tensor.cu:65), here the caller passes them.
+ */
+size_t fp8lin_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int fp8lin_linear_ws(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t scale_cols,
+                     uint16_t* y, int64_t M, int64_t N, int64_t K, int vector_gemv, void* workspace,
+                     size_t workspace_bytes, fp8lin_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Fused gate/up projection + SwiGLU: with G = fp8lin_linear(x, W) of shape
@@ -198,6 +224,9 @@ int fp8lin_gemm_bf16(const uint16_t* x, const uint16_t* w, uint16_t* y, int64_t 
  * optimized, a split other than 1 or 4; src/engine.cpp:78-81) make every
  * engine entry point return FP8LIN_ERR_ARGUMENT (and the *_workspace_bytes
  * and *_path queries 0).
+ * Records must be zero-initialised before their fields are set (C:
+ * `fp8lin_weight w = {0};`, C++: `fp8lin_weight w{};`), so that a member a
+ * caller does not know about, such as `bias` (added in 2.0.0), is NULL.
  */
 typedef struct fp8lin_weight {
     const void* data;            /* uint8 codes [N,K], or BF16 [N,K] if scales == NULL */

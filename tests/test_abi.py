@@ -29,7 +29,7 @@ def test_header_symbols_exported(fp8lin):
 
 def test_version_and_error_string(fp8lin):
     L = fp8lin.lib()
-    assert L.fp8lin_version() == 110
+    assert L.fp8lin_version() == 200
     assert isinstance(L.fp8lin_last_error(), bytes)
 
 
@@ -318,3 +318,45 @@ def test_engine_validation(fp8lin):
     w.scale_cols = 3
     rc = L.fp8lin_engine_linear(ctypes.byref(opt), ctypes.byref(w), P, 2, P, 256, None, 0, None, None)
     assert rc == F.ERR_ARGUMENT
+
+
+def splitk_plan_bytes(m, n, k, cus=256):
+    """K-split partials of the prefill GEMM plan (bm x 256 tiles, bm = 128 for
+    m <= 128): every tile when the tiles number at most half the CUs, else
+    the tiles of a last round on at most half of them; min(CUs / tiles,
+    K / 256, 8) K ranges of one bm x 256 FP32 partial each."""
+    bm = 128 if m <= 128 else 256
+    tiles = -(-m // bm) * -(-n // 256)
+    split = tiles if 2 * tiles <= cus else tiles % cus if tiles > cus and 2 * (tiles % cus) <= cus else 0
+    s = min(cus // split, k // 256, 8) if split else 0
+    return split * s * bm * 256 * 4 if s > 1 else 0
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 7168, 5120), (512, 5120, 8704), (64, 5120, 8704), (1024, 17408, 5120),
+                                   (4096, 17408, 5120), (512, 17408, 5120), (512, 75968, 5120)])
+def test_linear_workspace_bytes(fp8lin, m, n, k):
+    """fp8lin_linear_ws's partials follow the engine branch's split plan (no
+    GPU here: the plan assumes 256 CUs)."""
+    L = fp8lin.lib()
+    assert L.fp8lin_linear_workspace_bytes(m, n, k) == splitk_plan_bytes(m, n, k)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 7168, 5120), (8, 5120, 8704), (16, 5120, 8704), (32, 7168, 5120),
+                                   (512, 48, 5120), (0, 16, 16), (512, 7168, 0)])
+def test_linear_workspace_bytes_none(fp8lin, m, n, k):
+    """No partials where fp8_linear runs no GEMM tile (the decode GEMV, the
+    small-M kernel for 9..32 rows, the skinny kernel) or on empty shapes."""
+    assert fp8lin.lib().fp8lin_linear_workspace_bytes(m, n, k) == 0
+
+
+def test_linear_ws_validation(fp8lin):
+    """fp8lin_linear_ws checks its workspace before touching a device."""
+    L = fp8lin.lib()
+    need = L.fp8lin_linear_workspace_bytes(512, 7168, 5120)
+    assert need > 0
+    assert L.fp8lin_linear_ws(P, P, P, 40, P, 512, 7168, 5120, 0, None, need, None) == fp8lin.ERR_WORKSPACE
+    assert L.fp8lin_linear_ws(P, P, P, 40, P, 512, 7168, 5120, 0, P, need - 16, None) == fp8lin.ERR_WORKSPACE
+    assert L.fp8lin_linear_ws(P, P, P, 40, P, 512, 7168, 5120, 0, ctypes.c_void_p(0x10008), need,
+                              None) == fp8lin.ERR_WORKSPACE
+    assert L.fp8lin_linear_ws(None, P, P, 40, P, 512, 7168, 5120, 0, P, need, None) == fp8lin.ERR_ARGUMENT
+    assert L.fp8lin_linear_ws(P, P, P, 40, P, 0, 7168, 5120, 0, P, need, None) == fp8lin.ERR_SHAPE

@@ -316,3 +316,56 @@ def test_shim_rejects_like_reference(avi, gpu):
         avi.fp8_tensor_small(x, codes, torch.ones(16, 2, device=gpu), 2)
     with pytest.raises(RuntimeError, match="Invalid TileLang FP8 W8A16 inputs"):
         avi.tilelang_fp8_small(x, codes[:15].contiguous(), torch.ones(15, 2, device=gpu), 1)
+
+
+def _bits(t):
+    import numpy as np
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 7168, 5120), (512, 5120, 8704), (64, 5120, 8704)])
+def test_shim_fp8_linear_split_k(avi, fp8lin, gpu, oracle, m, n, k):
+    """avi::fp8_linear on the prefill projections whose GEMM tiles leave CUs
+    idle (the QKV-gate and down projections at a 512-row chunk, down at a
+    64-row chunk tail) splits K through its own workspace, as the engine
+    branch does (src/engine.cpp:222-224): at the parity bar against the FP64
+    oracle on the last 600 columns, equal to the Python mirror's call bit for
+    bit, and within the split-order bar of the unsplit call everywhere."""
+    from parity import assert_parity, ulp_distance
+    assert fp8lin.lib().fp8lin_linear_workspace_bytes(m, n, k) > 0
+    codes, scales = fp8lin.gen_weights(n, k, seed=0, tag=31, device=gpu)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=32, device=gpu)
+    y = avi.fp8_linear(x, codes, scales, True)
+    assert torch.equal(y, fp8lin.fp8_linear(x, codes, scales, True))
+    got = _bits(y)
+    cols = (n - 600, n)
+    ref = oracle.linear(_bits(x), codes.cpu().numpy(), scales.cpu().numpy(), rows=cols)
+    assert_parity(got[:, cols[0]:], ref[:, cols[0]:], f"shim split-K {m}x{n}x{k}")
+    plain = _bits(fp8lin.fp8_linear(x, codes, scales, True, split=False))
+    assert_parity(got, plain, f"shim split-K vs unsplit {m}x{n}x{k}", min_exact=0.99)
+    assert (ulp_distance(got, plain) > 1).sum() <= max(1, got.size // 10000)
+
+
+def test_shim_fp8_linear_split_k_graph_replay(avi, fp8lin, gpu):
+    """One avi::fp8_linear call with split K, captured in a HIP graph (its
+    workspace comes from the capture's private pool) and replayed with
+    updated activations, eager work and synchronisations in between: every
+    replay equals the eager call on the same input."""
+    m, n, k = 512, 5120, 8704
+    codes, scales = fp8lin.gen_weights(n, k, seed=0, tag=33, device=gpu)
+    x = fp8lin.gen_activations(m, k, seed=0, tag=34, device=gpu)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        out = avi.fp8_linear(x, codes, scales, True)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = avi.fp8_linear(x, codes, scales, True)
+    for i in range(3):
+        if i:
+            x.copy_(fp8lin.gen_activations(m, k, seed=i, tag=34, device=gpu))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, avi.fp8_linear(x, codes, scales, True)), f"replay {i}"

@@ -43,7 +43,7 @@ def check_swiglu(fp8lin, oracle, x, codes, scales, c_np, s_np, rows, what):
     helper), within 1 ulp of the oracle SwiGLU of the device's own gate/up,
     and at the bar against the oracle composition."""
     fused = fp8lin.linear_swiglu(x, codes, scales, split=False)
-    gate_up = fp8lin.fp8_linear(x, codes, scales, True)
+    gate_up = fp8lin.fp8_linear(x, codes, scales, True, split=False)
     assert torch.equal(fused, fp8lin.fused_swiglu(gate_up)), f"{what}: fused != unfused"
     ref_gu = oracle.linear(bits(x)[rows], c_np, s_np)
     gu = bits(gate_up)[rows]
@@ -124,7 +124,7 @@ def test_head_m512(fp8lin, gpu, oracle, head):
     codes, scales, c_np, s_np = head
     m, n = 512, 75968
     x = fp8lin.gen_activations(m, 5120, seed=0, tag=6, device=gpu)
-    y = bits(fp8lin.fp8_linear(x, codes, scales))
+    y = bits(fp8lin.fp8_linear(x, codes, scales, split=False))
     xb = bits(x)
     rows = np.array([0, 1, 100, 255, 256, 300, 510, 511])
     assert_parity(y[rows], oracle.linear(xb[rows], c_np, s_np), "head M=512 rows")

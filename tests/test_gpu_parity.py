@@ -251,8 +251,8 @@ def test_gemm_tile_heights_agree(fp8lin, gpu, oracle, n, k, swiglu):
         small = fp8lin.linear_swiglu(xg[:128].contiguous(), c, s, split=False)
         big = fp8lin.linear_swiglu(xg, c, s, split=False)
     else:
-        small = fp8lin.fp8_linear(xg[:128].contiguous(), c, s)
-        big = fp8lin.fp8_linear(xg, c, s)
+        small = fp8lin.fp8_linear(xg[:128].contiguous(), c, s, split=False)
+        big = fp8lin.fp8_linear(xg, c, s, split=False)
     assert torch.equal(small, big[:128])
     if swiglu:
         rows = [0, 1, 63, 64, 127]
@@ -319,7 +319,7 @@ def test_linear_swiglu_fused_equals_unfused(fp8lin, gpu, oracle, m, n, k):
     x = up(rand_bf16(rng, (m, k)), gpu)
     c, s = up(codes, gpu), up(scales, gpu)
     fused = fp8lin.linear_swiglu(x, c, s, split=False)
-    gate_up = fp8lin.fp8_linear(x, c, s)
+    gate_up = fp8lin.fp8_linear(x, c, s, split=False)
     ref_gu = oracle.linear(bits(x), codes, scales)
     assert_parity(bits(gate_up), ref_gu, "gate/up")
     # SwiGLU of the device's own gate/up: only expf may differ (<= 1 ulp).
@@ -364,6 +364,44 @@ def test_engine_paths(fp8lin, gpu, oracle):
         y, p = eng.linear(up(x, gpu), "w", return_path=True)
         assert p == path, (opt, rows, p)
         assert_parity(bits(y), oracle.linear_bf16w(x, ref_w), f"engine path {path}")
+
+
+@pytest.mark.parametrize("m", [1, 40])
+def test_engine_reference_prefill_mlp(fp8lin, gpu, oracle, m):
+    """--reference-prefill (src/engine.cpp:170-175, :403-416): gate_proj and
+    up_proj stay as views of the fused gate_up; a prefill step runs them
+    unoptimized (dequant-then-GEMM, src/engine.cpp:225-233) and unfused
+    (silu(gate) * up), a decode step runs the fused gate_up + SwiGLU; both
+    against the oracle composition, each down projection too."""
+    F = fp8lin
+    rng = np.random.default_rng(15 + m)
+    d, k = 384, 512
+    w = {}
+    for name, n, kk in (("gate_proj", d, k), ("up_proj", d, k), ("down_proj", k, d)):
+        c = rand_codes(rng, n, kk)
+        sc = (rng.random((n, kk // 128)) * .01 + .001).astype(np.float32)
+        w[name] = (c, sc)
+    eng = F.LinearEngine(reference_prefill=True)
+    for name, (c, sc) in w.items():
+        eng.add(f"l.mlp.{name}.weight", up(c, gpu), up(sc, gpu))
+    eng.fuse_weights("l.mlp.gate_up", ["l.mlp.gate_proj", "l.mlp.up_proj"])
+    x = rand_bf16(rng, (m, k))
+    xg = up(x, gpu)
+    ref_gu = np.concatenate([oracle.linear(x, *w["gate_proj"]), oracle.linear(x, *w["up_proj"])], axis=1)
+    for decode in (False, True):
+        with eng.step_mode(decode=decode):
+            if not decode:
+                _, p = eng.linear(xg, "l.mlp.gate_proj", return_path=True)
+                assert p == F.PATH_DEQUANT_GEMM
+            out = eng.mlp(xg, "l.mlp")
+            gated = F.fused_swiglu(eng.linear(xg, "l.mlp.gate_up")) if eng.options.optimized else None
+        assert eng.options.optimized
+        ref_g = oracle.swiglu(ref_gu)
+        if gated is not None:
+            assert_parity(bits(gated), ref_g, f"reference prefill gated m={m}", elementwise=False)
+        ref = oracle.linear(ref_g, *w["down_proj"])
+        assert_parity(bits(out), ref, f"reference prefill mlp m={m} decode={decode}", min_exact=None,
+                      elementwise=False)
 
 
 def test_engine_mixed_groups(fp8lin, gpu, oracle):
@@ -453,7 +491,7 @@ def test_engine_splitk_gemm(fp8lin, gpu, oracle, m, n, k):
     ref = oracle.linear(x, codes, scales, rows=cols)
     got = bits(y)
     assert_parity(got[:, cols[0]:cols[1]], ref[:, cols[0]:cols[1]], f"split-K {m}x{n}x{k}")
-    plain = bits(F.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu)))
+    plain = bits(F.fp8_linear(up(x, gpu), up(codes, gpu), up(scales, gpu), split=False))
     assert_parity(got, plain, f"split-K vs unsplit {m}x{n}x{k}", min_exact=0.99)
     # at most one output in 10^4 (and at least one allowed) beyond 1 ulp
     assert (ulp_distance(got, plain) > 1).sum() <= max(1, got.size // 10000)

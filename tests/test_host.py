@@ -21,6 +21,45 @@ def test_fuse_compatible_rows(fp8lin):
     assert "l.mlp.gate_proj.weight" not in eng.weights and not eng.mixed_projections
 
 
+def test_reference_prefill_keeps_source_views(fp8lin):
+    """--reference-prefill (src/engine.cpp:170-175): the fused weight is one
+    allocation and each source name stays as a view of its rows of it."""
+    eng = fp8lin.LinearEngine(reference_prefill=True)
+    g, gs = _fp8(256, 384)
+    u, us = _fp8(128, 384)
+    eng.add("l.mlp.gate_proj.weight", g, gs)
+    eng.add("l.mlp.up_proj.weight", u, us)
+    eng.fuse_weights("l.mlp.gate_up", ["l.mlp.gate_proj", "l.mlp.up_proj"])
+    fused = eng.weights["l.mlp.gate_up.weight"]
+    gv, uv = eng.weights["l.mlp.gate_proj.weight"], eng.weights["l.mlp.up_proj.weight"]
+    assert torch.equal(gv.data, g) and torch.equal(gv.scale, gs)
+    assert torch.equal(uv.data, u) and torch.equal(uv.scale, us)
+    assert gv.data.data_ptr() == fused.data.data_ptr()
+    assert uv.data.data_ptr() == fused.data.data_ptr() + 256 * 384
+    assert uv.scale.data_ptr() == fused.scale.data_ptr() + 256 * 3 * 4
+    assert gv.data.is_contiguous() and uv.scale.is_contiguous()
+
+
+def test_reference_prefill_step_mode(fp8lin):
+    """Engine::step turns `optimized` off for a prefill step under
+    --reference-prefill and restores it (src/engine.cpp:403-405); decode and
+    verification steps and engines without the option keep it."""
+    eng = fp8lin.LinearEngine(reference_prefill=True)
+    with eng.step_mode():
+        assert not eng.options.optimized
+    assert eng.options.optimized
+    for kw in ({"decode": True}, {"verifying": True}):
+        with eng.step_mode(**kw):
+            assert eng.options.optimized
+    plain = fp8lin.LinearEngine()
+    with plain.step_mode():
+        assert plain.options.optimized
+    with pytest.raises(ValueError):
+        with eng.step_mode():
+            raise ValueError("restored on the way out")
+    assert eng.options.optimized
+
+
 def test_fuse_mixed_groups_keep_order(fp8lin):
     """Qwen GDN in_proj_all: [FP8 qkv + z] and [BF16 b + a] become two groups
     (src/engine.cpp:151-165, tests/optimized_test.cpp:89-98)."""
