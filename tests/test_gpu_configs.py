@@ -202,3 +202,29 @@ def test_tensor_small_unaligned_views(fp8lin, gpu, oracle, m, k):
             y = fp8lin.fp8_tensor_small(xx, cc, s, split)
             assert_parity(bits(y), ref, f"unaligned {what} m={m} k={k} split={split}")
             assert torch.equal(y, fp8lin.fp8_linear(xx, cc, s)), what
+
+
+@pytest.fixture(scope="module")
+def head124160(fp8lin, gpu):
+    return weights(fp8lin, gpu, 124160, 5120, tag=41)
+
+
+@pytest.mark.parametrize("m", [2, 4, 8])
+@pytest.mark.parametrize("shape", ["5120x5120", "124160x5120"])
+def test_reference_benchmark_shapes(fp8lin, gpu, oracle, head124160, shape, m):
+    """The reference benchmark's remaining shapes (tests/linear_benchmark.cpp:
+    22-23): 5120 x 5120 and the full-vocabulary TP = 2 head 124160 x 5120 at
+    M = 2, 4, 8 through fp8_linear and fp8_tensor_small with split 1 and 4,
+    every output against the FP64 oracle; split 1 and 4 give the same bits
+    (the kernel's own K partition)."""
+    if shape == "5120x5120":
+        codes, scales, c_np, s_np = weights(fp8lin, gpu, 5120, 5120, tag=40)
+    else:
+        codes, scales, c_np, s_np = head124160
+    k = 5120
+    x = fp8lin.gen_activations(m, k, seed=0, tag=42, device=gpu)
+    ref = oracle.linear(bits(x), c_np, s_np)
+    assert_parity(bits(fp8lin.fp8_linear(x, codes, scales, True)), ref, f"{shape} fp8_linear M={m}")
+    s1 = fp8lin.fp8_tensor_small(x, codes, scales, 1)
+    assert_parity(bits(s1), ref, f"{shape} fp8_tensor_small M={m}")
+    assert torch.equal(fp8lin.fp8_tensor_small(x, codes, scales, 4), s1)
