@@ -19,7 +19,8 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libfp8lin.so")
-SOURCES = ["api.cpp", "gemv.hip", "small_m.hip", "gemm.hip", "skinny.hip", "elementwise.hip", "epilogue.hip"]
+SOURCES = ["api.cpp", "gemv.hip", "small_m.hip", "gemm.hip", "skinny.hip", "elementwise.hip", "epilogue.hip",
+           "chain.hip"]
 ARCH = "gfx950"
 
 COMMON = [

@@ -905,6 +905,39 @@ int fp8lin_engine_linear_candidates(const fp8lin_linear_options* options, const 
     });
 }
 
+size_t fp8lin_decode_chain_workspace_bytes(int nlinks) {
+    if (nlinks < 1 || nlinks > FP8LIN_CHAIN_MAX_LINKS) return 0;
+    return (fp8lin::chain_sync_words(nlinks) * 8 + 255) / 256 * 256;
+}
+
+int fp8lin_decode_chain(const fp8lin_chain_link* links, int nlinks, void* workspace, size_t workspace_bytes,
+                        fp8lin_stream_t stream) {
+    return guarded([&] {
+        require(links != nullptr, FP8LIN_ERR_ARGUMENT, "decode chain: null links");
+        require(nlinks >= 1 && nlinks <= FP8LIN_CHAIN_MAX_LINKS, FP8LIN_ERR_SHAPE,
+                "decode chain: 1 to FP8LIN_CHAIN_MAX_LINKS links");
+        fp8lin::ChainLink dev[FP8LIN_CHAIN_MAX_LINKS];
+        for (int L = 0; L < nlinks; ++L) {
+            const fp8lin_chain_link& k = links[L];
+            require(k.codes && k.scales && k.x && k.y, FP8LIN_ERR_ARGUMENT, "decode chain: null pointer in a link");
+            check_dims(1, k.N, k.K);
+            check_scales(k.scales, k.scale_cols, k.K);
+            require(k.after >= -1 && k.after < L, FP8LIN_ERR_ARGUMENT,
+                    "decode chain: a link may only wait for an earlier link");
+            require(fp8lin::chain_link_supported(k.N, k.K, k.scale_cols, k.swiglu != 0), FP8LIN_ERR_UNSUPPORTED,
+                    "decode chain: a link needs K % 16 == 0, K <= 9216 (5120 with SwiGLU, N even) and "
+                    "N * K < 2^31");
+            dev[L] = fp8lin::ChainLink{k.codes, k.scales, k.scale_cols, k.N, k.K, k.x, k.y, k.swiglu != 0, k.after};
+        }
+        check_workspace(workspace, workspace_bytes, fp8lin_decode_chain_workspace_bytes(nlinks),
+                        "decode chain: workspace too small");
+        require(workspace != nullptr, FP8LIN_ERR_WORKSPACE, "decode chain: null workspace");
+        ensure_device();
+        check_hip(fp8lin::launch_chain(dev, nlinks, static_cast<uint64_t*>(workspace), as_stream(stream)),
+                  "decode chain launch");
+    });
+}
+
 int fp8lin_gen_weights(uint64_t seed, uint32_t tag, int64_t N, int64_t K, float std_dev,
                        uint8_t* codes, float* scales, fp8lin_stream_t stream) {
     return guarded([&] {

@@ -135,4 +135,23 @@ hipError_t launch_qk_norm_rope(const uint16_t* p, int64_t ld, const uint16_t* qw
 
 hipError_t launch_mfma_ceiling(int64_t iters, float* sink, uint64_t* clocks, hipStream_t stream);
 
+// Decode chain (chain.hip): one-row linear links in one launch; link L waits
+// for link `after` (or nothing when after < 0) before it reads x.  sync:
+// chain_sync_words(nlinks) 64-bit words, zero before the first call of a
+// chain shape: word 0 counts waits that gave up, word 1 the chain's shape,
+// then per-link slot counters and per-XCD call words (chain.hip).
+constexpr int kChainMaxLinks = 8;  // FP8LIN_CHAIN_MAX_LINKS
+struct ChainLink {
+    const uint8_t* codes;
+    const float* scales;
+    int64_t S, N, K;
+    const uint16_t* x;
+    uint16_t* y;
+    bool swiglu;
+    int after;
+};
+bool chain_link_supported(int64_t N, int64_t K, int64_t S, bool swiglu);
+size_t chain_sync_words(int nlinks);
+hipError_t launch_chain(const ChainLink* links, int nlinks, uint64_t* sync, hipStream_t stream);
+
 }  // namespace fp8lin

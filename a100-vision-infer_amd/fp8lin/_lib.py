@@ -44,6 +44,7 @@ EXPORTED = [
     "fp8lin_linear_candidates_static",
     "fp8lin_linear_swiglu_workspace_bytes", "fp8lin_linear_swiglu_ws",
     "fp8lin_linear_workspace_bytes", "fp8lin_linear_ws",
+    "fp8lin_decode_chain_workspace_bytes", "fp8lin_decode_chain",
 ]
 
 
@@ -58,6 +59,16 @@ class Weight(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("scales", ctypes.c_void_p),
                 ("scale_cols", ctypes.c_int64), ("cached_bf16", ctypes.c_void_p),
                 ("N", ctypes.c_int64), ("K", ctypes.c_int64), ("bias", ctypes.c_void_p)]
+
+
+class ChainLink(ctypes.Structure):
+    """struct fp8lin_chain_link"""
+    _fields_ = [("codes", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("scale_cols", ctypes.c_int64),
+                ("N", ctypes.c_int64), ("K", ctypes.c_int64), ("x", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("swiglu", ctypes.c_int), ("after", ctypes.c_int)]
+
+
+CHAIN_MAX_LINKS = 8
 
 
 class LinearOptions(ctypes.Structure):
@@ -99,6 +110,8 @@ def lib():
         "fp8lin_linear": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i32, vp]),
         "fp8lin_linear_ld": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i64, i32, vp]),
         "fp8lin_linear_workspace_bytes": (sz, [i64, i64, i64]),
+        "fp8lin_decode_chain_workspace_bytes": (sz, [i32]),
+        "fp8lin_decode_chain": (i32, [ctypes.POINTER(ChainLink), i32, vp, sz, vp]),
         "fp8lin_linear_ws": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, i32, vp, sz, vp]),
         "fp8lin_linear_swiglu": (i32, [vp, vp, vp, i64, vp, i64, i64, i64, vp]),
         "fp8lin_swiglu": (i32, [vp, vp, i64, i64, vp]),

@@ -409,3 +409,54 @@ def mfma_ceiling(iters, sink, clocks):
     """MFMA-ceiling probe: sink float32 [>=1], clocks int64 [2] (shader-clock
     and 100 MHz ticks of workgroup 0), both on the device."""
     check(lib().fp8lin_mfma_ceiling(int(iters), _ptr(sink), _ptr(clocks), _stream(sink)))
+
+
+def decode_chain_workspace(nlinks, device):
+    """A zeroed workspace for decode_chain with `nlinks` links (64-bit
+    counters that never reset: word 0 counts waits that gave up, word 1 the
+    chain's shape); one serves any number of calls of one chain shape on one
+    stream.  Zero it again (or take another) for a chain of another shape."""
+    return torch.zeros(lib().fp8lin_decode_chain_workspace_bytes(int(nlinks)), dtype=torch.uint8, device=device)
+
+
+def decode_chain(links, workspace=None):
+    """The one-row projections of one decode step in one launch
+    (fp8lin_decode_chain; Engine::step's linear calls at one token,
+    src/engine.cpp:401-421).  links: a sequence of
+    (x, codes, scales, swiglu, after): x a BF16 [1, K] tensor, or the index of
+    an earlier link whose output it is (then `after` defaults to that index);
+    after: an earlier link to wait for before x is read, or -1.  Returns the
+    outputs, each equal to fp8_linear (linear_swiglu with swiglu) of its link
+    bit for bit."""
+    from ._lib import CHAIN_MAX_LINKS, ChainLink
+    n = len(links)
+    if not 1 <= n <= CHAIN_MAX_LINKS:
+        _fail(ERR_SHAPE, f"decode chain: 1 to {CHAIN_MAX_LINKS} links")
+    recs = (ChainLink * n)()
+    outs = []
+    for i, link in enumerate(links):
+        x, codes, scales = link[0], link[1], link[2]
+        swiglu = bool(link[3]) if len(link) > 3 else False
+        after = link[4] if len(link) > 4 and link[4] is not None else (x if isinstance(x, int) else -1)
+        if isinstance(x, int):
+            if not 0 <= x < i:
+                _fail(ERR_ARGUMENT, "decode chain: x must name an earlier link")
+            x = outs[x]
+        _check_x(x, "decode chain: x must be a CUDA BF16 [1,K] tensor")
+        _check_codes(codes, x)
+        sc = _scale_cols(scales, codes.size(0), codes.size(1))
+        if x.size(0) != 1:
+            _fail(ERR_SHAPE, "decode chain: one activation row per link")
+        N = codes.size(0)
+        y = torch.empty((1, N // 2 if swiglu else N), dtype=torch.bfloat16, device=x.device)
+        outs.append(y)
+        r = recs[i]
+        r.codes, r.scales, r.scale_cols = codes.data_ptr(), scales.data_ptr(), sc
+        r.N, r.K = N, codes.size(1)
+        r.x, r.y = x.data_ptr(), y.data_ptr()
+        r.swiglu, r.after = int(swiglu), int(after)
+    dev = outs[0].device
+    if workspace is None:
+        workspace = decode_chain_workspace(n, dev)
+    check(lib().fp8lin_decode_chain(recs, n, _ptr(workspace), workspace.numel(), _stream(outs[0])))
+    return outs

@@ -704,6 +704,35 @@ def layer_chain(torch, fp8lin, dev, rot, log):
             gbs = tot_bytes / (total_ms * 1e-3) / 1e9
             extra["chain_m1_GBs"] = round(gbs, 1)
             log(f"chain M=1: {total_ms * 1e3:.2f} us, {gbs:.1f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% HBM)")
+            # The same four links as one launch (fp8lin_decode_chain) on the
+            # same rotation: each link waiting for the previous one (the
+            # layer's order), and with no waits (the links read inputs
+            # already in HBM), each on a workspace of its own.
+            order = list(shapes)
+
+            def chain_recs(i, strict):
+                recs = (fp8lin._lib.ChainLink * 4)()
+                for j, name in enumerate(order):
+                    n, k, sw = shapes[name]
+                    c, s = weights[name][i % len(weights[name])]
+                    r = recs[j]
+                    r.codes, r.scales, r.scale_cols, r.N, r.K = c.data_ptr(), s.data_ptr(), s.size(1), n, k
+                    r.x, r.y = feeds[name].data_ptr(), outs[name].data_ptr()
+                    r.swiglu, r.after = int(sw), j - 1 if strict else -1
+                return recs
+            for strict, label in ((True, "one_launch"), (False, "one_launch_independent")):
+                cws = torch.zeros(L.fp8lin_decode_chain_workspace_bytes(4), dtype=torch.uint8, device=dev)
+                chain_sets = [chain_recs(i, strict) for i in range(copies)]
+                pms = time_it(lambda i: ok(L.fp8lin_decode_chain(chain_sets[i % copies], 4, P(cws), cws.numel(),
+                                                                 sp)))
+                sync = cws.view(torch.int64).cpu()
+                if sync[0] != 0:
+                    raise RuntimeError(f"decode chain: {int(sync[0])} waits gave up")
+                pgbs = tot_bytes / (pms * 1e-3) / 1e9
+                extra[f"chain_m1_{label}_us"] = round(pms * 1e3, 2)
+                extra[f"chain_m1_{label}_GBs"] = round(pgbs, 1)
+                log(f"chain M=1, one launch (fp8lin_decode_chain), {'each link after the previous' if strict else 'no waits'}: "
+                    f"{pms * 1e3:.2f} us, {pgbs:.1f} GB/s ({100 * pgbs / HBM_PEAK_GBS:.1f}% HBM)")
         else:
             tf = tot_flops / (total_ms * 1e-3) / 1e12
             extra[f"chain_m{m}_TFLOPs"] = round(tf, 1)

@@ -442,6 +442,51 @@ int fp8lin_engine_linear_candidates(const fp8lin_linear_options* options, const 
                                     fp8lin_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Decode chain: the one-row linear layers of one decode step in a single
+ * launch.  Replaces the sequence of Engine::linear calls of Engine::step
+ * (src/engine.cpp:401-421) at one token, which the reference replays as one
+ * captured graph (src/engine.cpp:522-539): link L computes y = x * W^T (with
+ * swiglu, the fused gate/up + SwiGLU of fp8lin_linear_swiglu) for one
+ * activation row, and its output equals fp8lin_linear's
+ * (fp8lin_linear_swiglu's) for M = 1 bit for bit.  A link whose `after` is
+ * an earlier link's index reads x only once that link has stored all its
+ * outputs, so x may be (part of) the output of link `after`; with
+ * after = -1, x must be ready when the call is enqueued.  The workgroups of
+ * the links run in link order, and each issues its weight loads before it
+ * waits, so HBM stays busy across the links.
+ * Requirements per link: K % 16 == 0, K <= 9216 (with swiglu, N even and
+ * K <= 5120), scale_cols 1 or ceil(K/128), N * K < 2^31; the outputs of the
+ * links do not overlap each other or any weight, and a link's output
+ * overlaps only the x of links that wait for it.
+ * Workspace: fp8lin_decode_chain_workspace_bytes(nlinks) bytes (16-byte
+ * aligned) of 64-bit counters, all zero before the first call on it.  The
+ * counters never reset, so one zeroed workspace serves any number of calls
+ * of ONE chain shape (the links' N, K, swiglu and after) on one stream and
+ * device; calls that may overlap, or a chain of another shape, need their
+ * own (or a workspace zeroed again).  Word 0 counts the waits that gave up:
+ * a link's input not complete after about 2^20 polls (which only a grid
+ * that cannot stay resident, e.g. beside other kernels on a shared GPU, can
+ * cause), or, at once, every wait of a chain given a workspace that counted
+ * a chain of another shape (word 1 records the shape).  A call that adds to
+ * word 0 has wrong outputs.  No counterpart in the reference's operator
+ * set.
+ */
+#define FP8LIN_CHAIN_MAX_LINKS 8
+typedef struct fp8lin_chain_link {
+    const uint8_t* codes;  /* E4M3FN [N, K] */
+    const float* scales;   /* [N] or [N, ceil(K/128)] */
+    int64_t scale_cols;    /* 1 or ceil(K/128) */
+    int64_t N, K;
+    const uint16_t* x;     /* BF16 [1, K] */
+    uint16_t* y;           /* BF16 [1, N], or [1, N/2] with swiglu */
+    int swiglu;            /* rows [0, N/2) gate, [N/2, N) up; y = SwiGLU */
+    int after;             /* index of an earlier link to wait for, or -1 */
+} fp8lin_chain_link;
+size_t fp8lin_decode_chain_workspace_bytes(int nlinks);
+int fp8lin_decode_chain(const fp8lin_chain_link* links, int nlinks, void* workspace, size_t workspace_bytes,
+                        fp8lin_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Deterministic synthetic inputs (no reference counterpart; used by the
  * benchmark and tests so that the device and a host checker see the same
  * bits).  Element i of stream `tag` is a standard normal from Philox4x32-10

@@ -360,3 +360,44 @@ def test_linear_ws_validation(fp8lin):
                               None) == fp8lin.ERR_WORKSPACE
     assert L.fp8lin_linear_ws(None, P, P, 40, P, 512, 7168, 5120, 0, P, need, None) == fp8lin.ERR_ARGUMENT
     assert L.fp8lin_linear_ws(P, P, P, 40, P, 0, 7168, 5120, 0, P, need, None) == fp8lin.ERR_SHAPE
+
+
+def _chain(fp8lin, specs):
+    """ChainLink records with fake (never dereferenced) pointers:
+    specs = [(N, K, scale_cols, swiglu, after)]."""
+    recs = (fp8lin._lib.ChainLink * len(specs))()
+    for r, (n, k, sc, sw, after) in zip(recs, specs):
+        r.codes = r.scales = r.x = r.y = 0x10000
+        r.scale_cols, r.N, r.K, r.swiglu, r.after = sc, n, k, sw, after
+    return recs
+
+
+@pytest.mark.parametrize("specs,ws,code", [
+    ([], 256, 1),                                                # no links
+    ([(16, 16, 1, 0, -1)] * 9, 256, 1),                          # more than FP8LIN_CHAIN_MAX_LINKS
+    ([(16, 16, 1, 0, 0)], 256, 2),                               # a link waits for itself
+    ([(16, 16, 1, 0, -1), (16, 16, 1, 0, 1)], 256, 2),           # ... or a later link
+    ([(16, 16, 1, 0, -1), (16, 16, 1, 0, -2)], 256, 2),          # after < -1
+    ([(16, 16, 3, 0, -1)], 256, 2),                              # scale_cols not in {1, ceil(K/128)}
+    ([(16, 24, 1, 0, -1)], 256, 3),                              # K % 16 != 0
+    ([(16, 9232, 1, 0, -1)], 256, 3),                            # K > 9216
+    ([(16, 5136, 1, 1, -1)], 256, 3),                            # SwiGLU with K > 5120
+    ([(15, 512, 4, 1, -1)], 256, 3),                             # SwiGLU with N odd
+    ([(0, 512, 4, 0, -1)], 256, 1),                              # N == 0
+    ([(16, 512, 4, 0, -1)], 0, 4),                               # no workspace
+    ([(16, 512, 4, 0, -1)] * 4, 256, 4),                         # workspace too small for 4 links
+])
+def test_decode_chain_validation(fp8lin, specs, ws, code):
+    """fp8lin_decode_chain rejects bad chains before touching a device."""
+    L = fp8lin.lib()
+    recs = _chain(fp8lin, specs) if specs else (fp8lin._lib.ChainLink * 1)()
+    assert L.fp8lin_decode_chain(recs, len(specs), P if ws else None, ws, None) == code
+    assert L.fp8lin_last_error()
+
+
+def test_decode_chain_workspace_bytes(fp8lin):
+    L = fp8lin.lib()
+    assert L.fp8lin_decode_chain_workspace_bytes(0) == 0
+    assert L.fp8lin_decode_chain_workspace_bytes(9) == 0
+    for n in range(1, 9):  # a 128-byte line for the timeouts, 256 lines of slot counters and 8 XCD words per link
+        assert L.fp8lin_decode_chain_workspace_bytes(n) == (128 + n * (256 * 128 + 8 * 256) + 255) // 256 * 256
