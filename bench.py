@@ -28,6 +28,9 @@ METRIC = "FP8 GEMV HBM GB/s (% peak) at M=1; prefill GEMM TFLOP/s (% MFMA peak)"
 # (68.0 KiB); the factors are what the counters read for a 256 MiB device copy
 # (`bench.py --calibrate`).  Re-measure when the kernel changes.
 GATE_UP_TRAFFIC_BYTES = 92_152_013
+# One M=4096 gate/up+SwiGLU prefill call (gemm_fp8_kernel<8, true> and its
+# tail_reduce_kernel), copy-calibrated FETCH_SIZE x2 + WRITE_SIZE, rotated.
+PREFILL_TRAFFIC_BYTES = 1_119_594_086
 # MFMA busy fraction of the prefill kernel over its whole dispatch (M=4096
 # gate/up+SwiGLU), one --pmc pass: SQ_VALU_MFMA_BUSY_CYCLES summed over the
 # 1024 SIMDs, per SIMD, over the dispatch's cycles.  GRBM_GUI_ACTIVE comes back
@@ -277,7 +280,10 @@ def main():
             "algorithmic_flop_per_call": 2 * 4096 * 17408 * 5120,
             "mfma_busy": PREFILL_MFMA_BUSY,
             "mfma_busy_source": PREFILL_MFMA_BUSY_SOURCE,
-            "traffic": None,
+            "traffic": PREFILL_TRAFFIC_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE x2.000 + WRITE_SIZE x1.000 (copy-calibrated), "
+                              "GEMM + tail reduce of one call",
+            "algorithmic_bytes_per_call": 4096 * 5120 * 2 + 17408 * 5120 + 17408 * 40 * 4 + 4096 * 8704 * 2,
         }
     print(json.dumps(out), flush=True)
 

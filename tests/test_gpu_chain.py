@@ -95,6 +95,8 @@ def test_chain_layer_and_head(fp8lin, gpu, oracle):
     assert_parity(bits(outs[1]), oracle.swiglu(ref_gu), "chain gate/up+SwiGLU", elementwise=False)
     assert_parity(bits(outs[2]), oracle.linear(bits(outs[1]), w[2][0].cpu().numpy(), w[2][1].cpu().numpy()),
                   "chain down")
+    assert_parity(bits(outs[3]), oracle.linear(bits(outs[2]), w[3][0].cpu().numpy(), w[3][1].cpu().numpy()),
+                  "chain head")
 
 
 def rand_case(rng, gpu, n, k, per_row=False):
