@@ -69,7 +69,7 @@ hipError_t launch_gemm(const uint16_t* x, const void* w, const float* scales, in
 // (0 when nothing splits); a smaller or unaligned workspace, unaligned x or
 // w, or another kernel's shape run unsplit.
 size_t gemm_workspace_bytes(int S, int64_t ldy, int M, int N, int K, bool swiglu);
-// Whether the GEMM dispatch sends this FP8 call (9..16 rows) to the small-M
+// Whether the GEMM dispatch sends this FP8 call (9..32 rows) to the small-M
 // matrix-core kernel instead of a GEMM tile.
 bool gemm_mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K);
 hipError_t launch_gemm_ws(const uint16_t* x, const void* w, const float* scales, int S, uint16_t* y, int64_t ldy,

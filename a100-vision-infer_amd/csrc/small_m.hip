@@ -93,18 +93,23 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, 
 //     (wave w takes blocks w, w + W, ...); their partial sums are added in
 //     LDS in wave order.
 // MX (8, 16 or 32: one or two 16-row MFMA tiles) bounds the activation rows
-// a launch may have.
-template <int W, int D, int NBW, int XA, int MX>
+// a launch may have.  TL row tiles per workgroup (K-split form): the waves
+// w / (W / TL) = t hold tile t's rows and split its blocks as W / TL waves
+// would alone, sharing one set of activation buffers.
+template <int W, int D, int NBW, int XA, int MX, int TL = 1>
 struct SmallCfg {
     static_assert(MX == 8 || MX == 16 || MX == 32, "8, 16 or 32 activation rows");
     static constexpr int T = MX > 16 ? 2 : 1;  // 16-row activation tiles
     static constexpr bool KSPLIT = NBW < 4;
     static constexpr int ROWS = KSPLIT ? 16 : 16 * W;
+    static constexpr int TW = W / TL;  // waves per row tile
     static constexpr int XBUFS = XA + 1;
     static constexpr int XQ = MX / W;  // activation rows DMA'd per wave per chunk
     static constexpr int CS = XQ + 1;
     static constexpr int W0 = wait0(D, CS, NBW, XA), W1 = wait1(D, CS, NBW, XA);
-    static_assert(W * NBW == 4 || NBW == 4, "a chunk's blocks are split evenly");
+    static_assert(TL == 1 || (KSPLIT && W % TL == 0), "row tiles split the waves evenly");
+    static_assert(XQ >= 1, "every wave stages activation rows");
+    static_assert(TW * NBW == 4 || NBW == 4, "a chunk's blocks are split evenly");
     static_assert(D % NBW == 0 && W0 <= 63 && W1 <= 63, "ring depth");
     static constexpr size_t lds(int M) {
         return (size_t)W * D * 2048 + (size_t)XBUFS * (M + 1) * kRowX + (size_t)W * XBUFS * 256;
@@ -121,13 +126,13 @@ struct SmallCfg {
 // its slot, so the outputs are fused_swiglu of the plain kernel's, bit for
 // bit.  Also requires N * K / 32 < 2^31 (scale offsets over the whole
 // matrix).
-template <int W, int D, int NBW, int XA, int MX, bool SW>
+template <int W, int D, int NBW, int XA, int MX, bool SW, int TL = 1>
 __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restrict__ x,
                                                          const uint8_t* __restrict__ codes,
                                                          const float* __restrict__ scales,
                                                          uint16_t* __restrict__ y, int64_t ldy, int M, int N,
                                                          int K, int per) {
-    using C = SmallCfg<W, D, NBW, XA, MX>;
+    using C = SmallCfg<W, D, NBW, XA, MX, TL>;
     static_assert(!SW || C::KSPLIT, "the SwiGLU form pairs the 16 rows of one workgroup");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -135,13 +140,16 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const int KB = K >> 7;
     const int nchunks = (KB + 3) >> 2;
+    // the wave's row tile and its place among the tile's waves
+    const int tile = wave / C::TW, wt = wave % C::TW;
     // this wave's first row and its row count
-    const int64_t nw = C::KSPLIT ? (int64_t)blockIdx.x * per : (int64_t)blockIdx.x * C::ROWS + 16 * wave;
+    const int64_t nw = C::KSPLIT ? ((int64_t)blockIdx.x * TL + tile) * per
+                                 : (int64_t)blockIdx.x * C::ROWS + 16 * wave;
     const int rows_here = (int)max((int64_t)0, min((int64_t)(C::KSPLIT ? per : 16), (int64_t)N - nw));
     // SW: output pairs pb..pb+pairs-1 (gate row pb + r in slot r, up row
     // half + pb + r in slot 8 + r)
     const int half = N >> 1;
-    const int64_t pb = (int64_t)blockIdx.x * per;
+    const int64_t pb = ((int64_t)blockIdx.x * TL + tile) * per;
     const int pairs = (int)max((int64_t)0, min((int64_t)per, (int64_t)half - pb));
     const int xbuf = (M + 1) * kRowX;
     const uint32_t o_codes = (uint32_t)(wave * D * 2048);
@@ -173,7 +181,7 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     // Own block j of this wave -> global block index.
     auto gblk = [&](int j) __attribute__((always_inline)) -> int {
         const int c = j / NBW, p = j % NBW;
-        return 4 * c + (C::KSPLIT ? wave + W * p : p);
+        return 4 * c + (C::KSPLIT ? wt + C::TW * p : p);
     };
     // DMA lane offsets.  Codes, instruction q: lane -> row 8q + lane/8, LDS
     // position lane%8 <- chunk (lane%8) ^ sw(row) of the block's 128 codes.
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
             ([&]() __attribute__((always_inline)) {
                 constexpr int p = P;
                 const int j = NBW * c + p;
-                const int b = C::KSPLIT ? wave + W * p : p;  // block within the chunk
+                const int b = C::KSPLIT ? wt + C::TW * p : p;  // block within the chunk
                 if constexpr (p == 0) {
                     // this chunk's activations, scales and first block landed in
                     // every wave, and every wave is done with the buffers of
@@ -303,15 +311,17 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
 #pragma unroll
             for (int i = 0; i < 4; ++i) red[wave * 256 * T + (16 * tt + 4 * g + i) * 16 + row] = acc[tt][i];
         __syncthreads();
-        if (wave != 0) return;
+        if (wt != 0) return;
+        // the tile's waves in order
+        const float* tr = red + tile * C::TW * 256 * T;
 #pragma unroll
         for (int tt = 0; tt < T; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int e = (16 * tt + 4 * g + i) * 16 + row;
-                float t = red[e];
+                float t = tr[e];
 #pragma unroll
-                for (int w = 1; w < W; ++w) t = t + red[w * 256 * T + e];
+                for (int w = 1; w < C::TW; ++w) t = t + tr[w * 256 * T + e];
                 total[tt][i] = t;
             }
     } else {
@@ -349,19 +359,20 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
     }
 }
 
-// per: rows (pairs for SW) of each workgroup.
-template <int W, int D, int NBW, int XA, int MX, bool SW>
+// per: rows (pairs for SW) of each row tile, TL tiles per workgroup.
+template <int W, int D, int NBW, int XA, int MX, bool SW, int TL = 1>
 hipError_t launch(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy, int M,
                   int N, int K, int per, hipStream_t stream) {
-    using C = SmallCfg<W, D, NBW, XA, MX>;
-    auto kern = small_m_kernel<W, D, NBW, XA, MX, SW>;
+    using C = SmallCfg<W, D, NBW, XA, MX, TL>;
+    auto kern = small_m_kernel<W, D, NBW, XA, MX, SW, TL>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       (int)C::lds(MX));
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
     if (attr != hipSuccess) return attr;
     static_assert(C::KSPLIT, "rows per workgroup are set at run time only in the K-split form");
-    const int groups = SW ? (N / 2 + per - 1) / per : (N + per - 1) / per;
+    const int tiles = SW ? (N / 2 + per - 1) / per : (N + per - 1) / per;
+    const int groups = (tiles + TL - 1) / TL;
     const size_t lds = C::lds(M);
+    if (lds > (size_t)kMaxLds) return hipErrorInvalidValue;
     hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * W), lds, stream, x, codes, scales, y, ldy, M, N, K, per);
     return hipGetLastError();
 }
@@ -404,9 +415,9 @@ constexpr int stream_lds_fixed() {
 }
 constexpr int floordiv(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 
-// Requirements (checked by the host): 1 <= M <= 16, K % 128 == 0,
-// 8 * (NB - 1) < K / 128 <= 8 * NB, N * K < 2^31, per * M * 2 bytes of LDS
-// beyond stream_lds_fixed.
+// Requirements (checked by the host): 1 <= M <= 16 T (T = 2, two activation
+// tiles, only with NB <= 5), K % 128 == 0, 8 * (NB - 1) < K / 128 <= 8 * NB,
+// N * K < 2^31, per * M * 2 bytes of LDS beyond stream_lds_fixed.
 // SW: gate/up + SwiGLU (N weight rows, gate [0, N/2), up [N/2, N); y is
 // [M, N/2]).  The units of the ranges and pieces are then output pairs: a
 // piece of pr <= 8 pairs holds its gate rows in slots 0..pr-1 and their up
@@ -680,14 +691,19 @@ int stream_nb(int K) {
 
 }  // namespace
 
-// Four waves share 16 weight rows and split every chunk's 4 blocks, with a
-// 4-block ring each.  Activations are prefetched 3 chunks ahead for 4 < M <= 8
-// (73 KiB of LDS at M = 8, two workgroups per CU) and 2 chunks ahead for
-// M <= 4, which brings the LDS under 54 KiB and fits three workgroups per CU:
-// 7% faster on the 75968-row head at M = 2 and 4, the same elsewhere.  The
-// prefetch distance does not change the arithmetic.  Measured on MI355X at
-// the decode shapes (M = 2..8) this beats 64-row workgroups (the NBW == 4
-// form) for every shape, and deeper rings that leave one workgroup per CU.
+// At M <= 8 a workgroup holds two row tiles (about one workgroup per CU):
+// four waves per tile split every chunk's 4 blocks, each with a 3-block
+// ring, and the eight waves share the activation buffers, staged 2 chunks
+// ahead (83 KiB of LDS at M = 8).  Each tile sums exactly as a four-wave
+// workgroup alone would.  Measured on MI355X at the narrow decode shapes
+// (graph replay, rotated weights; down 5120 x 8704 / QKV-gate 7168 x 5120 at
+// M = 8): 13.6 / 10.8 us against 14.4 / 11.5 with one tile per workgroup
+// (two workgroups per CU), and deeper prefetch was slower in both forms
+// (one tile: 3 chunks ahead at M = 8; two tiles: a 5-block ring 4 chunks
+// ahead 14.6 / 11.8 us, 6 blocks 5 ahead slower still at M <= 4).  9..16
+// rows keep one tile per workgroup (16 activation rows staged per chunk).
+// Measured on MI355X at the decode shapes (M = 2..8) the K-split tiles beat
+// 64-row workgroups (the NBW == 4 form) for every shape.
 //
 // The stream kernel serves N >= 32 rows per compute unit (measured on MI355X
 // at M = 2, 4, 8: 17408 x 5120 gate/up 16-18% faster, the 75968-row head
@@ -765,10 +781,10 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
                                                 stream, nullptr);
         return dispatch_stream<false, false>(nb, x, codes, scales, y, ldy, M, N, K, per_rows, stream, nullptr);
     }
-    // Rows per workgroup: about two workgroups per CU, 8..16 rows (4..8
-    // pairs), so every CU streams about the same number of rows in one round
-    // (16-row workgroups left the 5120-row down projection at 1.25 per CU,
-    // a quarter of the CUs streaming a second workgroup alone).
+    // Rows per tile: about two tiles per CU, 8..16 rows (4..8 pairs), so
+    // every CU streams about the same number of rows in one round (16-row
+    // tiles left the 5120-row down projection at 1.25 per CU, a quarter of
+    // the CUs streaming a second one alone).
     const int units = swiglu ? N / 2 : N;
     const int per = std::clamp((units + 2 * cus - 1) / (2 * cus), swiglu ? 4 : 8, swiglu ? 8 : 16);
     if (M > kMaxM) {
@@ -788,13 +804,11 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
     // faster).
     const bool xa2 = 2 * SmallCfg<4, 4, 1, 2, 16>::lds(M) <= (size_t)kMaxLds;
     if (swiglu) {
-        if (M <= 4) return launch<4, 4, 1, 2, 8, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-        if (M <= 8) return launch<4, 4, 1, 3, 8, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        if (M <= 8) return launch<8, 3, 1, 2, 8, true, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
         if (xa2) return launch<4, 4, 1, 2, 16, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
         return launch<4, 4, 1, 1, 16, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
     }
-    if (M <= 4) return launch<4, 4, 1, 2, 8, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
-    if (M <= 8) return launch<4, 4, 1, 3, 8, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    if (M <= 8) return launch<8, 3, 1, 2, 8, false, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
     if (xa2) return launch<4, 4, 1, 2, 16, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
     return launch<4, 4, 1, 1, 16, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
 }

@@ -435,7 +435,8 @@ def secondary(torch, fp8lin, dev, rot, log, sections, prefill_m=(128, 512, 1024,
         del xa, wb
     # The drop-in operator (fp8_linear through fp8lin_linear_ws, as the ATen
     # shim calls it) on the prefill projections whose tiles leave CUs idle,
-    # against the same call without a workspace (every tile whole).
+    # against the same call without a workspace (every tile whole); graph
+    # replays over the rotation, as the chain section times the engine branch.
     for name, n, k in (SHAPES[1:] if "prefill" in sections else ()):
         for m in (64, 512):
             x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
@@ -453,7 +454,7 @@ def secondary(torch, fp8lin, dev, rot, log, sections, prefill_m=(128, 512, 1024,
                         ok(L.fp8lin_linear_ws(P(x), P(c), P(s), s.size(1), P(y), m, n, k, 1, P(lws), need, sp))
                     else:
                         ok(L.fp8lin_linear(P(x), P(c), P(s), s.size(1), P(y), m, n, k, 1, sp))
-                ms = timed(torch, call, 2 * len(copies), warm=len(copies))
+                ms = graph_timed(torch, call, sp, reps=2 * len(copies), replays=5)
                 tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
                 extra[f"dropin_m{m}_{name}_{label}_us"] = round(ms * 1e3, 2)
                 log(f"fp8_linear M={m} {name} ({label}): {ms * 1e3:.2f} us {tf:.1f} TFLOP/s")
