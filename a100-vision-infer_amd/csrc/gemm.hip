@@ -144,8 +144,8 @@ hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, 
 // small-M matrix-core kernel (small_m.hip), whose 16x16 MFMA tile holds all
 // of them, streams the codes once with each dequantized once; a GEMM tile
 // would be at least seven eighths padding.  17..32 rows in its row-range
-// form with two activation tiles (at least 24 weight rows per CU, K <=
-// 5120), else in its 16-row workgroups with two activation tiles.  Its geometry limits are
+// form with two activation tiles (at least 32 weight rows per CU, K <=
+// 5120), else in its K-split 16-row tiles with two activation tiles.  Its geometry limits are
 // those of the decode routing (block scales [N, K/128], 16-byte aligned x
 // and codes).
 bool mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K) {

@@ -711,11 +711,12 @@ int stream_nb(int K) {
 // per CU) the 16-row workgroups stay faster, also against equal pieces of 14
 // and 10 rows (6-12% slower: fewer code bytes in flight per CU).
 constexpr int kStreamRowsPerCu = 32;
-// With two activation tiles every code byte feeds twice the MFMAs, and one
-// pass beats two passes of the 16-row workgroups from 24 rows per CU: the
-// 7168-row QKV-gate (28 per CU) at M = 17 / 24 / 32 in 15.2 / 16.9 / 18.8 us
-// against 22.1 / 22.4 / 23.7 (measured on MI355X).
-constexpr int kStreamRowsPerCuT2 = 24;
+// With two activation tiles (17..32 rows) the row-range kernel serves 32 rows
+// per CU and more, as with one: the 7168-row QKV-gate (28 per CU) at M = 17 /
+// 24 / 32 runs 13.7 / 14.5 / 14.6 us in the K-split tiles (two per
+// workgroup), against 15.3 / 17.1 / 18.9 in the row-range kernel (measured
+// on MI355X).
+constexpr int kStreamRowsPerCuT2 = 32;
 
 namespace {
 
@@ -788,29 +789,25 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
     const int units = swiglu ? N / 2 : N;
     const int per = std::clamp((units + 2 * cus - 1) / (2 * cus), swiglu ? 4 : 8, swiglu ? 8 : 16);
     if (M > kMaxM) {
-        // 17..32 rows off the row-range form: the same workgroups with two
+        // 17..32 rows off the row-range form: the same tiles with two
         // activation tiles (32 rows staged per chunk, 1 chunk ahead; each
-        // code word feeds both tiles).  Down at M = 17 / 24 / 32: 20.7 /
-        // 29.8 / 30.5 us, against 29.2 / 30.0 / 32.1 for two passes of 16
-        // rows and 36 in the split-K GEMM (two workgroups per CU fit up to
-        // M = 21).
+        // code word feeds both).  Down at M = 24 / 32: 19.8 / 20.0 us with
+        // two row tiles per workgroup, against 30.8 / 31.0 with one (two
+        // workgroups per CU fit up to M = 21), 29.2 / 32.1 for two passes
+        // of 16 rows and 36 in the split-K GEMM.
         if (M > kStreamMaxM) return hipErrorNotSupported;
-        if (swiglu) return launch<4, 4, 1, 1, 32, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-        return launch<4, 4, 1, 1, 32, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        if (swiglu) return launch<8, 3, 1, 1, 32, true, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        return launch<8, 3, 1, 1, 32, false, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
     }
-    // 9..16 rows: activations 2 chunks ahead while two workgroups still fit
-    // per CU (M <= 13), else 1 (measured at M = 16: 13.3 against 16.9 us at
-    // QKV-gate, 17.9 against 21.9 at down; at M = 9 two chunks ahead are 3%
-    // faster).
-    const bool xa2 = 2 * SmallCfg<4, 4, 1, 2, 16>::lds(M) <= (size_t)kMaxLds;
+    // 9..16 rows: activations 2 chunks ahead (down / QKV-gate at M = 16:
+    // 15.8 / 12.7 us with two row tiles per workgroup, against 18.6 / 13.9
+    // with one tile per workgroup and two workgroups per CU).
     if (swiglu) {
         if (M <= 8) return launch<8, 3, 1, 2, 8, true, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
-        if (xa2) return launch<4, 4, 1, 2, 16, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
-        return launch<4, 4, 1, 1, 16, true>(x, codes, scales, y, ldy, M, N, K, per, stream);
+        return launch<8, 3, 1, 2, 16, true, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
     }
     if (M <= 8) return launch<8, 3, 1, 2, 8, false, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
-    if (xa2) return launch<4, 4, 1, 2, 16, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
-    return launch<4, 4, 1, 1, 16, false>(x, codes, scales, y, ldy, M, N, K, per, stream);
+    return launch<8, 3, 1, 2, 16, false, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
 }
 
 }  // namespace fp8lin

@@ -738,8 +738,10 @@ def test_linear_mid_rows(fp8lin, gpu, oracle, m, n, k):
     small-M matrix-core kernel, whose 16x16 MFMA tile holds every row (the
     16-row workgroups at n = 2056 and 1040, the row-range form at n = 8208 and
     8240), instead of a mostly-padding GEMM tile; 17..32 rows run the
-    row-range form with two activation tiles (n >= 24 rows per CU, k <= 5120:
-    8208, 8240, 7168) or 16-row workgroups with two activation tiles.  Every output against the
+    row-range form with two activation tiles (n >= 32 rows per CU, k <= 5120:
+    8208, 8240) or the K-split 16-row tiles with two activation tiles (7168,
+    5120, 2056), each with the K partition of its 16-row form, so the first 16
+    rows' outputs are those of a 16-row call.  Every output against the
     FP64 oracle; the fused SwiGLU bit-equal to fused_swiglu(fp8_linear), with
     or without a workspace (none is needed); Engine::linear's FP8 GEMM branch
     asks for no workspace and gives the same bits; an unaligned view of x
@@ -754,9 +756,8 @@ def test_linear_mid_rows(fp8lin, gpu, oracle, m, n, k):
     c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
     y = F.fp8_linear(xg, c, s)
     assert_parity(bits(y), ref, f"mid rows {m}x{n}x{k}")
-    if m > 16 and n != 7168:
-        # the second activation tile changes no output's summation (at n = 7168, 28 rows per CU, 16 rows run the 16-row
-        # workgroups, another K partition: the oracle bar above holds there)
+    if m > 16:
+        # the second activation tile changes no output's summation
         assert torch.equal(F.fp8_linear(xg[:16], c, s), y[:16])
     assert F.lib().fp8lin_linear_swiglu_workspace_bytes(m, n, k) == 0
     fused = F.linear_swiglu(xg, c, s, split=False)
