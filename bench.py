@@ -454,7 +454,7 @@ def secondary(torch, fp8lin, dev, rot, log, sections, prefill_m=(128, 512, 1024,
                         ok(L.fp8lin_linear_ws(P(x), P(c), P(s), s.size(1), P(y), m, n, k, 1, P(lws), need, sp))
                     else:
                         ok(L.fp8lin_linear(P(x), P(c), P(s), s.size(1), P(y), m, n, k, 1, sp))
-                ms = graph_timed(torch, call, sp, reps=2 * len(copies), replays=5)
+                ms = graph_timed(torch, call, sp, reps=2 * len(copies), replays=10)
                 tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
                 extra[f"dropin_m{m}_{name}_{label}_us"] = round(ms * 1e3, 2)
                 log(f"fp8_linear M={m} {name} ({label}): {ms * 1e3:.2f} us {tf:.1f} TFLOP/s")
