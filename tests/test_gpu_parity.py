@@ -181,8 +181,9 @@ def test_tensor_small_wide(fp8lin, gpu, oracle, n, k, m):
     most 16 rows, as equal as the range allows (33 rows: 11 + 11 + 11; 36:
     12 x 3; 47: 16 + 16 + 15; 32: 16 + 16), each K band (4096, 5120, 9216)
     and a K with one block in the last step (4224); the decode down and
-    QKV-gate shapes and two of 17 rows per CU run the 16-row workgroups.
-    Every row against the FP64 oracle; split 1 and 4 bit-equal."""
+    QKV-gate shapes and two of 17 rows per CU run the row-staged form (one
+    workgroup of up to 32 rows per CU, M <= 8).  Every row against the FP64
+    oracle; split 1 and 4 bit-equal."""
     rng = np.random.default_rng(n + k + m)
     codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
     codes[(codes == 127) | (codes == 255)] = 0
@@ -701,10 +702,11 @@ def test_engine_workspace_under_capture(fp8lin, gpu, oracle):
                                    (2, 2064, 5248), (6, 1040, 8704)])
 def test_linear_small_m_rows(fp8lin, gpu, oracle, m, n, k):
     """fp8_linear with 2..8 rows (3..8, or 2 at K > 5120) against more than
-    1024 weight rows runs the small-M matrix-core kernel: the 16-row
-    workgroups (n = 2056, 2064, 1040: ragged last group and, for SwiGLU, a
-    ragged last group of pairs) or the persistent row-range form (n = 8208:
-    32 rows per CU and more, 17 pairs per range in pieces of 6).  Every output
+    1024 weight rows runs the small-M matrix-core kernel: the row-staged
+    form (n = 2056, 2064, 1040: 8 or 9 rows per workgroup, 4 or 5 SwiGLU
+    pairs, both tiles ragged; K tails of 384, 5248 and 8704 within the last
+    1024-wide stage) or the persistent row-range form (n = 8208: 32 rows per
+    CU and more, 17 pairs per range in pieces of 6).  Every output
     against the FP64 oracle; fp8_tensor_small bit-equal (the same kernel);
     the fused SwiGLU bit-equal to fused_swiglu(fp8_linear); an unaligned
     view of x runs the multi-row GEMV, at the bar."""
@@ -727,6 +729,36 @@ def test_linear_small_m_rows(fp8lin, gpu, oracle, m, n, k):
     assert_parity(bits(fp8lin.fp8_linear(xu, c, s, True)), ref, f"unaligned x {m}x{n}x{k}")
     assert_parity(bits(fp8lin.linear_swiglu(xu, c, s, split=False)), oracle.swiglu(ref),
                   f"unaligned x swiglu {m}x{n}x{k}", elementwise=False)
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 8190, 9216), (7, 8190, 9216), (5, 300, 1152), (2, 1154, 2176),
+                                   (4, 2050, 8192)])
+def test_small_m_row_staged_limits(fp8lin, gpu, oracle, m, n, k):
+    """The row-staged small-M form at its limits: 32 rows (16 SwiGLU pairs)
+    per workgroup with K = 9216 (the 72-block scale table of 32 rows, nine
+    stages), one or two rows per workgroup with a last stage of one block
+    (K = 1152), a last stage of 128 of 1024 values at an odd pair count
+    (1154 rows, 577 pairs), and K a whole number of stages.  Every output of
+    fp8_tensor_small (the small-M kernel at any row count) against the FP64
+    oracle, split 1 and 4 bit-equal; where fp8_linear takes the same kernel
+    (more than 1024 rows, 3..8 activation rows or 2 at K > 5120) it gives
+    the same bits; the fused SwiGLU bit-equal to fused_swiglu(fp8_linear)."""
+    rng = np.random.default_rng(m * 7919 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    yt = fp8lin.fp8_tensor_small(xg, c, s, 1)
+    assert_parity(bits(yt), ref, f"row-staged {m}x{n}x{k}")
+    assert torch.equal(fp8lin.fp8_tensor_small(xg, c, s, 4), yt)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"fp8_linear {m}x{n}x{k}")
+    if n > 1024 and (m > 2 or k > 5120):
+        assert torch.equal(y, yt)
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
 
 
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
