@@ -129,8 +129,8 @@ void check_scales(const float* scales, int64_t scale_cols, int64_t K) {
 // dequantizes each code once (measured 1.4-2.2x faster than the 4- and
 // 8-row GEMV at the decode shapes).  It takes block scales [N, K/128],
 // K % 128 == 0, 16-byte aligned x and codes and 16 K < 2^31; weights of at
-// most 1024 rows keep the GEMV (16-row workgroups would leave most CUs idle),
-// and so do two rows at K <= 5120, where the two-row ring GEMV is faster.
+// most 1024 rows keep the GEMV (four rows or fewer per CU), and so do two
+// rows at K <= 5120, where the two-row ring GEMV is faster.
 bool linear_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t M, int64_t N, int64_t K) {
     return M >= 2 && M <= 8 && (M > 2 || K > 5120) && N > 1024 && K % 128 == 0 && S == K / 128 &&
            aligned16(x) && aligned16(codes) && 16 * K < kMaxDim && N * S * 4 < kMaxDim;

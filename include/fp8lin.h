@@ -391,9 +391,10 @@ int fp8lin_merge_candidates(const double* gathered, int64_t ranks, int64_t rows,
  * codes, K % 16 == 0 and K <= 9216, K <= 5120 at M = 2) the GEMV's epilogue
  * emits one {max, column} pair per workgroup and no logits are written
  * (src/dual_path.cu:37-55 fused into the projection); where it runs the
- * small-M matrix-core kernel's row-range form (3..16 rows, or 2 at
- * K > 5120, against at least 32 weight rows per compute unit) that kernel
- * does the same, one pair per workgroup and row; otherwise the logits
+ * small-M matrix-core kernel's row-range form (3..32 rows, or 2 at
+ * K > 5120, against at least 32 weight rows per compute unit; 17..32 rows
+ * at K <= 5120) that kernel does the same, one pair per workgroup and row;
+ * otherwise the logits
  * [M, N] and the chunk pairs go to the workspace.  Workspace: the bytes
  * below, 16-byte aligned, any content.  Requirements of fp8lin_linear and
  * fp8lin_vocab_candidates.
