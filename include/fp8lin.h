@@ -394,10 +394,9 @@ int fp8lin_merge_candidates(const double* gathered, int64_t ranks, int64_t rows,
  * small-M matrix-core kernel's row-range form (3..32 rows, or 2 at
  * K > 5120, against at least 32 weight rows per compute unit; 17..32 rows
  * at K <= 5120) that kernel does the same, one pair per workgroup and row;
- * otherwise the logits
- * [M, N] and the chunk pairs go to the workspace.  Workspace: the bytes
- * below, 16-byte aligned, any content.  Requirements of fp8lin_linear and
- * fp8lin_vocab_candidates.
+ * otherwise the logits [M, N] and the chunk pairs go to the workspace.
+ * Workspace: the bytes below, 16-byte aligned, any content.  Requirements
+ * of fp8lin_linear and fp8lin_vocab_candidates.
  */
 size_t fp8lin_linear_candidates_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int fp8lin_linear_candidates(const uint16_t* x, const uint8_t* codes, const float* scales,
