@@ -40,10 +40,12 @@
 // granularity that leaves a partial last round (1088 workgroups over 512
 // slots at the 17408-row gate/up).  See the kernel for its pipeline.
 //
-// Narrower weights at M <= 8 (up to 32 rows per compute unit) run
+// At M <= 8, weights of up to 32 rows per compute unit run
 // small_m_row_kernel: one workgroup per compute unit streams its rows 1 KiB
 // of one row per DMA instruction, with the activations staged beside the
-// codes (see that kernel).
+// codes (see that kernel); 33..80 rows per compute unit at K <= 5120 run its
+// wide form, small_m_row_wide_kernel (512 bytes of each row per stage, up to
+// 5 tiles), where measured faster than the row-range kernel.
 #include <algorithm>
 #include <utility>
 
@@ -927,6 +929,240 @@ hipError_t launch_row(const uint16_t* x, const uint8_t* codes, const float* scal
     return hipGetLastError();
 }
 
+// ---- row-staged form for wider weights --------------------------------------
+//
+// The same scheme for 33..80 rows per CU (K <= 5120): up to 5 16-row tiles
+// per workgroup, so the stages hold 512 bytes of each row (one DMA moves two
+// rows' 512 bytes) and the workgroup has 8 waves, wave w converting K
+// [512 s + 64 w, +64) of every tile.  SW: tile t holds gate rows of pairs
+// 8t..8t+7 in lanes 0..7 and their up rows in lanes 8..15.  Codes: slot s
+// (tile s / 16, lane row s % 16) at 512 s, chunk c at c ^ (s & 15); x: row m
+// (1 KiB: 512 values) chunk c at c ^ 2m.  Per wave and stage: NT code DMAs
+// and one activation DMA; the wait at stage j leaves codes(j + 1) and
+// x(j + 1) in flight: vmcnt(NT + 1).
+constexpr int kWideWaves = 8;
+constexpr int kWideKS = 512;                                  // K bytes of a row per stage
+constexpr int kWideMaxK = 5120;
+constexpr int kWideXSlot = (kRowMaxM + 1) * 1024;             // x rows 0..M-1 and the zero row
+constexpr int kWideTable = 80 * (kWideMaxK / 128) * 4;        // 80 rows x 40 blocks
+constexpr int kWideTableHalf = kWideTable / 2;                // SW: the up rows' scales
+template <int NT>
+constexpr int wide_stage() { return 16 * NT * kWideKS; }
+template <int NT>
+constexpr int wide_ox() { return kRowD * wide_stage<NT>(); }
+template <int NT>
+constexpr int wide_otab() { return wide_ox<NT>() + kRowD * kWideXSlot; }
+template <int NT>
+constexpr int wide_lds() { return wide_otab<NT>() + kWideTable; }
+static_assert(wide_lds<5>() <= kMaxLds, "wide row-staged LDS");
+
+// Requirements (checked by the host): 1 <= M <= 8, K % 128 == 0,
+// K <= 512 NS <= 5120, at most 16 NT rows (8 NT pairs) per workgroup,
+// N * K < 2^31.
+template <int NS, bool SW, int NT>
+__global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const uint16_t* __restrict__ x,
+                                                                           const uint8_t* __restrict__ codes,
+                                                                           const float* __restrict__ scales,
+                                                                           uint16_t* __restrict__ y, int64_t ldy,
+                                                                           int M, int N, int K) {
+    constexpr int W = kWideWaves, D = kRowD, STAGE = wide_stage<NT>(), OX = wide_ox<NT>(), OTAB = wide_otab<NT>();
+    static_assert(W * NT * 256 * 4 <= D * STAGE, "partial sums fit in the code ring");
+    static_assert(NS * kWideKS <= kWideMaxK + kWideKS - 1, "the scale table holds 40 blocks per row");
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
+    const int S = K >> 7;
+    const int nst = (K + kWideKS - 1) / kWideKS;
+    const int half = N >> 1;
+    const int units = SW ? half : N;
+    const int u0 = (int)((int64_t)blockIdx.x * units / gridDim.x);
+    const int R = (int)((int64_t)(blockIdx.x + 1) * units / gridDim.x) - u0;  // rows, or pairs
+
+    for (int e = threadIdx.x; e < D * 64; e += 64 * W)
+        *reinterpret_cast<u32x4*>(lds + OX + (e >> 6) * kWideXSlot + M * 1024 + (e & 63) * 16) = u32x4{0, 0, 0, 0};
+    __syncthreads();
+
+    i32x4 dq[2], sq[2];
+    if constexpr (SW) {
+        dq[0] = make_desc(codes + (R ? (int64_t)u0 * K : 0), (uint32_t)(R * K));
+        dq[1] = make_desc(codes + (R ? (int64_t)(half + u0) * K : 0), (uint32_t)(R * K));
+        sq[0] = make_desc(scales + (R ? (int64_t)u0 * S : 0), (uint32_t)(R * S * 4));
+        sq[1] = make_desc(scales + (R ? (int64_t)(half + u0) * S : 0), (uint32_t)(R * S * 4));
+    } else {
+        dq[0] = dq[1] = make_desc(codes + (R ? (int64_t)u0 * K : 0), (uint32_t)(R * K));
+        sq[0] = sq[1] = make_desc(scales + (R ? (int64_t)u0 * S : 0), (uint32_t)(R * S * 4));
+    }
+    const i32x4 dx = make_desc(x, (uint32_t)(M * K * 2));
+
+    // Code DMA q of a stage: instruction i = wave + 8 q fills slots 2i, 2i + 1
+    // (lanes 0..31, 32..63); lane l fetches chunk (l & 31) ^ (slot & 15) of
+    // its slot's row, local row lr of descriptor part (SW: slot lane rows
+    // 0..7 gate, 8..15 up).
+    uint32_t cvoff[NT];
+    int cch[NT];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+        const int slot = 2 * (wave + W * q) + (lane >> 5);
+        const int t = slot >> 4, n = slot & 15;
+        const int lr = SW ? 8 * t + (n & 7) : slot;
+        cch[q] = (lane & 31) ^ n;
+        cvoff[q] = lr < R ? (uint32_t)(lr * K + 16 * cch[q]) : kBufferOob;
+    }
+    auto issue_codes = [&](int s) __attribute__((always_inline)) {
+        const uint32_t base = lds0 + (uint32_t)((s % D) * STAGE);
+#pragma unroll
+        for (int q = 0; q < NT; ++q) {
+            const int ins = wave + W * q;
+            const int part = SW ? ((2 * ins) & 15) >> 3 : 0;  // both slots of an instruction are gate or up
+            const bool ok = s < nst && kWideKS * s + 16 * cch[q] < K && cvoff[q] != kBufferOob;
+            dma16(__builtin_amdgcn_readfirstlane(base + (uint32_t)(ins * 1024)),
+                  ok ? cvoff[q] + (uint32_t)(kWideKS * s) : kBufferOob, dq[part], 0);
+        }
+    };
+    // Activation DMA of a stage: wave w < M fills row w (chunk l ^ 2w at
+    // position l); the other waves land zeros in the zero row.
+    const int xm = wave;
+    const int xch = lane ^ (2 * xm);
+    auto issue_x = [&](int s) __attribute__((always_inline)) {
+        const int k = kWideKS * s + 8 * xch;
+        const bool ok = xm < M && k < K;
+        const uint32_t dst = lds0 + (uint32_t)(OX + (s % D) * kWideXSlot + (xm < M ? xm : M) * 1024);
+        dma16(__builtin_amdgcn_readfirstlane(dst), ok ? (uint32_t)((xm * K + k) * 2) : kBufferOob, dx, 0);
+    };
+
+    // Scale table (dword DMAs, 256 bytes each): plain, the rows' R x S floats
+    // over the 8 waves; SW, the gate rows' (waves 0..3) and, from
+    // kWideTableHalf, the up rows' (waves 4..7).
+    {
+        const int part = SW ? wave >> 2 : 0;
+        const int c = SW ? wave & 3 : wave, cs = SW ? 4 : 8;
+        const int nt = (SW ? kWideTableHalf : kWideTable) / 256;
+        const uint32_t bytes = (uint32_t)(R * S * 4);
+        for (int idx = c; idx < nt; idx += cs) {
+            const uint32_t at = (uint32_t)(256 * idx);
+            if (at >= bytes) break;
+            const uint32_t off = at + 4u * (uint32_t)lane;
+            dma4(__builtin_amdgcn_readfirstlane(lds0 + OTAB + (uint32_t)(part * kWideTableHalf) + at),
+                 off < bytes ? off : kBufferOob, sq[part]);
+        }
+    }
+    auto sidx = [&](int slot) __attribute__((always_inline)) -> int {
+        if constexpr (SW) {
+            const int t = slot >> 4, n = slot & 15;
+            return (n < 8 ? 0 : kWideTableHalf / 4) + (8 * t + (n & 7)) * S;
+        }
+        return slot * S;
+    };
+
+    issue_codes(0);
+    issue_x(0);
+    issue_codes(1);
+    issue_x(1);
+
+    const int row = lane & 15, g = lane >> 4;
+    const int xr = row < M ? row : M;
+    const uint32_t xoff = (uint32_t)(OX + xr * 1024 + 16 * ((8 * wave + 2 * g) ^ (2 * (xr & 7))));
+    const uint32_t coff = (uint32_t)(row * kWideKS + 16 * ((4 * wave + g) ^ row));
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const float* tab = reinterpret_cast<const float*>(lds + OTAB);
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+        wait_vm<NT + 1>();
+        gemm_fp8::wait_lgkm<0>();  // stage j - 1's LDS reads are in registers
+        barrier();
+        issue_codes(j + 2);
+        issue_x(j + 2);
+        if (j < nst && kWideKS * j + 64 * wave < K) {
+            const u32x4 x0 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * kWideXSlot);
+            const u32x4 x1 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * kWideXSlot + 16);
+            const int blk = 4 * j + (wave >> 1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const u32x4 cw =
+                    *reinterpret_cast<const u32x4*>(lds + (j % D) * STAGE + t * 16 * kWideKS + coff);
+                const float sc = tab[sidx(16 * t + row) + blk];
+                uint32_t wv[8];
+                dequant4(cw.x, sc, wv[0], wv[1]);
+                dequant4(cw.y, sc, wv[2], wv[3]);
+                dequant4(cw.z, sc, wv[4], wv[5]);
+                dequant4(cw.w, sc, wv[6], wv[7]);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x0),
+                                                                 as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc[t], 0,
+                                                                 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1),
+                                                                 as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc[t], 0,
+                                                                 0, 0);
+            }
+        }
+    }
+    wait_vm<0>();
+    __syncthreads();
+
+    // acc[t][i] = C[m = 4 g + i][slot 16 t + row]; partials in wave order
+    float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[(wave * NT + t) * 256 + (4 * g + i) * 16 + row] = acc[t][i];
+    __syncthreads();
+    auto total = [&](int t, int e) __attribute__((always_inline)) -> float {
+        float v = red[t * 256 + e];
+#pragma unroll
+        for (int w = 1; w < W; ++w) v = v + red[(w * NT + t) * 256 + e];
+        return v;
+    };
+    for (int q = threadIdx.x; q < NT * 256; q += 64 * W) {
+        const int t = q >> 8, e = q & 255, m = e >> 4, n = e & 15;
+        if (m >= M) continue;
+        if constexpr (SW) {
+            if (n < 8 && 8 * t + n < R)
+                y[(int64_t)m * ldy + u0 + 8 * t + n] =
+                    swiglu_bf16_bits(f32_to_bf16_bits(total(t, e)), f32_to_bf16_bits(total(t, e + 8)));
+        } else {
+            if (16 * t + n < R) y[(int64_t)m * ldy + u0 + 16 * t + n] = f32_to_bf16_bits(total(t, e));
+        }
+    }
+}
+
+template <int NS, bool SW, int NT>
+hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                           int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
+    auto kern = small_m_row_wide_kernel<NS, SW, NT>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, wide_lds<NT>());
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kWideWaves), wide_lds<NT>(), stream, x, codes, scales, y, ldy,
+                       M, N, K);
+    return hipGetLastError();
+}
+
+// Tiles of the wide row-staged form where it runs for this geometry (0: it
+// does not); groups in `groups`.  Measured on MI355X against the row-range
+// kernel (graph replay over 1 GiB of rotated codes, M = 4 / 8): faster at
+// K = 5120 for every row count (17408 rows 19.6 / 19.7 us against 20.2 /
+// 20.7, 12288 rows 14.1 / 14.2 against 15.8 / 16.3, 8240 rows 10.9 / 11.2
+// against 13.1 / 13.8) and at K = 4096 up to 40 rows per CU (8240 rows 10.5
+// / 10.7 against 11.1 / 11.6), slower at K = 4096 from 48 rows per CU
+// (17408 rows 19.1 / 19.2 against 17.0 / 17.6, 12288 rows 13.8 / 13.9
+// against 13.2 / 13.6), so those stay on the row-range kernel.  The choice
+// depends on the weight geometry only, the same for the plain and the
+// SwiGLU form.
+int row_wide_tiles(int M, int N, int K, bool swiglu, int& groups) {
+    const int cus = compute_units();
+    const int units = swiglu ? N / 2 : N;
+    if (M < 1 || M > kRowMaxM || K % 128 != 0 || K > kWideMaxK || units < 1 || (int64_t)N * K >= ((int64_t)1 << 31))
+        return 0;
+    const int rows_per_cu = (N + cus - 1) / cus;
+    if (K <= 4096 && stream_nb(K) != 0 && rows_per_cu > 40) return 0;
+    groups = std::min(cus, units);
+    const int per = (units + groups - 1) / groups;
+    const int t = swiglu ? (per + 7) / 8 : (per + 15) / 16;
+    return t >= 3 && t <= 5 ? t : 0;
+}
+
 // Workgroups of the row-staged form for this geometry (0: not served).
 int row_groups(int M, int N, int K, bool swiglu) {
     const int cus = compute_units();
@@ -941,7 +1177,8 @@ int row_groups(int M, int N, int K, bool swiglu) {
 
 }  // namespace
 
-// At M <= 8 and up to 32 rows per CU (K <= 9216) the row-staged form runs.
+// At M <= 8 and up to 32 rows per CU (K <= 9216) the row-staged form runs
+// (33..80 rows: its wide form, see row_wide_tiles).
 // Measured on MI355X (graph replay over 1 GiB of rotated codes; down
 // 5120 x 8704, QKV-gate 7168 x 5120, the reference benchmark's 5120 x 5120
 // at M = 8): 12.4 / 10.7 / 9.2 us against 13.5-13.7 / 10.8 / 9.6 for the
@@ -1019,9 +1256,31 @@ hipError_t dispatch_stream(int nb, const uint16_t* x, const uint8_t* codes, cons
 
 
 bool small_m_candidates_supported(int M, int N, int K) {
-    int nb = 0, per = 0;
+    int nb = 0, per = 0, groups = 0;
+    // only where fp8lin_linear runs the row-range kernel (its candidates
+    // are that kernel's sums)
+    if (row_wide_tiles(M, N, K, false, groups)) return false;
     return stream_form(M, N, K, nb, per);
 }
+
+namespace {
+
+template <bool SW, int NT>
+hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                             int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
+    if (K <= 4096) return launch_row_wide<8, SW, NT>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    return launch_row_wide<10, SW, NT>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+}
+
+template <bool SW>
+hipError_t dispatch_row_wide(int nt, const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                             int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
+    if (nt == 3) return dispatch_row_wide<SW, 3>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    if (nt == 4) return dispatch_row_wide<SW, 4>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    return dispatch_row_wide<SW, 5>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+}
+
+}  // namespace
 
 hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
                                      int K, uint32_t* part, int64_t& groups, hipStream_t stream) {
@@ -1037,7 +1296,11 @@ hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, co
 hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                           int64_t ldy, int M, int N, int K, int /*split*/, bool swiglu, hipStream_t stream) {
     const int cus = compute_units();
-    int nb = 0, per_rows = 0;
+    int nb = 0, per_rows = 0, wide_groups = 0;
+    if (const int nt = row_wide_tiles(M, N, K, swiglu, wide_groups)) {
+        if (swiglu) return dispatch_row_wide<true>(nt, x, codes, scales, y, ldy, M, N, K, wide_groups, stream);
+        return dispatch_row_wide<false>(nt, x, codes, scales, y, ldy, M, N, K, wide_groups, stream);
+    }
     if (stream_form(M, N, K, nb, per_rows)) {
         if (swiglu)
             return dispatch_stream<true, false>(nb, x, codes, scales, y, ldy, M, N, K, (N / 2 + cus - 1) / cus,

@@ -174,16 +174,16 @@ def test_tensor_small_vs_fp64(fp8lin, gpu, oracle, m, k, n):
 
 @pytest.mark.parametrize("n,k,m", [(8192, 4096, 2), (8200, 3584, 8), (9000, 8704, 5), (8240, 5120, 3),
                                    (12000, 4224, 7), (8192, 5120, 8), (5120, 8704, 8), (7168, 5120, 4),
-                                   (4100, 4096, 3), (4352, 5120, 2)])
+                                   (4100, 4096, 3), (4352, 5120, 2), (12288, 4096, 8), (31040, 4096, 4),
+                                   (24000, 5120, 6)])
 def test_tensor_small_wide(fp8lin, gpu, oracle, n, k, m):
-    """Weights of 32 or more rows per compute unit take the persistent
-    row-range kernel: ranges of ceil(N / CUs) rows walked in pieces of at
-    most 16 rows, as equal as the range allows (33 rows: 11 + 11 + 11; 36:
-    12 x 3; 47: 16 + 16 + 15; 32: 16 + 16), each K band (4096, 5120, 9216)
-    and a K with one block in the last step (4224); the decode down and
-    QKV-gate shapes and two of 17 rows per CU run the row-staged form (one
-    workgroup of up to 32 rows per CU, M <= 8).  Every row against the FP64
-    oracle; split 1 and 4 bit-equal."""
+    """The small-M kernels by rows per compute unit at M <= 8: up to 32 rows
+    the row-staged form (the decode down and QKV-gate shapes, 17 and 32 rows
+    per CU); 33..80 rows at K <= 5120 the wide row-staged form (33, 36 and
+    47 rows; K = 3584, 4224 and 5120), except from 48 rows at K = 4096 and
+    from 81 rows, which take the persistent row-range kernel (48, 122 and 94
+    rows per CU), as do K > 5120 from 33 rows (9000 x 8704: 36 rows in pieces
+    of 12).  Every row against the FP64 oracle; split 1 and 4 bit-equal."""
     rng = np.random.default_rng(n + k + m)
     codes = rng.integers(0, 256, (n, k), dtype=np.uint8)
     codes[(codes == 127) | (codes == 255)] = 0
@@ -705,8 +705,8 @@ def test_linear_small_m_rows(fp8lin, gpu, oracle, m, n, k):
     1024 weight rows runs the small-M matrix-core kernel: the row-staged
     form (n = 2056, 2064, 1040: 8 or 9 rows per workgroup, 4 or 5 SwiGLU
     pairs, both tiles ragged; K tails of 384, 5248 and 8704 within the last
-    1024-wide stage) or the persistent row-range form (n = 8208: 32 rows per
-    CU and more, 17 pairs per range in pieces of 6).  Every output
+    1024-wide stage) or its wide form (n = 8208: 33 rows per CU in three
+    tiles, 17 SwiGLU pairs).  Every output
     against the FP64 oracle; fp8_tensor_small bit-equal (the same kernel);
     the fused SwiGLU bit-equal to fused_swiglu(fp8_linear); an unaligned
     view of x runs the multi-row GEMV, at the bar."""
@@ -759,6 +759,38 @@ def test_small_m_row_staged_limits(fp8lin, gpu, oracle, m, n, k):
     fused = fp8lin.linear_swiglu(xg, c, s, split=False)
     assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
     assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 17408, 5120), (7, 20480, 5120), (5, 8240, 4096), (3, 12000, 4224),
+                                   (2, 9000, 2048), (4, 12288, 4096)])
+def test_small_m_row_wide(fp8lin, gpu, oracle, m, n, k):
+    """The wide row-staged small-M form (33..80 rows per CU, 512-byte
+    stages, up to 5 tiles): 68 rows (34 SwiGLU pairs) per workgroup at the
+    gate/up shape, the 80-row maximum, 33 rows at K = 4096, a last stage of
+    128 values (K = 4224), K outside the row-range kernel's bands (2048), and
+    48 rows at K = 4096, which stays on the row-range kernel.  Every output of
+    fp8_tensor_small against the FP64 oracle, split 1 and 4 bit-equal;
+    fp8_linear the same bits where it takes the small-M path; the fused
+    SwiGLU bit-equal to fused_swiglu(fp8_linear); the head candidates of
+    one call equal to those of the stored logits."""
+    rng = np.random.default_rng(m * 104729 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    yt = fp8lin.fp8_tensor_small(xg, c, s, 1)
+    assert_parity(bits(yt), ref, f"row-wide {m}x{n}x{k}")
+    assert torch.equal(fp8lin.fp8_tensor_small(xg, c, s, 4), yt)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"fp8_linear {m}x{n}x{k}")
+    if m > 2 or k > 5120:
+        assert torch.equal(y, yt)
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+    want = fp8lin.vocabulary_candidates(y, 0)
+    assert torch.equal(fp8lin.linear_candidates(xg, c, s, 0), want)
 
 
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
