@@ -821,8 +821,9 @@ __global__ __launch_bounds__(64 * kRowWaves) void small_m_row_kernel(const uint1
 
     // Scale table: plain, the rows' R x S floats (waves 0..11, 768 bytes
     // each); SW, the gate rows' and, from kRowTableHalf, the up rows' (waves
-    // 0..5 and 8..13).  Dword DMAs: the buffer range check would zero a
-    // 16-byte load that crosses the end of the rows' scales.
+    // 0..5 and 8..13).  Dword DMAs, so that no lane's load straddles the end
+    // of the rows' scales (what a partly out-of-range 16-byte load returns
+    // is left to the buffer range check).
     {
         const int part = SW ? wave >> 3 : 0;
         const int c = SW ? wave & 7 : wave;
