@@ -10,14 +10,15 @@
 // has drained.  Here the links share one grid:
 //
 //  - the grid holds every link's workgroups in link order; a workgroup is
-//    the decode GEMV's (gemv_kernel.hpp, ring form): 4 waves, each owning one
-//    item of 2 weight rows (a gate/up pair with SwiGLU) of up to 5 K steps of
-//    1024 codes, or 1 row of up to 9 steps, with every code and scale load
-//    of the item issued at once;
+//    4 waves, each owning two items of the decode GEMV's ring form
+//    (gemv_kernel.hpp): an item is 2 weight rows (a gate/up pair with
+//    SwiGLU) of up to 5 K steps of 1024 codes, or 1 row of up to 9 steps;
 //  - workgroups are dispatched in grid order on each XCD, so the first
 //    workgroups of link L + 1 start while link L drains: they issue their
-//    code loads -- which never depend on the activations -- and only then
-//    wait for the link whose output they read.  Waiting workgroups hold
+//    first item's code loads -- which never depend on the activations --
+//    then wait for the link whose output they read, then load the
+//    activations and the second item's codes, so HBM has the second items'
+//    bytes to stream while the first items are summed.  Waiting workgroups hold
 //    slots that link L no longer needs (all of its workgroups on that XCD
 //    were dispatched before them), so the waits always end;
 //  - a link that reads an earlier link's output waits for that link: each
@@ -57,13 +58,16 @@
 //    the count), so the grid always drains.
 //
 // Measured (graph replay, weights rotated over 600 MB): links with no waits
-// stream at 6.8 TB/s in one launch (QKV-gate + gate/up + down + head,
-// 85 us against 93 us as four GEMV launches), but each wait costs about
-// 10 us: the producer's last adds reach the pollers 2-3 us after its last
-// stores, and the waiting workgroups that hold the compute units then fetch
-// x and compute while no weight loads are in flight.  The same four links
-// each after the previous take 125 us; a graph of four GEMV launches
-// remains the faster strict chain.
+// stream at 6.7 TB/s in one launch (QKV-gate + gate/up + down + head,
+// 86 us against 93 us as four GEMV launches), but each wait costs about
+// 8 us: the producer's last adds reach the pollers 2-3 us after its last
+// stores, its last workgroups start late (when earlier ones free their
+// slots) and finish last, and the waiting workgroups' activations land only
+// after the code loads queued before them.  The same four links each after
+// the previous take 110 us (124 us with one item per wave, when the
+// workgroups that held the compute units at the wake left HBM idle until
+// they finished); a graph of four GEMV launches remains the faster strict
+// chain.
 //
 // Numerics: each row is summed exactly as the decode GEMV's one-row ring
 // kernel sums it (lane l takes the 16-code chunks l + 64 j in step order,
@@ -79,7 +83,8 @@
 namespace fp8lin {
 namespace {
 
-constexpr int kWPG = 4;          // waves per workgroup, one item each
+constexpr int kWPG = 4;          // waves per workgroup
+constexpr int kItems = 2;        // items per wave: item it of wave w of workgroup b is g = (b kItems + it) kWPG + w
 constexpr int kMaxSteps = 9;     // K <= 9216
 constexpr int kXDmas = kMaxSteps * 2;   // 1 KiB direct-to-LDS loads of a link's activations
 constexpr int kXBytes = kXDmas * 1024;  // a workgroup's activations in LDS
@@ -156,74 +161,92 @@ __device__ __forceinline__ int xcc_id() {
     return (int)(v & (kXcds - 1));
 }
 
-// One wave's item of link k: R rows (slot_row of the ring kernel) x up to NS
-// steps.  Loads every chunk up front.  A link that waits: the chunks first,
-// then `wait` (the dependency, all 4 waves together), then `x_dma` (the
-// activations into LDS `xs`) and every load landed; otherwise, as the ring
-// kernel orders them, `x_dma` first and the wait only for the activations.
-// Then sums each row in the ring kernel's order with the activations from
-// LDS (step s at xs + 2048 s: lane l's 16 BF16 of chunk l + 64 s at +16 l
-// and +1024 + 16 l) and stores its rows.
+// One wave's kItems items of link k (item it: g + kWPG it), each R rows
+// (slot_row of the ring kernel) x up to NS steps.  A link that waits: the
+// first item's chunks, then `wait` (the dependency, all 4 waves together),
+// then `x_dma` (the activations into LDS `xs`), then the other items'
+// chunks, and the activations and first item landed before the sums start;
+// otherwise, as the ring kernel orders them, `x_dma` first, every item's
+// chunks, and the wait only for the activations.  Then sums each item's rows
+// in the ring kernel's order with the activations from LDS (step s at
+// xs + 2048 s: lane l's 16 BF16 of chunk l + 64 s at +16 l and +1024 + 16 l)
+// and stores them.
 template <int R, int NS, bool SWIGLU, class Wait, class XDma>
 __device__ __forceinline__ void run_item(const LinkDev& k, int64_t g, int lane, const uint8_t* xs, Wait&& wait,
                                          XDma&& x_dma) {
     using gemv::Chunk;
     const gemv::Buffers b = gemv::make_buffers(k.x, k.codes, k.scales, k.S, 1, k.N, k.K, true);
-    int64_t rows[R];
-    bool ok[R];
+    int64_t rows[kItems][R];
+    bool ok[kItems][R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) rows[r] = gemv::slot_row<R, SWIGLU>(g, r, k.N, ok[r]);
+    for (int it = 0; it < kItems; ++it)
+#pragma unroll
+        for (int r = 0; r < R; ++r) rows[it][r] = gemv::slot_row<R, SWIGLU>(g + kWPG * it, r, k.N, ok[it][r]);
     const int chunks = k.K >> 4;
     const int steps = (chunks + kWave - 1) / kWave;
     const bool dep = k.after >= 0;
-    if (!dep) x_dma();
-    Chunk<true> ring[NS][R];
+    Chunk<true> ring[kItems][NS][R];
+    auto load_item = [&](int it) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        const int c = lane + j * kWave;
+        for (int j = 0; j < NS; ++j) {
+            const int c = lane + j * kWave;
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            gemv::load_chunk_buf<true, 2>(ring[j][r], b, k.S, rows[r], k.K, c << 4, ok[r] && c < chunks);
-    }
+            for (int r = 0; r < R; ++r)
+                gemv::load_chunk_buf<true, 2>(ring[it][j][r], b, k.S, rows[it][r], k.K, c << 4,
+                                              ok[it][r] && c < chunks);
+        }
+    };
     if (dep) {
+        // the first item's codes, the wait, the activations, the other items'
+        // codes; then the activations and everything older
+        load_item(0);
         wait();
         x_dma();
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int it = 1; it < kItems; ++it) load_item(it);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * R * NS * (kItems - 1)) : "memory");
     } else {
-        // the activation DMAs are older than the 2 R NS chunk loads
-        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * R * NS) : "memory");
+        // the activation DMAs are older than the 2 R NS chunk loads per item
+        x_dma();
+#pragma unroll
+        for (int it = 0; it < kItems; ++it) load_item(it);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"i"(2 * R * NS * kItems) : "memory");
     }
     wg_barrier();
-    float acc[R][1];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r][0] = 0.0f;
+    for (int it = 0; it < kItems; ++it) {
+        float acc[R][1];
 #pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        // each step's LDS reads stay in its step
+        for (int r = 0; r < R; ++r) acc[r][0] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) asm volatile("" : "+v"(acc[r][0])::"memory");
-        const u32x4 lo = *reinterpret_cast<const u32x4*>(xs + 2048 * j + 16 * lane);
-        const u32x4 hi = *reinterpret_cast<const u32x4*>(xs + 2048 * j + 1024 + 16 * lane);
-        const uint32_t xv[1][8] = {{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w}};
-        float nxt[R][1];
+        for (int j = 0; j < NS; ++j) {
+            // each step's LDS reads stay in its step
 #pragma unroll
-        for (int r = 0; r < R; ++r) nxt[r][0] = acc[r][0];
-        gemv::accumulate<R, 1, true>(nxt, ring[j], xv);
-        const bool live = j < steps;
+            for (int r = 0; r < R; ++r) asm volatile("" : "+v"(acc[r][0])::"memory");
+            const u32x4 lo = *reinterpret_cast<const u32x4*>(xs + 2048 * j + 16 * lane);
+            const u32x4 hi = *reinterpret_cast<const u32x4*>(xs + 2048 * j + 1024 + 16 * lane);
+            const uint32_t xv[1][8] = {{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w}};
+            float nxt[R][1];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r][0] = live ? nxt[r][0] : acc[r][0];
-    }
+            for (int r = 0; r < R; ++r) nxt[r][0] = acc[r][0];
+            gemv::accumulate<R, 1, true>(nxt, ring[it][j], xv);
+            const bool live = j < steps;
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r][0] = wave_sum(acc[r][0]);
-    if (lane != 0) return;
-    if constexpr (SWIGLU) {
-        if (ok[0])
-            store_out(k.y + rows[0], swiglu_bf16_bits(f32_to_bf16_bits(acc[0][0]), f32_to_bf16_bits(acc[1][0])),
-                      k.publish);
-    } else {
+            for (int r = 0; r < R; ++r) acc[r][0] = live ? nxt[r][0] : acc[r][0];
+        }
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (ok[r]) store_out(k.y + rows[r], f32_to_bf16_bits(acc[r][0]), k.publish);
+        for (int r = 0; r < R; ++r) acc[r][0] = wave_sum(acc[r][0]);
+        if (lane == 0) {
+            if constexpr (SWIGLU) {
+                if (ok[it][0])
+                    store_out(k.y + rows[it][0],
+                              swiglu_bf16_bits(f32_to_bf16_bits(acc[0][0]), f32_to_bf16_bits(acc[1][0])), k.publish);
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (ok[it][r]) store_out(k.y + rows[it][r], f32_to_bf16_bits(acc[r][0]), k.publish);
+            }
+        }
     }
 }
 
@@ -235,7 +258,7 @@ __global__ __launch_bounds__(64 * kWPG) void chain_kernel(ChainArgs a) {
     int L = 0;
     while (L + 1 < a.nlinks && b >= a.link[L + 1].wg0) ++L;
     const LinkDev& k = a.link[L];
-    const int64_t g = (int64_t)(b - k.wg0) * kWPG + wave;
+    const int64_t g = (int64_t)(b - k.wg0) * kWPG * kItems + wave;
     uint64_t* sync = a.sync;
     const int w = b - k.wg0, slot = w % kCountSlots;
     // the call index, from this workgroup's own slot (see header)
@@ -373,7 +396,7 @@ hipError_t launch_chain(const ChainLink* links, int nlinks, uint64_t* sync, hipS
         d.mode = (s.swiglu || s.K <= 5120) ? 0 : 1;
         d.groups = (int)(d.mode == 0 ? (s.swiglu ? s.N / 2 : (s.N + 1) / 2) : s.N);
         d.wg0 = wg;
-        d.wgs = (d.groups + kWPG - 1) / kWPG;
+        d.wgs = (d.groups + kWPG * kItems - 1) / (kWPG * kItems);
         d.publish = 0;
         if (s.after >= 0) a.link[s.after].publish = 1;
         wg += d.wgs;

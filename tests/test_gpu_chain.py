@@ -23,12 +23,12 @@ def bits(t):
 
 
 def link_workgroups(link):
-    """Workgroups of a chain link: 4 items each, an item 2 rows (a gate/up
-    pair with SwiGLU) for K <= 5120, else 1 row."""
+    """Workgroups of a chain link: 8 items each (4 waves of 2 items), an
+    item 2 rows (a gate/up pair with SwiGLU) for K <= 5120, else 1 row."""
     codes, swiglu = link[1], bool(link[3]) if len(link) > 3 else False
     n, k = codes.shape
     items = n // 2 if swiglu else ((n + 1) // 2 if k <= 5120 else n)
-    return -(-items // 4)
+    return -(-items // 8)
 
 
 def check_sync(ws, links, calls):
