@@ -64,10 +64,10 @@
 // stores, its last workgroups start late (when earlier ones free their
 // slots) and finish last, and the waiting workgroups' activations land only
 // after the code loads queued before them.  The same four links each after
-// the previous take 110 us (124 us with one item per wave, when the
+// the previous take 108 us (124 us with one item per wave, when the
 // workgroups that held the compute units at the wake left HBM idle until
-// they finished); a graph of four GEMV launches remains the faster strict
-// chain.
+// they finished; 110 us with polls 512 clocks apart instead of 256); a
+// graph of four GEMV launches remains the faster strict chain.
 //
 // Numerics: each row is summed exactly as the decode GEMV's one-row ring
 // kernel sums it (lane l takes the 16-code chunks l + 64 j in step order,
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * kWPG) void chain_kernel(ChainArgs a) {
                                                            __HIP_MEMORY_SCOPE_AGENT);
                                 break;
                             }
-                            __builtin_amdgcn_s_sleep(8);
+                            __builtin_amdgcn_s_sleep(4);
                             continue;
                         }
                         uint64_t part = 0;
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(64 * kWPG) void chain_kernel(ChainArgs a) {
                                 __hip_atomic_fetch_add(sync, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             break;
                         }
-                        __builtin_amdgcn_s_sleep(8);
+                        __builtin_amdgcn_s_sleep(4);
                     }
                     // record it for the call (the activations are then
                     // read with coherent loads: no L2 invalidate)
