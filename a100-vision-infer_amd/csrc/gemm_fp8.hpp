@@ -466,16 +466,15 @@ __device__ __forceinline__ void setup(Ctx<MT>& c, const Unit& w, const uint16_t*
         c.brd[cp] = lds0 + A_BYTES + wave * B_WAVE + l32 * 64 + 16 * ((2 * cp + h) ^ gb(l32));
 }
 
-// Prologue loads of a unit: A(0), A(1) into stages 0, 1; B(0..2) into slots
-// 0..2; scale blocks 0, 1.
+// Prologue loads of a unit, in the order the first step needs them: A(0)
+// into stage 0, B(0) and B(1) into slots 0 and 1, scale blocks 0 and 1, then
+// A(1) into stage 1 and B(2) into slot 2 (the last MT + 4 loads).
 template <int MT>
 __device__ __forceinline__ void issue_prologue(State<MT>& st, const Ctx<MT>& c) {
 #pragma unroll
     for (int ii = 0; ii < MT; ++ii) dma16(c.m0a + ii * 1024, c.aoff[ii], c.dx, 0);
 #pragma unroll
-    for (int ii = 0; ii < MT; ++ii) dma16(c.m0a + Geo<MT>::A_STAGE + ii * 1024, c.aoff[ii], c.dx, BK * 2);
-#pragma unroll
-    for (int p = 0; p < 3; ++p)
+    for (int p = 0; p < 2; ++p)
 #pragma unroll
         for (int gi = 0; gi < 4; ++gi) dma16(c.m0b + p * B_SLOT + gi * 1024, c.boff[gi], c.dw, p * BK);
 #pragma unroll
@@ -483,14 +482,23 @@ __device__ __forceinline__ void issue_prologue(State<MT>& st, const Ctx<MT>& c) 
         buf_load1(st.bsc[0][j], c.soff[j], c.ds, 0);
         buf_load1(st.bsc[1][j], c.soff[j], c.ds, c.scol);
     }
+#pragma unroll
+    for (int ii = 0; ii < MT; ++ii) dma16(c.m0a + Geo<MT>::A_STAGE + ii * 1024, c.aoff[ii], c.dx, BK * 2);
+#pragma unroll
+    for (int gi = 0; gi < 4; ++gi) dma16(c.m0b + 2 * B_SLOT + gi * 1024, c.boff[gi], c.dw, 2 * BK);
 }
 
-// The rest of the prologue once those loads (and anything else in flight)
-// have landed: B(0) dequantized, B(1) codes and step 0's first A fragments
-// read; the accumulators cleared.
+// The rest of the prologue once A(0), B(0), B(1) and the scales have landed
+// (at most the MT + 4 loads of A(1) and B(2), or later stores, still in
+// flight): B(0) dequantized, B(1) codes and step 0's first A fragments read;
+// the accumulators cleared.  Step 0 first touches A(1) and B(2) after its
+// mid-step wait, which leaves only that step's own loads in flight, so
+// those two need no wait here; the kernel starts its first step about 1 us
+// earlier than with everything waited for (M = 512: 4.3 against 5.5 us
+// from launch to the first MFMA).
 template <int MT>
 __device__ __forceinline__ void finish_prologue(State<MT>& st, const Ctx<MT>& c) {
-    wait_vm4<0>(st.bsc[0], st.bsc[1]);
+    wait_vm4<MT + 4>(st.bsc[0], st.bsc[1]);
     barrier();
 #pragma unroll
     for (int j = 0; j < NT; ++j)
