@@ -177,6 +177,35 @@ def test_gdn_in_proj_all(fp8lin, gpu, oracle, m):
         assert eng.cache_stats()["fp8_tensor_calls"] == 1
 
 
+def test_split_k_into_unaligned_column_slice(fp8lin, gpu, oracle):
+    """A K-split FP8 group (7168 rows at M=512: 56 tiles x 4 K ranges) written
+    into the column slice that starts 6 columns into a 7174-column output,
+    after a 6-row BF16 group: with a row stride of 7174 elements the tail
+    reduce stores every other row with 8-byte stores and the others with
+    2-byte stores.  The slice equals the same projection on its own (column
+    0, every row aligned) bit for bit, and both groups meet the parity bar."""
+    F, k, m = fp8lin, 5120, 512
+    codes, scales, c_np, s_np = weights(F, gpu, 7168, k, tag=31)
+    w = (F.gen_activations(6, k, seed=1, tag=32, device=gpu).float() * 0.02).to(torch.bfloat16).contiguous()
+    eng = F.LinearEngine()
+    eng.add("l.b.weight", w)
+    eng.add("l.q.weight", codes, scales)
+    eng.fuse_weights("l.mix", ["l.b", "l.q"])
+    assert eng.mixed_projections["l.mix"] == ["l.b", "l.q"]
+    alone = F.LinearEngine()
+    alone.add("q.weight", codes, scales)
+    x = F.gen_activations(m, k, seed=0, tag=33, device=gpu)
+    y = bits(eng.linear(x, "l.mix"))
+    assert y.shape == (m, 7174)
+    ya, path = alone.linear(x, "q", return_path=True)
+    assert path == F.PATH_FP8_GEMM
+    assert np.array_equal(y[:, 6:], bits(ya))
+    rows = np.array([0, 1, 2, 255, 256, 511])
+    xb = bits(x)[rows]
+    assert_parity(y[rows, 6:], oracle.linear(xb, c_np, s_np), "split slice")
+    assert_parity(y[rows, :6], oracle.linear_bf16w(xb, bits(w)), "bf16 group")
+
+
 @pytest.mark.parametrize("m,k", [(2, 256), (4, 5120), (8, 384)])
 def test_tensor_small_unaligned_views(fp8lin, gpu, oracle, m, k):
     """An unaligned contiguous view of x or of the codes (the reference's own
