@@ -133,6 +133,17 @@ __device__ __forceinline__ void dma16(uint32_t m0v, uint32_t voff, i32x4 desc, i
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  ::"s"(m0v), "v"(voff), "s"(desc), "s"(soff) : "memory", "m0");
 }
+// The same with the non-temporal policy, for weight codes that one launch
+// reads once (the decode and small-M streams).  Measured on MI355X: a DMA
+// stream in the small-M kernels' patterns moves 10-15% more bytes per second
+// from HBM with it (the 75968-row head 66 -> 57 us, 128-byte pieces; the
+// gate/up codes in 512-byte row pieces 17.1 -> 15.5 us), about the rate of
+// non-temporal register loads.  Data that several workgroups read (the
+// activations, the prefill GEMM's tiles) keeps the default policy.
+__device__ __forceinline__ void dma16_nt(uint32_t m0v, uint32_t voff, i32x4 desc, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 ::"s"(m0v), "v"(voff), "s"(desc), "s"(soff) : "memory", "m0");
+}
 __device__ __forceinline__ void buf_load1(float& d, uint32_t voff, i32x4 desc, int soff) {
     asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(d) : "v"(voff), "s"(desc), "s"(soff));
 }

@@ -57,6 +57,7 @@ namespace {
 
 using gemm_fp8::barrier;
 using gemm_fp8::dma16;
+using gemm_fp8::dma16_nt;
 using gemm_fp8::i32x4;
 using gemm_fp8::make_desc;
 using gemm_fp8::wait_vm;
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(64 * W) void small_m_kernel(const uint16_t* __restr
         const bool ok = blk < KB;
 #pragma unroll
         for (int q = 0; q < 2; ++q)
-            dma16(m0 + q * 1024, ok ? cvoff[q] + (uint32_t)blk * 128u : kBufferOob, dwq[q], 0);
+            dma16_nt(m0 + q * 1024, ok ? cvoff[q] + (uint32_t)blk * 128u : kBufferOob, dwq[q], 0);
     };
     auto dma_chunk = [&](int c) __attribute__((always_inline)) {
         const uint32_t xb = lds0 + o_x + (uint32_t)((c % C::XBUFS) * xbuf);
@@ -506,7 +507,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void small_m_stream_kernel(const
         for (int q = 0; q < 2; ++q) {
             bool rok;
             const int n = slot_row(base, crow[q], rok);
-            dma16(m0 + q * 1024, ok && rok ? (uint32_t)(n * K + blk * 128) + cvoff[q] : kBufferOob, dw, 0);
+            dma16_nt(m0 + q * 1024, ok && rok ? (uint32_t)(n * K + blk * 128) + cvoff[q] : kBufferOob, dw, 0);
         }
     };
     // scales of piece p into buffer p % 3 as [j][row]
@@ -803,8 +804,8 @@ __global__ __launch_bounds__(64 * kRowWaves) void small_m_row_kernel(const uint1
         const bool ok = s < nst && 1024 * s + 16 * cch < K;
 #pragma unroll
         for (int q = 0; q < 2; ++q)
-            dma16(__builtin_amdgcn_readfirstlane(base + (uint32_t)((wave + 16 * q) * 1024)),
-                  ok && cvoff[q] != kBufferOob ? cvoff[q] + 1024u * (uint32_t)s : kBufferOob, dq[q], 0);
+            dma16_nt(__builtin_amdgcn_readfirstlane(base + (uint32_t)((wave + 16 * q) * 1024)),
+                     ok && cvoff[q] != kBufferOob ? cvoff[q] + 1024u * (uint32_t)s : kBufferOob, dq[q], 0);
     };
     // Activation DMA of a stage: wave w < 2M fills row w / 2, positions
     // 64 (w % 2) + l, with chunk (64 (w % 2) + l) ^ 2 m (8 values each); the
@@ -1017,8 +1018,8 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
             const int ins = wave + W * q;
             const int part = SW ? ((2 * ins) & 15) >> 3 : 0;  // both slots of an instruction are gate or up
             const bool ok = s < nst && kWideKS * s + 16 * cch[q] < K && cvoff[q] != kBufferOob;
-            dma16(__builtin_amdgcn_readfirstlane(base + (uint32_t)(ins * 1024)),
-                  ok ? cvoff[q] + (uint32_t)(kWideKS * s) : kBufferOob, dq[part], 0);
+            dma16_nt(__builtin_amdgcn_readfirstlane(base + (uint32_t)(ins * 1024)),
+                     ok ? cvoff[q] + (uint32_t)(kWideKS * s) : kBufferOob, dq[part], 0);
         }
     };
     // Activation DMA of a stage: wave w < M fills row w (chunk l ^ 2w at
