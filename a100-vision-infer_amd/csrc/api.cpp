@@ -130,10 +130,16 @@ void check_scales(const float* scales, int64_t scale_cols, int64_t K) {
 // 8-row GEMV at the decode shapes).  It takes block scales [N, K/128],
 // K % 128 == 0, 16-byte aligned x and codes and 16 K < 2^31; weights of at
 // most 1024 rows keep the GEMV (four rows or fewer per CU), and so do two
-// rows at K <= 5120, where the two-row ring GEMV is faster.
+// rows at K <= 5120, where the two-row ring GEMV is as fast or faster
+// (gate/up 17.2 against 18.1 us) except on weights that the kernel's
+// row-range form serves (the output heads: 61.8 against 66.6 us at 75968 x
+// 5120, 96.0 against 109.2 at 124160 x 5120, 23.5 against 24.6 at 31040 x
+// 4096; measured on MI355X with random weights).
 bool linear_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t M, int64_t N, int64_t K) {
-    return M >= 2 && M <= 8 && (M > 2 || K > 5120) && N > 1024 && K % 128 == 0 && S == K / 128 &&
-           aligned16(x) && aligned16(codes) && 16 * K < kMaxDim && N * S * 4 < kMaxDim;
+    if (!(M >= 2 && M <= 8 && N > 1024 && K % 128 == 0 && S == K / 128 && aligned16(x) && aligned16(codes) &&
+          16 * K < kMaxDim && N * S * 4 < kMaxDim))
+        return false;
+    return M > 2 || K > 5120 || fp8lin::small_m_candidates_supported(2, (int)N, (int)K);
 }
 
 // K-split partials of fp8_linear's prefill GEMM (M > 8) for output row stride
@@ -436,8 +442,8 @@ size_t linear_candidates_ws(int64_t M, int64_t N) {
 }
 
 // Whether fp8lin_linear runs the small-M matrix-core kernel for this call
-// (3..8 rows, or 2 at K > 5120, through linear_small_m; 9..32 rows through
-// the GEMM dispatch's mid-rows rule).
+// (3..8 rows, or 2 at K > 5120 or on a weight of its row-range form, through
+// linear_small_m; 9..32 rows through the GEMM dispatch's mid-rows rule).
 bool linear_runs_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t M, int64_t N, int64_t K) {
     return linear_small_m(x, codes, S, M, N, K) || fp8lin::gemm_mid_rows(x, codes, (int)S, M, N, K);
 }
@@ -445,7 +451,8 @@ bool linear_runs_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int
 void linear_candidates_impl(const uint16_t* x, const uint8_t* codes, const float* scales, int64_t S, int64_t M,
                             int64_t N, int64_t K, int64_t offset, void* ws, double* out, hipStream_t stream) {
     const bool wide = K % 16 == 0 && aligned16(x) && aligned16(codes);
-    if (M <= 8 && fp8lin::gemv_candidates_supported((int)M, (int)N, (int)K, wide)) {
+    if (M <= 8 && !linear_runs_small_m(x, codes, S, M, N, K) &&
+        fp8lin::gemv_candidates_supported((int)M, (int)N, (int)K, wide)) {
         check_hip(fp8lin::launch_gemv_candidates(x, codes, scales, (int)S, (int)M, (int)N, (int)K, offset, ws, out,
                                                  stream),
                   "fp8 gemv candidates launch");
