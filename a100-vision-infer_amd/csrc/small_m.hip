@@ -45,7 +45,13 @@
 // of one row per DMA instruction, with the activations staged beside the
 // codes (see that kernel); 33..80 rows per compute unit at K <= 5120 run its
 // wide form, small_m_row_wide_kernel (512 bytes of each row per stage, up to
-// 5 tiles), where measured faster than the row-range kernel.
+// 5 tiles), where measured faster than the row-range kernel.  At 9..16 rows
+// the wide form stages 16 activation rows and serves up to 64 rows per
+// compute unit at K <= 5120 and up to 32 at K <= 9216.
+//
+// Every kernel here DMAs the weight codes, which one launch reads once, with
+// the non-temporal cache policy (dma16_nt): 10-15% more bytes per second
+// from HBM than the default policy in these patterns.
 #include <algorithm>
 #include <utility>
 
@@ -945,31 +951,35 @@ hipError_t launch_row(const uint16_t* x, const uint8_t* codes, const float* scal
 constexpr int kWideWaves = 8;
 constexpr int kWideKS = 512;                                  // K bytes of a row per stage
 constexpr int kWideMaxK = 5120;
-constexpr int kWideXSlot = (kRowMaxM + 1) * 1024;             // x rows 0..M-1 and the zero row
+template <int MX>
+constexpr int wide_xslot() { return (MX + 1) * 1024; }         // x rows 0..M-1 and the zero row
 constexpr int kWideTable = 80 * (kWideMaxK / 128) * 4;        // 80 rows x 40 blocks
 constexpr int kWideTableHalf = kWideTable / 2;                // SW: the up rows' scales
 template <int NT>
 constexpr int wide_stage() { return 16 * NT * kWideKS; }
 template <int NT>
 constexpr int wide_ox() { return kRowD * wide_stage<NT>(); }
-template <int NT>
-constexpr int wide_otab() { return wide_ox<NT>() + kRowD * kWideXSlot; }
-template <int NT>
-constexpr int wide_lds() { return wide_otab<NT>() + kWideTable; }
-static_assert(wide_lds<5>() <= kMaxLds, "wide row-staged LDS");
+template <int NT, int MX>
+constexpr int wide_otab() { return wide_ox<NT>() + kRowD * wide_xslot<MX>(); }
+template <int NT, int MX>
+constexpr int wide_lds() { return wide_otab<NT, MX>() + kWideTable; }
+static_assert(wide_lds<5, 8>() <= kMaxLds && wide_lds<4, 16>() <= kMaxLds, "wide row-staged LDS");
 
-// Requirements (checked by the host): 1 <= M <= 8, K % 128 == 0,
-// K <= 512 NS <= 5120, at most 16 NT rows (8 NT pairs) per workgroup,
-// N * K < 2^31.
-template <int NS, bool SW, int NT>
+// Requirements (checked by the host): 1 <= M <= MX (8, or 16 with NT <= 4),
+// K % 128 == 0, K <= 512 NS <= 5120, at most 16 NT rows (8 NT pairs) per
+// workgroup, N * K < 2^31.  MX = 16 stages 16 activation rows (two DMAs per
+// wave and stage: rows w and w + 8); the MFMA tile is the same.
+template <int NS, bool SW, int NT, int MX>
 __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const uint16_t* __restrict__ x,
                                                                            const uint8_t* __restrict__ codes,
                                                                            const float* __restrict__ scales,
                                                                            uint16_t* __restrict__ y, int64_t ldy,
                                                                            int M, int N, int K) {
-    constexpr int W = kWideWaves, D = kRowD, STAGE = wide_stage<NT>(), OX = wide_ox<NT>(), OTAB = wide_otab<NT>();
+    constexpr int W = kWideWaves, D = kRowD, STAGE = wide_stage<NT>(), OX = wide_ox<NT>();
+    constexpr int OTAB = wide_otab<NT, MX>(), XSLOT = wide_xslot<MX>(), XD = MX / 8;
+    static_assert(MX == 8 || MX == 16, "8 or 16 activation rows");
     static_assert(W * NT * 256 * 4 <= D * STAGE, "partial sums fit in the code ring");
-    static_assert(NS * kWideKS <= kWideMaxK + kWideKS - 1, "the scale table holds 40 blocks per row");
+    static_assert(16 * NT * (NS * kWideKS / 128) * 4 <= kWideTable, "the scale table holds the tiles' rows");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -982,7 +992,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     const int R = (int)((int64_t)(blockIdx.x + 1) * units / gridDim.x) - u0;  // rows, or pairs
 
     for (int e = threadIdx.x; e < D * 64; e += 64 * W)
-        *reinterpret_cast<u32x4*>(lds + OX + (e >> 6) * kWideXSlot + M * 1024 + (e & 63) * 16) = u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(lds + OX + (e >> 6) * XSLOT + M * 1024 + (e & 63) * 16) = u32x4{0, 0, 0, 0};
     __syncthreads();
 
     i32x4 dq[2], sq[2];
@@ -1022,15 +1032,19 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
                      ok ? cvoff[q] + (uint32_t)(kWideKS * s) : kBufferOob, dq[part], 0);
         }
     };
-    // Activation DMA of a stage: wave w < M fills row w (chunk l ^ 2w at
-    // position l); the other waves land zeros in the zero row.
-    const int xm = wave;
-    const int xch = lane ^ (2 * xm);
+    // Activation DMA of a stage: wave w fills row w (and w + 8 when MX =
+    // 16; chunk l ^ 2m of row m at position l); rows past M land zeros in
+    // the zero row.
     auto issue_x = [&](int s) __attribute__((always_inline)) {
-        const int k = kWideKS * s + 8 * xch;
-        const bool ok = xm < M && k < K;
-        const uint32_t dst = lds0 + (uint32_t)(OX + (s % D) * kWideXSlot + (xm < M ? xm : M) * 1024);
-        dma16(__builtin_amdgcn_readfirstlane(dst), ok ? (uint32_t)((xm * K + k) * 2) : kBufferOob, dx, 0);
+#pragma unroll
+        for (int h = 0; h < XD; ++h) {
+            const int xm = wave + 8 * h;
+            const int xch = lane ^ (2 * xm);
+            const int k = kWideKS * s + 8 * xch;
+            const bool ok = xm < M && k < K;
+            const uint32_t dst = lds0 + (uint32_t)(OX + (s % D) * XSLOT + (xm < M ? xm : M) * 1024);
+            dma16(__builtin_amdgcn_readfirstlane(dst), ok ? (uint32_t)((xm * K + k) * 2) : kBufferOob, dx, 0);
+        }
     };
 
     // Scale table (dword DMAs, 256 bytes each): plain, the rows' R x S floats
@@ -1064,7 +1078,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
 
     const int row = lane & 15, g = lane >> 4;
     const int xr = row < M ? row : M;
-    const uint32_t xoff = (uint32_t)(OX + xr * 1024 + 16 * ((8 * wave + 2 * g) ^ (2 * (xr & 7))));
+    const uint32_t xoff = (uint32_t)(OX + xr * 1024 + 16 * ((8 * wave + 2 * g) ^ (2 * (xr & (MX - 1)))));
     const uint32_t coff = (uint32_t)(row * kWideKS + 16 * ((4 * wave + g) ^ row));
     f32x4 acc[NT];
 #pragma unroll
@@ -1072,14 +1086,14 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     const float* tab = reinterpret_cast<const float*>(lds + OTAB);
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        wait_vm<NT + 1>();
+        wait_vm<NT + XD>();
         gemm_fp8::wait_lgkm<0>();  // stage j - 1's LDS reads are in registers
         barrier();
         issue_codes(j + 2);
         issue_x(j + 2);
         if (j < nst && kWideKS * j + 64 * wave < K) {
-            const u32x4 x0 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * kWideXSlot);
-            const u32x4 x1 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * kWideXSlot + 16);
+            const u32x4 x0 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * XSLOT);
+            const u32x4 x1 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * XSLOT + 16);
             const int blk = 4 * j + (wave >> 1);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -1129,15 +1143,15 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     }
 }
 
-template <int NS, bool SW, int NT>
+template <int NS, bool SW, int NT, int MX>
 hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                            int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
-    auto kern = small_m_row_wide_kernel<NS, SW, NT>;
+    auto kern = small_m_row_wide_kernel<NS, SW, NT, MX>;
+    constexpr int lds = wide_lds<NT, MX>();
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, wide_lds<NT>());
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kWideWaves), wide_lds<NT>(), stream, x, codes, scales, y, ldy,
-                       M, N, K);
+    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kWideWaves), lds, stream, x, codes, scales, y, ldy, M, N, K);
     return hipGetLastError();
 }
 
@@ -1149,19 +1163,29 @@ hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float*
 // against 13.1 / 13.8) and at K = 4096 up to 40 rows per CU (8240 rows 10.5
 // / 10.7 against 11.1 / 11.6), slower at K = 4096 from 48 rows per CU
 // (17408 rows 19.1 / 19.2 against 17.0 / 17.6, 12288 rows 13.8 / 13.9
-// against 13.2 / 13.6), so those stay on the row-range kernel.  The choice
-// depends on the weight geometry only, the same for the plain and the
-// SwiGLU form.
+// against 13.2 / 13.6), so those stay on the row-range kernel.
+// At 9..16 rows (16 staged activation rows, at most 4 tiles in LDS, 2 when
+// K > 5120 for the scale table) it replaces the K-split tiles and the
+// row-range kernel at every shape measured (graph replay, random weights,
+// M = 9 / 16, non-temporal code DMAs in both): 8240 x 5120 11.0 / 11.5 us
+// against 13.4 / 15.0 (row-range), 12288 x 5120 13.8 / 14.1 against 15.8 /
+// 17.0, 7168 x 5120 9.5 / 10.1 against 10.6 / 11.2 (K-split), 5120 x 5120
+// 8.8 / 9.2 against 9.6 / 10.1, 5120 x 8704 12.3 / 13.3 against 13.5 / 14.2,
+// 8240 x 4096 10.9 / 11.0 against 11.0 / 12.4.  The choice depends on the
+// weight geometry and on M <= 8 against M > 8 only, the same for the plain
+// and the SwiGLU form.
 int row_wide_tiles(int M, int N, int K, bool swiglu, int& groups) {
     const int cus = compute_units();
     const int units = swiglu ? N / 2 : N;
-    if (M < 1 || M > kRowMaxM || K % 128 != 0 || K > kWideMaxK || units < 1 || (int64_t)N * K >= ((int64_t)1 << 31))
+    if (M < 1 || M > 16 || K % 128 != 0 || K > 9216 || units < 1 || (int64_t)N * K >= ((int64_t)1 << 31))
         return 0;
     const int rows_per_cu = (N + cus - 1) / cus;
-    if (K <= 4096 && stream_nb(K) != 0 && rows_per_cu > 40) return 0;
     groups = std::min(cus, units);
     const int per = (units + groups - 1) / groups;
     const int t = swiglu ? (per + 7) / 8 : (per + 15) / 16;
+    if (M > kRowMaxM) return t >= 1 && t <= (K > kWideMaxK ? 2 : 4) ? t : 0;
+    if (K > kWideMaxK) return 0;
+    if (K <= 4096 && stream_nb(K) != 0 && rows_per_cu > 40) return 0;
     return t >= 3 && t <= 5 ? t : 0;
 }
 
@@ -1267,19 +1291,27 @@ bool small_m_candidates_supported(int M, int N, int K) {
 
 namespace {
 
-template <bool SW, int NT>
+template <bool SW, int NT, int MX>
 hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
-    if (K <= 4096) return launch_row_wide<8, SW, NT>(x, codes, scales, y, ldy, M, N, K, groups, stream);
-    return launch_row_wide<10, SW, NT>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    if (K <= 4096) return launch_row_wide<8, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    if constexpr (MX == 16 && NT <= 2)
+        if (K > kWideMaxK) return launch_row_wide<18, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    return launch_row_wide<10, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
 }
 
 template <bool SW>
 hipError_t dispatch_row_wide(int nt, const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
-    if (nt == 3) return dispatch_row_wide<SW, 3>(x, codes, scales, y, ldy, M, N, K, groups, stream);
-    if (nt == 4) return dispatch_row_wide<SW, 4>(x, codes, scales, y, ldy, M, N, K, groups, stream);
-    return dispatch_row_wide<SW, 5>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    if (M > kRowMaxM) {
+        if (nt == 1) return dispatch_row_wide<SW, 1, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        if (nt == 2) return dispatch_row_wide<SW, 2, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        if (nt == 3) return dispatch_row_wide<SW, 3, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        return dispatch_row_wide<SW, 4, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    }
+    if (nt == 3) return dispatch_row_wide<SW, 3, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    if (nt == 4) return dispatch_row_wide<SW, 4, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    return dispatch_row_wide<SW, 5, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
 }
 
 }  // namespace

@@ -793,6 +793,35 @@ def test_small_m_row_wide(fp8lin, gpu, oracle, m, n, k):
     assert torch.equal(fp8lin.linear_candidates(xg, c, s, 0), want)
 
 
+@pytest.mark.parametrize("m,n,k", [(16, 16384, 5120), (12, 12288, 4096), (9, 4100, 4224), (16, 8190, 9216),
+                                   (11, 1100, 8704), (14, 6000, 640)])
+def test_small_m_row_wide_16_rows(fp8lin, gpu, oracle, m, n, k):
+    """The wide row-staged form with 16 staged activation rows (fp8_linear at
+    9..16 rows): 64 rows per workgroup (4 tiles, the maximum; 32 SwiGLU
+    pairs), 48 rows at K = 4096, a last stage of 128 values (K = 4224), 32
+    rows at K = 9216 (18 stages, the longest), one tile at K = 8704 and a
+    short K.  Every output against the FP64 oracle; the first 9 rows those of
+    a 9-row call (the summation depends on K only); the fused SwiGLU
+    bit-equal to fused_swiglu(fp8_linear) and within 1 ulp of the oracle
+    SwiGLU of the same sums; the head candidates of one call equal to those
+    of the stored logits."""
+    rng = np.random.default_rng(m * 7919 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"row-wide 16 {m}x{n}x{k}")
+    if m > 9:
+        assert torch.equal(fp8lin.fp8_linear(xg[:9].contiguous(), c, s, True), y[:9])
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+    want = fp8lin.vocabulary_candidates(y, 0)
+    assert torch.equal(fp8lin.linear_candidates(xg, c, s, 0), want)
+
+
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
 @pytest.mark.parametrize("m,n,k", [(9, 2056, 384), (16, 2056, 384), (12, 8208, 5120), (16, 8208, 4096),
                                    (13, 1040, 8704), (16, 8240, 8704), (17, 8208, 5120), (32, 8208, 4096),
@@ -800,14 +829,17 @@ def test_small_m_row_wide(fp8lin, gpu, oracle, m, n, k):
 def test_linear_mid_rows(fp8lin, gpu, oracle, m, n, k):
     """fp8_linear with 9..16 rows against more than 1024 weight rows runs the
     small-M matrix-core kernel, whose 16x16 MFMA tile holds every row (the
-    16-row workgroups at n = 2056 and 1040, the row-range form at n = 8208 and
-    8240), instead of a mostly-padding GEMM tile; 17..32 rows run the
-    row-range form with two activation tiles (n >= 32 rows per CU, k <= 5120:
-    8208, 8240) or the K-split 16-row tiles with two activation tiles (7168,
-    5120, 2056), each with the K partition of its 16-row form, so the first 16
-    rows' outputs are those of a 16-row call.  Every output against the
-    FP64 oracle; the fused SwiGLU bit-equal to fused_swiglu(fp8_linear), with
-    or without a workspace (none is needed); Engine::linear's FP8 GEMM branch
+    wide row-staged form with 16 staged activation rows up to 64 rows per CU
+    and K <= 5120, 32 rows per CU up to K = 9216: every shape here but 8240 x
+    8704, which takes the row-range form), instead of a mostly-padding
+    GEMM tile; 17..32 rows run the row-range form with two activation tiles
+    (n >= 32 rows per CU, k <= 5120: 8208, 8240) or the K-split 16-row tiles
+    with two activation tiles (7168, 5120, 2056).  Each form's summation
+    depends on K only: the first 9 rows of a 9..16-row call are those of a
+    9-row call, and the second activation tile of a 17..32-row call changes
+    none of the first 16 rows' outputs.  Every output against the FP64
+    oracle; the fused SwiGLU bit-equal to fused_swiglu(fp8_linear), with or
+    without a workspace (none is needed); Engine::linear's FP8 GEMM branch
     asks for no workspace and gives the same bits; an unaligned view of x
     runs the GEMM, at the bar."""
     import ctypes
@@ -822,7 +854,11 @@ def test_linear_mid_rows(fp8lin, gpu, oracle, m, n, k):
     assert_parity(bits(y), ref, f"mid rows {m}x{n}x{k}")
     if m > 16:
         # the second activation tile changes no output's summation
-        assert torch.equal(F.fp8_linear(xg[:16], c, s), y[:16])
+        xz = xg.clone()
+        xz[16:] = 0
+        assert torch.equal(F.fp8_linear(xz, c, s)[:16], y[:16])
+    elif m > 9:
+        assert torch.equal(F.fp8_linear(xg[:9].contiguous(), c, s), y[:9])
     assert F.lib().fp8lin_linear_swiglu_workspace_bytes(m, n, k) == 0
     fused = F.linear_swiglu(xg, c, s, split=False)
     assert torch.equal(fused, F.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
