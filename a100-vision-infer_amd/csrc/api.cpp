@@ -130,16 +130,13 @@ void check_scales(const float* scales, int64_t scale_cols, int64_t K) {
 // 8-row GEMV at the decode shapes).  It takes block scales [N, K/128],
 // K % 128 == 0, 16-byte aligned x and codes and 16 K < 2^31; weights of at
 // most 1024 rows keep the GEMV (four rows or fewer per CU), and so do two
-// rows at K <= 5120, where the two-row ring GEMV is as fast or faster
-// (gate/up 17.2 against 18.1 us) except on weights that the kernel's
-// row-range form serves (the output heads: 61.8 against 66.6 us at 75968 x
-// 5120, 96.0 against 109.2 at 124160 x 5120, 23.5 against 24.6 at 31040 x
-// 4096; measured on MI355X with random weights).
+// rows at K <= 5120 except on the weights where the matrix-core kernel
+// measured faster (small_m_two_rows: the output heads, 25..40 rows per CU).
 bool linear_small_m(const uint16_t* x, const uint8_t* codes, int64_t S, int64_t M, int64_t N, int64_t K) {
     if (!(M >= 2 && M <= 8 && N > 1024 && K % 128 == 0 && S == K / 128 && aligned16(x) && aligned16(codes) &&
           16 * K < kMaxDim && N * S * 4 < kMaxDim))
         return false;
-    return M > 2 || K > 5120 || fp8lin::small_m_candidates_supported(2, (int)N, (int)K);
+    return M > 2 || K > 5120 || fp8lin::small_m_two_rows((int)N, (int)K);
 }
 
 // K-split partials of fp8_linear's prefill GEMM (M > 8) for output row stride

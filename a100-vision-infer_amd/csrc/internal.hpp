@@ -50,6 +50,9 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
 // Supported: K / 128 in 25..40 with at least 32 weight rows per CU for M <=
 // 16 (24 for 17..32 rows), or K / 128 in 65..72 with 32 rows per CU for M <= 16.
 bool small_m_candidates_supported(int M, int N, int K);
+// Whether fp8lin_linear runs the small-M kernel at two rows and K <= 5120
+// (where it measured faster than the two-row ring GEMV for this weight).
+bool small_m_two_rows(int N, int K);
 hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
                                      int K, uint32_t* part, int64_t& groups, hipStream_t stream);
 // out[2m] = value, out[2m + 1] = column + offset of the best of the `chunks`

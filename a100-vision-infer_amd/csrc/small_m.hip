@@ -40,14 +40,10 @@
 // granularity that leaves a partial last round (1088 workgroups over 512
 // slots at the 17408-row gate/up).  See the kernel for its pipeline.
 //
-// At M <= 8, weights of up to 32 rows per compute unit run
-// small_m_row_kernel: one workgroup per compute unit streams its rows 1 KiB
-// of one row per DMA instruction, with the activations staged beside the
-// codes (see that kernel); 33..80 rows per compute unit at K <= 5120 run its
-// wide form, small_m_row_wide_kernel (512 bytes of each row per stage, up to
-// 5 tiles), where measured faster than the row-range kernel.  At 9..16 rows
-// the wide form stages 16 activation rows and serves up to 64 rows per
-// compute unit at K <= 5120 and up to 32 at K <= 9216.
+// Most decode shapes run small_m_row_wide_kernel, the row-staged form: one
+// workgroup per compute unit streams its rows (up to 80 at M <= 8, 64 at
+// 9..16 rows; 32 when K > 5120) 512 bytes of each row per stage, with the
+// activations staged beside the codes (see that kernel).
 //
 // Every kernel here DMAs the weight codes, which one launch reads once, with
 // the non-temporal cache policy (dma16_nt): 10-15% more bytes per second
@@ -703,251 +699,46 @@ int stream_nb(int K) {
     return 0;
 }
 
-// ---- row-staged form ----------------------------------------------------------
+// ---- row-staged form -----------------------------------------------------------
 //
-// Workgroup b (16 waves, one per CU) owns units [b U / G, (b + 1) U / G) of
-// the U = N rows (N / 2 output pairs for SW): at most 32 rows in two 16-row
-// MFMA tiles (SW: gate rows in tile 0, their up rows in tile 1).  The codes
-// stream through an LDS ring of 3 stages; stage s is the 1 KiB of K
-// [1024 s, 1024 s + 1024) of every row, one direct-to-LDS DMA per row, each
-// reading 1 KiB of one row as the decode GEMV does (the 8-row x 128-byte
-// DMAs of the forms above touch 8 rows per instruction).  The activations of
-// a stage (M <= 8 rows x 2 KiB) come by DMA with the stage's codes, 1 KiB per
-// wave (waves 2M.. land zeros in the zero row M that the padding lanes
-// read): register loads of the activations, even of padding rows, cost the
-// code stream 2 us at the decode shapes.  The block scales of the
-// workgroup's rows come once, into a table after the ring.
+// Workgroup b (8 waves, one workgroup per CU) owns units [b U / G, (b + 1) U
+// / G) of the U = N rows (N / 2 output pairs for SW): up to NT 16-row MFMA
+// tiles (SW: tile t holds the gate rows of pairs 8t..8t+7 in lanes 0..7 and
+// their up rows in lanes 8..15).  The codes stream through an LDS ring of 3
+// stages; stage s is the 512 bytes of K [512 s, 512 s + 512) of every row,
+// one direct-to-LDS DMA moving two rows' 512 bytes (non-temporal: the codes
+// are read once).  The activations of a stage (M <= MX rows x 1 KiB) come by
+// DMA with the stage's codes, one (MX = 8) or two (MX = 16) per wave; rows
+// past M land zeros in the zero row M that the padding lanes read.  The
+// block scales of the workgroup's rows come once, into a table after the
+// ring (dword DMAs, so that no load straddles the end of the range's
+// scales).
 //
 // LDS rows are 16-byte chunks XOR-swizzled so that the reads of one K offset
-// from 16 rows (codes: chunk c of row r at c ^ (r & 15)) or 8 rows (x: chunk
-// c of row m at c ^ 2m) fall on distinct banks; each DMA lane fetches the
-// global chunk that belongs at its LDS position.  K % 128 == 0 keeps every
-// XOR inside a group of chunks that is wholly in or out of range.
+// from 16 rows fall on distinct banks (codes: slot s = (tile s / 16, lane row
+// s % 16) at 512 s, chunk c at c ^ (s & 15); x: row m chunk c at c ^ 2m);
+// each DMA lane fetches the global chunk that belongs at its LDS position.
+// K % 128 == 0 keeps every XOR inside a group of chunks that is wholly in or
+// out of range.
 //
-// Wave w owns K [1024 s + 64 w, +64) of every stage s, both tiles.  Lane
+// Wave w owns K [512 s + 64 w, +64) of every stage s and every tile.  Lane
 // (n, g) reads the 16 codes of row n at 64 w + 16 g, converts them with the
 // row's scale and issues the two MFMAs of the K-step pair (codes 0..7, then
-// 8..15, against x at the same K).  The 16 waves' 16x16 sums are then added
-// in LDS in wave order.
+// 8..15, against x at the same K).  The 8 waves' 16x16 sums are then added in
+// LDS in wave order.  Summation order: per wave its K-steps in K order
+// through MFMA, then the wave partials in wave order; it depends on K only
+// (not on the row range, the tile, M or MX), so the SwiGLU form's sums are
+// the plain form's bit for bit.
 //
 // Issue order per wave: the scale table, codes(0), x(0), codes(1), x(1);
 // then at stage j (after the wait and the barrier) codes(j + 2), x(j + 2).
 // The wait at stage j needs x(j) and everything older; codes(j + 1) and
-// x(j + 1) are younger, so it is vmcnt(3) at every stage.
-//
-// Summation order: per wave its K-steps in K order through MFMA, then the 16
-// wave partials in wave order; it depends on K only, not on the row range or
-// the tile, so the SwiGLU form's sums are the plain form's bit for bit.
-constexpr int kRowWaves = 16;
-constexpr int kRowMax = 32;                               // rows per workgroup (two tiles)
-constexpr int kRowMaxM = 8;                               // activation rows
-constexpr int kRowD = 3;                                  // stages in the ring
-constexpr int kRowStage = kRowMax * 1024;                 // codes of a stage
-constexpr int kRowXSlot = (kRowMaxM + 1) * 2048;          // x rows 0..M-1 and the zero row
-constexpr int kRowOX = kRowD * kRowStage;
-constexpr int kRowOTab = kRowOX + kRowD * kRowXSlot;
-constexpr int kRowTable = kRowMax * 72 * 4;               // 32 rows x 72 blocks
-constexpr int kRowTableHalf = kRowTable / 2;              // SW: the up rows' scales
-constexpr int kRowLds = kRowOTab + kRowTable;             // 162816 bytes
-static_assert(kRowLds <= kMaxLds, "row-staged LDS");
-static_assert(kRowWaves * 2 * 256 * 4 <= kRowD * kRowStage, "partial sums fit in the code ring");
-static_assert(2 * kRowMaxM <= kRowWaves, "one activation DMA per wave and stage");
-
-// Requirements (checked by the host): 1 <= M <= 8, K % 128 == 0,
-// K <= 1024 NS (S = K / 128 <= 72), at most 32 rows (16 pairs) per
-// workgroup, N * K < 2^31.
-template <int NS, bool SW>
-__global__ __launch_bounds__(64 * kRowWaves) void small_m_row_kernel(const uint16_t* __restrict__ x,
-                                                                     const uint8_t* __restrict__ codes,
-                                                                     const float* __restrict__ scales,
-                                                                     uint16_t* __restrict__ y, int64_t ldy, int M,
-                                                                     int N, int K) {
-    constexpr int W = kRowWaves, D = kRowD;
-    static_assert(NS <= 9, "the scale table holds 72 blocks per row");
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
-    const int S = K >> 7;
-    const int nst = (K + 1023) >> 10;
-    const int half = N >> 1;
-    const int units = SW ? half : N;
-    const int u0 = (int)((int64_t)blockIdx.x * units / gridDim.x);
-    const int R = (int)((int64_t)(blockIdx.x + 1) * units / gridDim.x) - u0;  // rows, or pairs
-
-    // row M of every activation slot stays zero (padding lanes read it)
-    for (int e = threadIdx.x; e < D * 128; e += 64 * W)
-        *reinterpret_cast<u32x4*>(lds + kRowOX + (e >> 7) * kRowXSlot + M * 2048 + (e & 127) * 16) =
-            u32x4{0, 0, 0, 0};
-    __syncthreads();
-
-    // descriptors: q = 0 the rows (SW: gate rows) of slots 0..15, q = 1
-    // slots 16..31 (SW: the up rows)
-    i32x4 dq[2], sq[2];
-    if constexpr (SW) {
-        dq[0] = make_desc(codes + (R ? (int64_t)u0 * K : 0), (uint32_t)(R * K));
-        dq[1] = make_desc(codes + (R ? (int64_t)(half + u0) * K : 0), (uint32_t)(R * K));
-        sq[0] = make_desc(scales + (R ? (int64_t)u0 * S : 0), (uint32_t)(R * S * 4));
-        sq[1] = make_desc(scales + (R ? (int64_t)(half + u0) * S : 0), (uint32_t)(R * S * 4));
-    } else {
-        dq[0] = dq[1] = make_desc(codes + (R ? (int64_t)u0 * K : 0), (uint32_t)(R * K));
-        sq[0] = sq[1] = make_desc(scales + (R ? (int64_t)u0 * S : 0), (uint32_t)(R * S * 4));
-    }
-    const i32x4 dx = make_desc(x, (uint32_t)(M * K * 2));
-
-    // Code DMA q of a stage fills slot r = wave + 16 q with the row at local
-    // index lr of descriptor q (slot 16 + wave: row 16 + wave, or the up row
-    // of pair wave); lane l fetches chunk l ^ (r & 15) (r & 15 == wave).
-    const int cch = lane ^ wave;
-    uint32_t cvoff[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const int lr = SW ? wave : wave + 16 * q;
-        cvoff[q] = lr < R ? (uint32_t)(lr * K + 16 * cch) : kBufferOob;
-    }
-    auto issue_codes = [&](int s) __attribute__((always_inline)) {
-        const uint32_t base = lds0 + (uint32_t)((s % D) * kRowStage);
-        const bool ok = s < nst && 1024 * s + 16 * cch < K;
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-            dma16_nt(__builtin_amdgcn_readfirstlane(base + (uint32_t)((wave + 16 * q) * 1024)),
-                     ok && cvoff[q] != kBufferOob ? cvoff[q] + 1024u * (uint32_t)s : kBufferOob, dq[q], 0);
-    };
-    // Activation DMA of a stage: wave w < 2M fills row w / 2, positions
-    // 64 (w % 2) + l, with chunk (64 (w % 2) + l) ^ 2 m (8 values each); the
-    // other waves land zeros in the zero row.
-    const int xm = wave >> 1, xh = wave & 1;
-    const int xch = (64 * xh + lane) ^ (2 * xm);
-    auto issue_x = [&](int s) __attribute__((always_inline)) {
-        const int k = 1024 * s + 8 * xch;
-        const bool ok = xm < M && k < K;
-        const uint32_t dst = lds0 + (uint32_t)(kRowOX + (s % D) * kRowXSlot + (xm < M ? xm : M) * 2048 +
-                                               (xm < M ? 1024 * xh : 0));
-        dma16(__builtin_amdgcn_readfirstlane(dst), ok ? (uint32_t)((xm * K + k) * 2) : kBufferOob, dx, 0);
-    };
-
-    // Scale table: plain, the rows' R x S floats (waves 0..11, 768 bytes
-    // each); SW, the gate rows' and, from kRowTableHalf, the up rows' (waves
-    // 0..5 and 8..13).  Dword DMAs, so that no lane's load straddles the end
-    // of the rows' scales (what a partly out-of-range 16-byte load returns
-    // is left to the buffer range check).
-    {
-        const int part = SW ? wave >> 3 : 0;
-        const int c = SW ? wave & 7 : wave;
-        if (c < (SW ? 6 : 12)) {
-            const uint32_t bytes = (uint32_t)(R * S * 4);
-#pragma unroll
-            for (int i = 0; i < 3; ++i) {
-                const uint32_t at = (uint32_t)(256 * (3 * c + i));
-                const uint32_t off = at + 4u * (uint32_t)lane;
-                dma4(__builtin_amdgcn_readfirstlane(lds0 + kRowOTab + (uint32_t)(part * kRowTableHalf) + at),
-                     off < bytes ? off : kBufferOob, sq[part]);
-            }
-        }
-    }
-    auto sidx = [&](int r) __attribute__((always_inline)) -> int {
-        if constexpr (SW) return r < 16 ? r * S : kRowTableHalf / 4 + (r - 16) * S;
-        return r * S;
-    };
-
-    issue_codes(0);
-    issue_x(0);
-    issue_codes(1);
-    issue_x(1);
-
-    const int row = lane & 15, g = lane >> 4;
-    const int xr = row < M ? row : M;
-    // x chunk 8 w + 2 g (and + 1) of row xr, swizzled (the zero row: any)
-    const uint32_t xoff = (uint32_t)(kRowOX + xr * 2048 + 16 * ((8 * wave + 2 * g) ^ (2 * (xr & 7))));
-    // code chunk 4 w + g of slot 16 t + row, swizzled by row
-    const uint32_t coff = (uint32_t)(row * 1024 + 16 * ((4 * wave + g) ^ row));
-    f32x4 acc[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
-    const float* tab = reinterpret_cast<const float*>(lds + kRowOTab);
-#pragma unroll
-    for (int j = 0; j < NS; ++j) {
-        // x(j) and everything older have landed in this wave, so after the
-        // barrier in every wave, and every wave is done with stage j - 1,
-        // whose slots codes(j + 2) and x(j + 2) refill
-        wait_vm<3>();
-        gemm_fp8::wait_lgkm<0>();  // stage j - 1's LDS reads are in registers
-        barrier();
-        issue_codes(j + 2);
-        issue_x(j + 2);
-        if (j < nst && 1024 * j + 64 * wave < K) {
-            const uint8_t* st = lds + (j % D) * kRowStage + coff;
-            const u32x4 x0 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * kRowXSlot);
-            const u32x4 x1 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * kRowXSlot + 16);
-            const int blk = 8 * j + (wave >> 1);
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int r = 16 * t + row;
-                const u32x4 cw = *reinterpret_cast<const u32x4*>(st + t * 16 * 1024);
-                const float sc = tab[sidx(r) + blk];
-                uint32_t wv[8];
-                dequant4(cw.x, sc, wv[0], wv[1]);
-                dequant4(cw.y, sc, wv[2], wv[3]);
-                dequant4(cw.z, sc, wv[4], wv[5]);
-                dequant4(cw.w, sc, wv[6], wv[7]);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x0),
-                                                                 as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc[t], 0,
-                                                                 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1),
-                                                                 as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc[t], 0,
-                                                                 0, 0);
-            }
-        }
-    }
-    // stages past the end were issued too, into this workgroup's ring
-    wait_vm<0>();
-    __syncthreads();
-
-    // acc[t][i] = C[m = 4 g + i][slot 16 t + row]; partials in wave order
-    float* red = reinterpret_cast<float*>(lds);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) red[(wave * 2 + t) * 256 + (4 * g + i) * 16 + row] = acc[t][i];
-    __syncthreads();
-    const int e = threadIdx.x & 255, m = e >> 4, n = e & 15;
-    auto total = [&](int t) __attribute__((always_inline)) -> float {
-        float v = red[t * 256 + e];
-#pragma unroll
-        for (int w = 1; w < W; ++w) v = v + red[(w * 2 + t) * 256 + e];
-        return v;
-    };
-    if constexpr (SW) {
-        if (threadIdx.x < 256 && m < M && n < R)
-            y[(int64_t)m * ldy + u0 + n] = swiglu_bf16_bits(f32_to_bf16_bits(total(0)), f32_to_bf16_bits(total(1)));
-    } else {
-        const int t = (threadIdx.x >> 8) & 1;
-        if (threadIdx.x < 512 && m < M && 16 * t + n < R)
-            y[(int64_t)m * ldy + u0 + 16 * t + n] = f32_to_bf16_bits(total(t));
-    }
-}
-
-template <int NS, bool SW>
-hipError_t launch_row(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y, int64_t ldy,
-                      int M, int N, int K, int groups, hipStream_t stream) {
-    auto kern = small_m_row_kernel<NS, SW>;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kRowLds);
-    if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(kern, dim3(groups), dim3(64 * kRowWaves), kRowLds, stream, x, codes, scales, y, ldy, M, N,
-                       K);
-    return hipGetLastError();
-}
-
-// ---- row-staged form for wider weights --------------------------------------
-//
-// The same scheme for 33..80 rows per CU (K <= 5120): up to 5 16-row tiles
-// per workgroup, so the stages hold 512 bytes of each row (one DMA moves two
-// rows' 512 bytes) and the workgroup has 8 waves, wave w converting K
-// [512 s + 64 w, +64) of every tile.  SW: tile t holds gate rows of pairs
-// 8t..8t+7 in lanes 0..7 and their up rows in lanes 8..15.  Codes: slot s
-// (tile s / 16, lane row s % 16) at 512 s, chunk c at c ^ (s & 15); x: row m
-// (1 KiB: 512 values) chunk c at c ^ 2m.  Per wave and stage: NT code DMAs
-// and one activation DMA; the wait at stage j leaves codes(j + 1) and
-// x(j + 1) in flight: vmcnt(NT + 1).
+// x(j + 1) are younger: vmcnt(NT + MX / 8).  Stages past K still issue their
+// DMAs, with out-of-range offsets that land zeros in the ring, so the counts
+// are the same at every stage (a dummy register load in their place, in an
+// early form, overwrote a register the compiler had given to another value).
+constexpr int kRowMaxM = 8;                                   // activation rows staged at M <= 8
+constexpr int kRowD = 3;                                      // stages in the ring
 constexpr int kWideWaves = 8;
 constexpr int kWideKS = 512;                                  // K bytes of a row per stage
 constexpr int kWideMaxK = 5120;
@@ -1184,41 +975,29 @@ int row_wide_tiles(int M, int N, int K, bool swiglu, int& groups) {
     const int per = (units + groups - 1) / groups;
     const int t = swiglu ? (per + 7) / 8 : (per + 15) / 16;
     if (M > kRowMaxM) return t >= 1 && t <= (K > kWideMaxK ? 2 : 4) ? t : 0;
-    if (K > kWideMaxK) return 0;
+    if (K > kWideMaxK) return t >= 1 && t <= 2 ? t : 0;
     if (K <= 4096 && stream_nb(K) != 0 && rows_per_cu > 40) return 0;
-    return t >= 3 && t <= 5 ? t : 0;
-}
-
-// Workgroups of the row-staged form for this geometry (0: not served).
-int row_groups(int M, int N, int K, bool swiglu) {
-    const int cus = compute_units();
-    const int units = swiglu ? N / 2 : N;
-    const int cap = swiglu ? 16 : kRowMax;
-    if (M < 1 || M > kRowMaxM || K % 128 != 0 || K > 1024 * 9 || units < 1 ||
-        (int64_t)N * K >= ((int64_t)1 << 31))
-        return 0;
-    const int groups = std::min(cus, units);
-    return (units + groups - 1) / groups <= cap ? groups : 0;
+    return t >= 1 && t <= 5 ? t : 0;
 }
 
 }  // namespace
 
-// At M <= 8 and up to 32 rows per CU (K <= 9216) the row-staged form runs
-// (33..80 rows: its wide form, see row_wide_tiles).
-// Measured on MI355X (graph replay over 1 GiB of rotated codes; down
-// 5120 x 8704, QKV-gate 7168 x 5120, the reference benchmark's 5120 x 5120
-// at M = 8): 12.4 / 10.7 / 9.2 us against 13.5-13.7 / 10.8 / 9.6 for the
-// K-split tiles below; down at M = 2 12.2 against 13.3.  A pure DMA stream
-// in its pattern (no activations, no arithmetic) takes 9.9 / 8.6 / 7.0 us:
-// the activations (16 KiB per CU and stage at M = 8) cost about 1 us and
-// the conversions and MFMAs about 0.5-1.5 us beside it.  Variants measured
-// slower: 8 waves (13.1 us at down M = 8), activations held in registers
-// (loaded up front or per stage: 14.2-15.1), an activation ring one stage
-// ahead (12.5), and skipping the activation DMAs of padding rows (M = 8
-// unchanged in work but 13.5).
+// The row-staged form (row_wide_tiles) runs first.  Its first version
+// streamed up to 32 rows per CU in 1 KiB row pieces with 16 waves per
+// workgroup (two tiles, 3 stages of 32 KiB); with the non-temporal code DMAs
+// the 512-byte form took every such shape from it (graph replay, random
+// weights, M = 4 / 8, on one box): 7168 x 5120 8.98 / 9.15 us against 10.21 /
+// 10.33, 5120 x 5120 8.02 / 8.19 against 8.75 / 8.89, 6144 x 4096 7.87 /
+// 8.11 against 9.45 / 9.62, 5120 x 8704 11.74 / 11.83 against 12.15 /
+// 12.25, 2048 x 5120 6.59 / 6.62 against 8.09 / 8.12.  Variants of the
+// first version measured slower: 8 waves, activations held in registers
+// (loaded up front or per stage: an extra 2 us on the code stream), an
+// activation ring one stage ahead, and no activation DMA for the waves of
+// padding rows.
 //
-// Otherwise (9..16 rows, or K > 9216) a workgroup holds two row tiles (about
-// one workgroup per CU): four waves per tile split every chunk's 4 blocks,
+// Otherwise (K > 9216, or more rows per CU than the row-staged form holds
+// where the row-range kernel does not serve) a workgroup holds two row tiles
+// (about one workgroup per CU): four waves per tile split every chunk's 4 blocks,
 // each with a 3-block ring, and the eight waves share the activation
 // buffers, staged 2 chunks ahead.  Each tile sums exactly as a four-wave
 // workgroup alone would.  At M = 8 (before the row-staged form): 13.6 / 10.8
@@ -1281,6 +1060,22 @@ hipError_t dispatch_stream(int nb, const uint16_t* x, const uint8_t* codes, cons
 }  // namespace
 
 
+// fp8lin_linear at two rows and K <= 5120 takes the matrix-core path where it
+// measured faster than the two-row ring GEMV (graph replay, random weights):
+// the weights of the row-range kernel (the output heads: 75968 x 5120 61.8
+// against 66.6 us, 124160 x 5120 96.0 against 109.2) and those of the
+// row-staged form with 25..40 rows per CU (7168 x 5120 9.0 against 9.8,
+// 8192 x 5120 9.5 against 10.0, 8240 x 5120 10.4 against 10.6).  Fewer rows
+// per CU (5120 x 5120 8.0 against 7.8, 2048 x 5120 6.5 against 5.1) and the
+// 68 of gate/up (18.1 against 17.8) keep the GEMV.
+bool small_m_two_rows(int N, int K) {
+    if (small_m_candidates_supported(2, N, K)) return true;
+    const int cus = compute_units();
+    const int rows_per_cu = (N + cus - 1) / cus;
+    int groups = 0;
+    return rows_per_cu > 24 && rows_per_cu <= 40 && row_wide_tiles(2, N, K, false, groups) != 0;
+}
+
 bool small_m_candidates_supported(int M, int N, int K) {
     int nb = 0, per = 0, groups = 0;
     // only where fp8lin_linear runs the row-range kernel (its candidates
@@ -1295,7 +1090,7 @@ template <bool SW, int NT, int MX>
 hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
     if (K <= 4096) return launch_row_wide<8, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
-    if constexpr (MX == 16 && NT <= 2)
+    if constexpr (NT <= 2)
         if (K > kWideMaxK) return launch_row_wide<18, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     return launch_row_wide<10, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
 }
@@ -1309,6 +1104,8 @@ hipError_t dispatch_row_wide(int nt, const uint16_t* x, const uint8_t* codes, co
         if (nt == 3) return dispatch_row_wide<SW, 3, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
         return dispatch_row_wide<SW, 4, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     }
+    if (nt == 1) return dispatch_row_wide<SW, 1, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    if (nt == 2) return dispatch_row_wide<SW, 2, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     if (nt == 3) return dispatch_row_wide<SW, 3, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     if (nt == 4) return dispatch_row_wide<SW, 4, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     return dispatch_row_wide<SW, 5, 8>(x, codes, scales, y, ldy, M, N, K, groups, stream);
@@ -1357,13 +1154,6 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
         if (M > kStreamMaxM) return hipErrorNotSupported;
         if (swiglu) return launch<8, 3, 1, 1, 32, true, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
         return launch<8, 3, 1, 1, 32, false, 2>(x, codes, scales, y, ldy, M, N, K, per, stream);
-    }
-    if (const int rg = row_groups(M, N, K, swiglu)) {
-        if (K <= 5120)
-            return swiglu ? launch_row<5, true>(x, codes, scales, y, ldy, M, N, K, rg, stream)
-                          : launch_row<5, false>(x, codes, scales, y, ldy, M, N, K, rg, stream);
-        return swiglu ? launch_row<9, true>(x, codes, scales, y, ldy, M, N, K, rg, stream)
-                      : launch_row<9, false>(x, codes, scales, y, ldy, M, N, K, rg, stream);
     }
     // 9..16 rows: activations 2 chunks ahead (down / QKV-gate at M = 16:
     // 15.8 / 12.7 us with two row tiles per workgroup, against 18.6 / 13.9

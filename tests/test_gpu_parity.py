@@ -734,15 +734,16 @@ def test_linear_small_m_rows(fp8lin, gpu, oracle, m, n, k):
 @pytest.mark.parametrize("m,n,k", [(8, 8190, 9216), (7, 8190, 9216), (5, 300, 1152), (2, 1154, 2176),
                                    (4, 2050, 8192)])
 def test_small_m_row_staged_limits(fp8lin, gpu, oracle, m, n, k):
-    """The row-staged small-M form at its limits: 32 rows (16 SwiGLU pairs)
-    per workgroup with K = 9216 (the 72-block scale table of 32 rows, nine
-    stages), one or two rows per workgroup with a last stage of one block
-    (K = 1152), a last stage of 128 of 1024 values at an odd pair count
-    (1154 rows, 577 pairs), and K a whole number of stages.  Every output of
-    fp8_tensor_small (the small-M kernel at any row count) against the FP64
-    oracle, split 1 and 4 bit-equal; where fp8_linear takes the same kernel
-    (more than 1024 rows, 3..8 activation rows or 2 at K > 5120) it gives
-    the same bits; the fused SwiGLU bit-equal to fused_swiglu(fp8_linear)."""
+    """The row-staged small-M form at its K limit and smallest row counts:
+    32 rows (16 SwiGLU pairs) per workgroup with K = 9216 (two tiles, the
+    72-block scale table of 32 rows, 18 stages of 512 values), one or two
+    rows per workgroup with a last stage of 128 values (K = 1152), a last
+    stage of 128 of 512 values at an odd pair count (1154 rows, 577 pairs),
+    and K a whole number of stages.  Every output of fp8_tensor_small (the
+    small-M kernel at any row count) against the FP64 oracle, split 1 and 4
+    bit-equal; where fp8_linear takes the same kernel (more than 1024 rows,
+    3..8 activation rows or 2 at K > 5120) it gives the same bits; the fused
+    SwiGLU bit-equal to fused_swiglu(fp8_linear)."""
     rng = np.random.default_rng(m * 7919 + n + k)
     codes = rand_codes(rng, n, k)
     scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
