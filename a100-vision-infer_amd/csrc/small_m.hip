@@ -748,26 +748,27 @@ constexpr int kWideTable = 80 * (kWideMaxK / 128) * 4;        // 80 rows x 40 bl
 constexpr int kWideTableHalf = kWideTable / 2;                // SW: the up rows' scales
 template <int NT>
 constexpr int wide_stage() { return 16 * NT * kWideKS; }
-template <int NT>
-constexpr int wide_ox() { return kRowD * wide_stage<NT>(); }
-template <int NT, int MX>
-constexpr int wide_otab() { return wide_ox<NT>() + kRowD * wide_xslot<MX>(); }
-template <int NT, int MX>
-constexpr int wide_lds() { return wide_otab<NT, MX>() + kWideTable; }
+template <int NT, int D = kRowD>
+constexpr int wide_ox() { return D * wide_stage<NT>(); }
+template <int NT, int MX, int D = kRowD>
+constexpr int wide_otab() { return wide_ox<NT, D>() + D * wide_xslot<MX>(); }
+template <int NT, int MX, int D = kRowD>
+constexpr int wide_lds() { return wide_otab<NT, MX, D>() + kWideTable; }
 static_assert(wide_lds<5, 8>() <= kMaxLds && wide_lds<4, 16>() <= kMaxLds, "wide row-staged LDS");
 
 // Requirements (checked by the host): 1 <= M <= MX (8, or 16 with NT <= 4),
 // K % 128 == 0, K <= 512 NS <= 5120, at most 16 NT rows (8 NT pairs) per
 // workgroup, N * K < 2^31.  MX = 16 stages 16 activation rows (two DMAs per
 // wave and stage: rows w and w + 8); the MFMA tile is the same.
-template <int NS, bool SW, int NT, int MX>
+template <int NS, bool SW, int NT, int MX, int D>
 __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const uint16_t* __restrict__ x,
                                                                            const uint8_t* __restrict__ codes,
                                                                            const float* __restrict__ scales,
                                                                            uint16_t* __restrict__ y, int64_t ldy,
                                                                            int M, int N, int K) {
-    constexpr int W = kWideWaves, D = kRowD, STAGE = wide_stage<NT>(), OX = wide_ox<NT>();
-    constexpr int OTAB = wide_otab<NT, MX>(), XSLOT = wide_xslot<MX>(), XD = MX / 8;
+    constexpr int W = kWideWaves, STAGE = wide_stage<NT>(), OX = wide_ox<NT, D>();
+    constexpr int OTAB = wide_otab<NT, MX, D>(), XSLOT = wide_xslot<MX>(), XD = MX / 8;
+    static_assert(D >= 3, "at least two stages in flight");
     static_assert(MX == 8 || MX == 16, "8 or 16 activation rows");
     static_assert(W * NT * 256 * 4 <= D * STAGE, "partial sums fit in the code ring");
     static_assert(16 * NT * (NS * kWideKS / 128) * 4 <= kWideTable, "the scale table holds the tiles' rows");
@@ -862,10 +863,11 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
         return slot * S;
     };
 
-    issue_codes(0);
-    issue_x(0);
-    issue_codes(1);
-    issue_x(1);
+#pragma unroll
+    for (int p = 0; p < D - 1; ++p) {
+        issue_codes(p);
+        issue_x(p);
+    }
 
     const int row = lane & 15, g = lane >> 4;
     const int xr = row < M ? row : M;
@@ -877,11 +879,11 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     const float* tab = reinterpret_cast<const float*>(lds + OTAB);
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        wait_vm<NT + XD>();
+        wait_vm<(D - 2) * (NT + XD)>();
         gemm_fp8::wait_lgkm<0>();  // stage j - 1's LDS reads are in registers
         barrier();
-        issue_codes(j + 2);
-        issue_x(j + 2);
+        issue_codes(j + D - 1);
+        issue_x(j + D - 1);
         if (j < nst && kWideKS * j + 64 * wave < K) {
             const u32x4 x0 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * XSLOT);
             const u32x4 x1 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * XSLOT + 16);
@@ -934,11 +936,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     }
 }
 
-template <int NS, bool SW, int NT, int MX>
+template <int NS, bool SW, int NT, int MX, int D = kRowD>
 hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                            int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
-    auto kern = small_m_row_wide_kernel<NS, SW, NT, MX>;
-    constexpr int lds = wide_lds<NT, MX>();
+    auto kern = small_m_row_wide_kernel<NS, SW, NT, MX, D>;
+    constexpr int lds = wide_lds<NT, MX, D>();
+    static_assert(lds <= kMaxLds, "row-staged LDS");
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return attr;
@@ -1086,13 +1089,19 @@ bool small_m_candidates_supported(int M, int N, int K) {
 
 namespace {
 
+// Ring depth: 3 stages (two in flight), 4 for one tile, whose stages are
+// 8 KiB (measured on MI355X, graph replay, M = 4 / 8: 3072 x 8704 8.89 /
+// 8.84 us against 9.74 / 9.74, 2048 x 5120 6.31 / 6.36 against 6.59 / 6.60;
+// with two tiles a fourth stage was 2-5% slower, a fifth 5-8%).
 template <bool SW, int NT, int MX>
 hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
-    if (K <= 4096) return launch_row_wide<8, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    constexpr int D = NT == 1 ? 4 : kRowD;
+    if (K <= 4096) return launch_row_wide<8, SW, NT, MX, D>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     if constexpr (NT <= 2)
-        if (K > kWideMaxK) return launch_row_wide<18, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
-    return launch_row_wide<10, SW, NT, MX>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        if (K > kWideMaxK)
+            return launch_row_wide<18, SW, NT, MX, D>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    return launch_row_wide<10, SW, NT, MX, D>(x, codes, scales, y, ldy, M, N, K, groups, stream);
 }
 
 template <bool SW>
