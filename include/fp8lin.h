@@ -81,9 +81,10 @@ int fp8lin_decode(const uint8_t* codes, const float* scales, int64_t scale_cols,
  * (include/avi/ops.h:18, src/optimized.cu:61-70).  M <= 8 runs the decode
  * GEMV (128-bit loads when K, x and codes are 16-byte aligned, otherwise
  * byte loads with bit-identical results; vector_gemv changes nothing), except
- * that 3..8 rows (2 rows at K > 5120, or on weights of its row-range form:
- * more than 80 rows per compute unit at K = 4224..5120, more than 40 at
- * K = 3200..4096, as the output heads) against more than 1024 weight rows with
+ * that 3..8 rows (2 rows at K > 5120; at K <= 5120 on weights of its
+ * row-range form: more than 80 rows per compute unit at K = 4224..5120, more
+ * than 40 at K = 3200..4096, as the output heads; or 25..40 rows per compute
+ * unit on its row-staged form) against more than 1024 weight rows with
  * block scales, K % 128 == 0 and 16-byte aligned x and codes run the small-M
  * matrix-core kernel of fp8lin_tensor_small (one pass over the weights for
  * all rows; same parity bar, another FP32 summation order, so such a call and
