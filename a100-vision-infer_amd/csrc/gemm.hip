@@ -145,10 +145,11 @@ hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, 
 // of them, stream the codes once with each dequantized once (the wide
 // row-staged form up to 64 rows per CU, else the row-range form or the
 // K-split 16-row tiles); a GEMM tile would be at least seven eighths
-// padding.  17..32 rows in the row-range form with two activation tiles (at
-// least 32 weight rows per CU, K <= 5120), else in the K-split 16-row tiles
-// with two activation tiles.  Its geometry limits are those of the decode
-// routing (block scales [N, K/128], 16-byte aligned x and codes).
+// padding.  17..32 rows in the wide row-staged form with 32 staged
+// activation rows (up to 32 weight rows per CU), else in the row-range form
+// with two activation tiles (K <= 5120) or the K-split 16-row tiles with two
+// activation tiles.  Its geometry limits are those of the decode routing
+// (block scales [N, K/128], 16-byte aligned x and codes).
 bool mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K) {
     const int64_t lim = (int64_t)1 << 31;
     return M > 8 && M <= 32 && N > 1024 && K % 128 == 0 && S == K / 128 &&

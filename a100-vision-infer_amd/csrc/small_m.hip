@@ -708,8 +708,8 @@ int stream_nb(int K) {
 // stages; stage s is the 512 bytes of K [512 s, 512 s + 512) of every row,
 // one direct-to-LDS DMA moving two rows' 512 bytes (non-temporal: the codes
 // are read once).  The activations of a stage (M <= MX rows x 1 KiB) come by
-// DMA with the stage's codes, one (MX = 8) or two (MX = 16) per wave; rows
-// past M land zeros in the zero row M that the padding lanes read.  The
+// DMA with the stage's codes, MX / 8 per wave (MX = 8, 16 or 32); rows past
+// M land zeros in the zero row M that the padding lanes read.  The
 // block scales of the workgroup's rows come once, into a table after the
 // ring (dword DMAs, so that no load straddles the end of the range's
 // scales).
@@ -754,12 +754,17 @@ template <int NT, int MX, int D = kRowD>
 constexpr int wide_otab() { return wide_ox<NT, D>() + D * wide_xslot<MX>(); }
 template <int NT, int MX, int D = kRowD>
 constexpr int wide_lds() { return wide_otab<NT, MX, D>() + kWideTable; }
-static_assert(wide_lds<5, 8>() <= kMaxLds && wide_lds<4, 16>() <= kMaxLds, "wide row-staged LDS");
+static_assert(wide_lds<5, 8>() <= kMaxLds && wide_lds<4, 16>() <= kMaxLds && wide_lds<2, 32>() <= kMaxLds,
+              "wide row-staged LDS");
 
-// Requirements (checked by the host): 1 <= M <= MX (8, or 16 with NT <= 4),
-// K % 128 == 0, K <= 512 NS <= 5120, at most 16 NT rows (8 NT pairs) per
-// workgroup, N * K < 2^31.  MX = 16 stages 16 activation rows (two DMAs per
-// wave and stage: rows w and w + 8); the MFMA tile is the same.
+// Requirements (checked by the host): 1 <= M <= MX (8; 16 with NT <= 4; 32
+// with NT <= 2), K % 128 == 0, K <= 512 NS <= 5120, at most 16 NT rows (8 NT
+// pairs) per workgroup, N * K < 2^31.  MX = 16 stages 16 activation rows
+// (two DMAs per wave and stage: rows w and w + 8); the MFMA tile is the
+// same.  MX = 32 stages 32 (four DMAs: rows w + 8h) and runs two activation
+// tiles, rows 0..15 and 16..31: each converted code word feeds the MFMAs of
+// both, each with its own accumulator, so a row's sums do not depend on the
+// other tile.
 template <int NS, bool SW, int NT, int MX, int D>
 __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const uint16_t* __restrict__ x,
                                                                            const uint8_t* __restrict__ codes,
@@ -768,9 +773,10 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
                                                                            int M, int N, int K) {
     constexpr int W = kWideWaves, STAGE = wide_stage<NT>(), OX = wide_ox<NT, D>();
     constexpr int OTAB = wide_otab<NT, MX, D>(), XSLOT = wide_xslot<MX>(), XD = MX / 8;
+    constexpr int MI = MX == 32 ? 2 : 1;  // activation tiles
     static_assert(D >= 3, "at least two stages in flight");
-    static_assert(MX == 8 || MX == 16, "8 or 16 activation rows");
-    static_assert(W * NT * 256 * 4 <= D * STAGE, "partial sums fit in the code ring");
+    static_assert(MX == 8 || MX == 16 || MX == 32, "8, 16 or 32 activation rows");
+    static_assert(W * NT * MI * 256 * 4 <= D * STAGE, "partial sums fit in the code ring");
     static_assert(16 * NT * (NS * kWideKS / 128) * 4 <= kWideTable, "the scale table holds the tiles' rows");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -870,12 +876,18 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     }
 
     const int row = lane & 15, g = lane >> 4;
-    const int xr = row < M ? row : M;
-    const uint32_t xoff = (uint32_t)(OX + xr * 1024 + 16 * ((8 * wave + 2 * g) ^ (2 * (xr & (MX - 1)))));
-    const uint32_t coff = (uint32_t)(row * kWideKS + 16 * ((4 * wave + g) ^ row));
-    f32x4 acc[NT];
+    uint32_t xoff[MI];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mi = 0; mi < MI; ++mi) {
+        const int xr = 16 * mi + row < M ? 16 * mi + row : M;
+        xoff[mi] = (uint32_t)(OX + xr * 1024 + 16 * ((8 * wave + 2 * g) ^ (2 * (xr & (MX - 1)))));
+    }
+    const uint32_t coff = (uint32_t)(row * kWideKS + 16 * ((4 * wave + g) ^ row));
+    f32x4 acc[NT][MI];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) acc[t][mi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const float* tab = reinterpret_cast<const float*>(lds + OTAB);
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
@@ -885,8 +897,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
         issue_codes(j + D - 1);
         issue_x(j + D - 1);
         if (j < nst && kWideKS * j + 64 * wave < K) {
-            const u32x4 x0 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * XSLOT);
-            const u32x4 x1 = *reinterpret_cast<const u32x4*>(lds + xoff + (j % D) * XSLOT + 16);
+            u32x4 x0[MI], x1[MI];
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi) {
+                x0[mi] = *reinterpret_cast<const u32x4*>(lds + xoff[mi] + (j % D) * XSLOT);
+                x1[mi] = *reinterpret_cast<const u32x4*>(lds + xoff[mi] + (j % D) * XSLOT + 16);
+            }
             const int blk = 4 * j + (wave >> 1);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -898,40 +914,47 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
                 dequant4(cw.y, sc, wv[2], wv[3]);
                 dequant4(cw.z, sc, wv[4], wv[5]);
                 dequant4(cw.w, sc, wv[6], wv[7]);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x0),
-                                                                 as_bf16x8(wv[0], wv[1], wv[2], wv[3]), acc[t], 0,
-                                                                 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1),
-                                                                 as_bf16x8(wv[4], wv[5], wv[6], wv[7]), acc[t], 0,
-                                                                 0, 0);
+#pragma unroll
+                for (int mi = 0; mi < MI; ++mi) {
+                    acc[t][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x0[mi]),
+                                                                         as_bf16x8(wv[0], wv[1], wv[2], wv[3]),
+                                                                         acc[t][mi], 0, 0, 0);
+                    acc[t][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1[mi]),
+                                                                         as_bf16x8(wv[4], wv[5], wv[6], wv[7]),
+                                                                         acc[t][mi], 0, 0, 0);
+                }
             }
         }
     }
     wait_vm<0>();
     __syncthreads();
 
-    // acc[t][i] = C[m = 4 g + i][slot 16 t + row]; partials in wave order
+    // acc[t][mi][i] = C[m = 16 mi + 4 g + i][slot 16 t + row]; partials in
+    // wave order (block tm = MI t + mi)
     float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[(wave * NT + t) * 256 + (4 * g + i) * 16 + row] = acc[t][i];
-    __syncthreads();
-    auto total = [&](int t, int e) __attribute__((always_inline)) -> float {
-        float v = red[t * 256 + e];
+        for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int w = 1; w < W; ++w) v = v + red[(w * NT + t) * 256 + e];
+            for (int i = 0; i < 4; ++i)
+                red[((wave * NT + t) * MI + mi) * 256 + (4 * g + i) * 16 + row] = acc[t][mi][i];
+    __syncthreads();
+    auto total = [&](int tm, int e) __attribute__((always_inline)) -> float {
+        float v = red[tm * 256 + e];
+#pragma unroll
+        for (int w = 1; w < W; ++w) v = v + red[(w * NT * MI + tm) * 256 + e];
         return v;
     };
-    for (int q = threadIdx.x; q < NT * 256; q += 64 * W) {
-        const int t = q >> 8, e = q & 255, m = e >> 4, n = e & 15;
+    for (int q = threadIdx.x; q < NT * MI * 256; q += 64 * W) {
+        const int tm = q >> 8, t = tm / MI, e = q & 255, m = 16 * (tm % MI) + (e >> 4), n = e & 15;
         if (m >= M) continue;
         if constexpr (SW) {
             if (n < 8 && 8 * t + n < R)
                 y[(int64_t)m * ldy + u0 + 8 * t + n] =
-                    swiglu_bf16_bits(f32_to_bf16_bits(total(t, e)), f32_to_bf16_bits(total(t, e + 8)));
+                    swiglu_bf16_bits(f32_to_bf16_bits(total(tm, e)), f32_to_bf16_bits(total(tm, e + 8)));
         } else {
-            if (16 * t + n < R) y[(int64_t)m * ldy + u0 + 16 * t + n] = f32_to_bf16_bits(total(t, e));
+            if (16 * t + n < R) y[(int64_t)m * ldy + u0 + 16 * t + n] = f32_to_bf16_bits(total(tm, e));
         }
     }
 }
@@ -965,18 +988,27 @@ hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float*
 // against 13.4 / 15.0 (row-range), 12288 x 5120 13.8 / 14.1 against 15.8 /
 // 17.0, 7168 x 5120 9.5 / 10.1 against 10.6 / 11.2 (K-split), 5120 x 5120
 // 8.8 / 9.2 against 9.6 / 10.1, 5120 x 8704 12.3 / 13.3 against 13.5 / 14.2,
-// 8240 x 4096 10.9 / 11.0 against 11.0 / 12.4.  The choice depends on the
-// weight geometry and on M <= 8 against M > 8 only, the same for the plain
-// and the SwiGLU form.
+// 8240 x 4096 10.9 / 11.0 against 11.0 / 12.4.  At 17..32 rows (32 staged
+// activation rows, two activation tiles, at most 2 tiles in LDS: 163 328
+// bytes at K > 5120) it replaces the K-split tiles with two activation tiles
+// at every shape measured (graph replay, random weights, M = 17 / 32):
+// 5120 x 8704 17.0 / 17.2 us against 18.1 / 18.9, 7168 x 5120 12.0 / 12.9
+// against 13.2 / 14.1, 5120 x 5120 11.0 / 11.9 against 12.0 / 13.1, 2048 x
+// 5120 8.1 / 9.4 against 10.9 / 11.9, 3072 x 8704 12.1 / 14.3 against 16.2 /
+// 17.2, 6144 x 9216 16.5 / 18.2 against 18.5 / 20.2, 6144 x 4096 10.3 / 10.9
+// against 10.8 / 11.7.  The choice depends on the weight geometry and on the
+// row count's range (1..8, 9..16, 17..32) only, the same for the plain and
+// the SwiGLU form.
 int row_wide_tiles(int M, int N, int K, bool swiglu, int& groups) {
     const int cus = compute_units();
     const int units = swiglu ? N / 2 : N;
-    if (M < 1 || M > 16 || K % 128 != 0 || K > 9216 || units < 1 || (int64_t)N * K >= ((int64_t)1 << 31))
+    if (M < 1 || M > 32 || K % 128 != 0 || K > 9216 || units < 1 || (int64_t)N * K >= ((int64_t)1 << 31))
         return 0;
     const int rows_per_cu = (N + cus - 1) / cus;
     groups = std::min(cus, units);
     const int per = (units + groups - 1) / groups;
     const int t = swiglu ? (per + 7) / 8 : (per + 15) / 16;
+    if (M > 16) return t >= 1 && t <= 2 ? t : 0;
     if (M > kRowMaxM) return t >= 1 && t <= (K > kWideMaxK ? 2 : 4) ? t : 0;
     if (K > kWideMaxK) return t >= 1 && t <= 2 ? t : 0;
     if (K <= 4096 && stream_nb(K) != 0 && rows_per_cu > 40) return 0;
@@ -1092,11 +1124,12 @@ namespace {
 // Ring depth: 3 stages (two in flight), 4 for one tile, whose stages are
 // 8 KiB (measured on MI355X, graph replay, M = 4 / 8: 3072 x 8704 8.89 /
 // 8.84 us against 9.74 / 9.74, 2048 x 5120 6.31 / 6.36 against 6.59 / 6.60;
-// with two tiles a fourth stage was 2-5% slower, a fifth 5-8%).
+// with two tiles a fourth stage was 2-5% slower, a fifth 5-8%; with 32
+// staged activation rows a one-tile ring stays at 3 stages, 122 KiB).
 template <bool SW, int NT, int MX>
 hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
-    constexpr int D = NT == 1 ? 4 : kRowD;
+    constexpr int D = NT == 1 && MX < 32 ? 4 : kRowD;
     if (K <= 4096) return launch_row_wide<8, SW, NT, MX, D>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     if constexpr (NT <= 2)
         if (K > kWideMaxK)
@@ -1107,6 +1140,10 @@ hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const floa
 template <bool SW>
 hipError_t dispatch_row_wide(int nt, const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
+    if (M > 16) {
+        if (nt == 1) return dispatch_row_wide<SW, 1, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        return dispatch_row_wide<SW, 2, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    }
     if (M > kRowMaxM) {
         if (nt == 1) return dispatch_row_wide<SW, 1, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
         if (nt == 2) return dispatch_row_wide<SW, 2, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);

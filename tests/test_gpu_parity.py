@@ -823,6 +823,36 @@ def test_small_m_row_wide_16_rows(fp8lin, gpu, oracle, m, n, k):
     assert torch.equal(fp8lin.linear_candidates(xg, c, s, 0), want)
 
 
+@pytest.mark.parametrize("m,n,k", [(32, 5120, 8704), (24, 7168, 5120), (17, 2048, 5120), (32, 6144, 4096),
+                                   (20, 3100, 9216), (31, 8190, 640), (25, 4100, 4224)])
+def test_small_m_row_wide_32_rows(fp8lin, gpu, oracle, m, n, k):
+    """The wide row-staged form with 32 staged activation rows (fp8_linear at
+    17..32 rows, up to 32 weight rows per CU): two tiles at K = 8704 (18
+    stages, the ring at its LDS limit), K = 5120 and K = 4096, one tile at
+    K = 5120 and at K = 9216 (the longest), a short K, and a last stage of
+    128 values (K = 4224).  Every output against the FP64 oracle; the first
+    17 rows those of a 17-row call, and rows 16.. changing none of the first
+    16 outputs (each activation tile sums on its own, in an order that
+    depends on K only); the fused SwiGLU bit-equal to fused_swiglu(fp8_linear)
+    and within 1 ulp of the oracle SwiGLU of the same sums."""
+    rng = np.random.default_rng(m * 7907 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"row-wide 32 {m}x{n}x{k}")
+    if m > 17:
+        assert torch.equal(fp8lin.fp8_linear(xg[:17].contiguous(), c, s, True), y[:17])
+    xz = xg.clone()
+    xz[16:] = 0
+    assert torch.equal(fp8lin.fp8_linear(xz, c, s, True)[:16], y[:16])
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+
+
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
 @pytest.mark.parametrize("m,n,k", [(9, 2056, 384), (16, 2056, 384), (12, 8208, 5120), (16, 8208, 4096),
                                    (13, 1040, 8704), (16, 8240, 8704), (17, 8208, 5120), (32, 8208, 4096),
@@ -833,9 +863,9 @@ def test_linear_mid_rows(fp8lin, gpu, oracle, m, n, k):
     wide row-staged form with 16 staged activation rows up to 64 rows per CU
     and K <= 5120, 32 rows per CU up to K = 9216: every shape here but 8240 x
     8704, which takes the row-range form), instead of a mostly-padding
-    GEMM tile; 17..32 rows run the row-range form with two activation tiles
-    (n >= 32 rows per CU, k <= 5120: 8208, 8240) or the K-split 16-row tiles
-    with two activation tiles (7168, 5120, 2056).  Each form's summation
+    GEMM tile; 17..32 rows run the wide row-staged form with 32 staged rows
+    (up to 32 rows per CU: 7168, 5120, 2056) or the row-range form with two
+    activation tiles (8208, 8240).  Each form's summation
     depends on K only: the first 9 rows of a 9..16-row call are those of a
     9-row call, and the second activation tile of a 17..32-row call changes
     none of the first 16 rows' outputs.  Every output against the FP64
