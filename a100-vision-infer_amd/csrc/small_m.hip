@@ -705,9 +705,10 @@ int stream_nb(int K) {
 // / G) of the U = N rows (N / 2 output pairs for SW): up to NT 16-row MFMA
 // tiles (SW: tile t holds the gate rows of pairs 8t..8t+7 in lanes 0..7 and
 // their up rows in lanes 8..15).  The codes stream through an LDS ring of 3
-// stages; stage s is the 512 bytes of K [512 s, 512 s + 512) of every row,
-// one direct-to-LDS DMA moving two rows' 512 bytes (non-temporal: the codes
-// are read once).  The activations of a stage (M <= MX rows x 1 KiB) come by
+// stages; stage s is the 512 bytes of K [512 s, 512 s + 512) of every row
+// (256 bytes in the half-stage form, where 512 would not fit), one
+// direct-to-LDS DMA moving two rows' 512 bytes (non-temporal: the codes are
+// read once).  The activations of a stage (M <= MX rows x 1 KiB) come by
 // DMA with the stage's codes, MX / 8 per wave (MX = 8, 16 or 32); rows past
 // M land zeros in the zero row M that the padding lanes read.  The
 // block scales of the workgroup's rows come once, into a table after the
@@ -742,55 +743,85 @@ constexpr int kRowD = 3;                                      // stages in the r
 constexpr int kWideWaves = 8;
 constexpr int kWideKS = 512;                                  // K bytes of a row per stage
 constexpr int kWideMaxK = 5120;
-template <int MX>
-constexpr int wide_xslot() { return (MX + 1) * 1024; }         // x rows 0..M-1 and the zero row
+template <int MX, int KS = kWideKS>
+constexpr int wide_xslot() { return (MX + 1) * 2 * KS; }      // x rows 0..M-1 and the zero row
 constexpr int kWideTable = 80 * (kWideMaxK / 128) * 4;        // 80 rows x 40 blocks
 constexpr int kWideTableHalf = kWideTable / 2;                // SW: the up rows' scales
-template <int NT>
-constexpr int wide_stage() { return 16 * NT * kWideKS; }
-template <int NT, int D = kRowD>
-constexpr int wide_ox() { return D * wide_stage<NT>(); }
-template <int NT, int MX, int D = kRowD>
-constexpr int wide_otab() { return wide_ox<NT, D>() + D * wide_xslot<MX>(); }
-template <int NT, int MX, int D = kRowD>
-constexpr int wide_lds() { return wide_otab<NT, MX, D>() + kWideTable; }
-static_assert(wide_lds<5, 8>() <= kMaxLds && wide_lds<4, 16>() <= kMaxLds && wide_lds<2, 32>() <= kMaxLds,
+template <int NT, int KS = kWideKS>
+constexpr int wide_stage() { return 16 * NT * KS; }
+template <int NT, int KS = kWideKS>
+constexpr int wide_code_dmas() { return (16 * NT * KS / 1024 + kWideWaves - 1) / kWideWaves; }  // per wave
+template <int NT, int D = kRowD, int KS = kWideKS>
+constexpr int wide_ox() { return D * wide_stage<NT, KS>(); }
+template <int NT, int MX, int D = kRowD, int KS = kWideKS>
+constexpr int wide_otab() { return wide_ox<NT, D, KS>() + D * wide_xslot<MX, KS>(); }
+// The table, then (where the last code DMA of a stage would run past the
+// stage) 1 KiB that such DMAs fill with zeros.
+template <int NT, int MX, int D = kRowD, int KS = kWideKS>
+constexpr int wide_odump() { return wide_otab<NT, MX, D, KS>() + kWideTable; }
+template <int NT, int MX, int D = kRowD, int KS = kWideKS>
+constexpr int wide_lds() {
+    return wide_odump<NT, MX, D, KS>() + (wide_code_dmas<NT, KS>() * kWideWaves * 1024 > wide_stage<NT, KS>() ? 1024 : 0);
+}
+static_assert(wide_lds<5, 8>() <= kMaxLds && wide_lds<4, 16>() <= kMaxLds && wide_lds<2, 32>() <= kMaxLds &&
+                  wide_lds<5, 32, kRowD, 256>() <= kMaxLds,
               "wide row-staged LDS");
 
 // Requirements (checked by the host): 1 <= M <= MX (8; 16 with NT <= 4; 32
-// with NT <= 2), K % 128 == 0, K <= 512 NS <= 5120, at most 16 NT rows (8 NT
-// pairs) per workgroup, N * K < 2^31.  MX = 16 stages 16 activation rows
-// (two DMAs per wave and stage: rows w and w + 8); the MFMA tile is the
-// same.  MX = 32 stages 32 (four DMAs: rows w + 8h) and runs two activation
-// tiles, rows 0..15 and 16..31: each converted code word feeds the MFMAs of
-// both, each with its own accumulator, so a row's sums do not depend on the
-// other tile.
-template <int NS, bool SW, int NT, int MX, int D>
+// with NT <= 2; with KS = 256, 16 or 32 with NT <= 5), K % 128 == 0,
+// K <= KS NS <= 5120 (9216 with NT <= 2), at most 16 NT rows (8 NT pairs) per
+// workgroup, N * K < 2^31.  MX = 16 stages 16 activation rows (two DMAs per
+// wave and stage at KS = 512: rows w and w + 8); the MFMA tile is the same.
+// MX = 32 stages 32 and runs two activation tiles, rows 0..15 and 16..31:
+// each converted code word feeds the MFMAs of both, each with its own
+// accumulator, so a row's sums do not depend on the other tile.
+//
+// KS is the stage's K bytes per row.  KS = 512: wave w owns K [512 s + 64 w,
+// +64) of stage s, a lane 16 codes, two MFMAs per tile.  KS = 256 (half the
+// ring and activation slots, for the tiles that do not fit at 512): wave w
+// owns K [256 s + 32 w, +32), a lane (n, g) the 8 codes of row n at
+// 32 w + 8 g, one MFMA per tile; a code DMA moves four rows' 256 bytes, an
+// activation DMA two rows' 512 bytes (a pair past M lands zeros in the zero
+// row and the unused row after it).  The summation order (per wave its
+// K-steps in K order, then the wave partials in wave order) depends on K and
+// KS only.
+template <int NS, bool SW, int NT, int MX, int D, int KS = kWideKS>
 __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const uint16_t* __restrict__ x,
                                                                            const uint8_t* __restrict__ codes,
                                                                            const float* __restrict__ scales,
                                                                            uint16_t* __restrict__ y, int64_t ldy,
                                                                            int M, int N, int K) {
-    constexpr int W = kWideWaves, STAGE = wide_stage<NT>(), OX = wide_ox<NT, D>();
-    constexpr int OTAB = wide_otab<NT, MX, D>(), XSLOT = wide_xslot<MX>(), XD = MX / 8;
-    constexpr int MI = MX == 32 ? 2 : 1;  // activation tiles
+    constexpr int W = kWideWaves, STAGE = wide_stage<NT, KS>(), OX = wide_ox<NT, D, KS>();
+    constexpr int OTAB = wide_otab<NT, MX, D, KS>(), XSLOT = wide_xslot<MX, KS>();
+    constexpr int XROW = 2 * KS;                 // activation bytes of a row per stage
+    constexpr int XRPD = 1024 / XROW;            // activation rows per DMA
+    constexpr int XD = MX / (8 * XRPD);          // activation DMAs per wave
+    constexpr int RPD = 1024 / KS;               // code rows per DMA
+    constexpr int CD = wide_code_dmas<NT, KS>(); // code DMAs per wave
+    constexpr int CPR = KS / 16;                 // 16-byte chunks of a row's stage
+    constexpr int KW = KS / 8;                   // K of a wave per stage
+    constexpr int MI = MX == 32 ? 2 : 1;         // activation tiles
+    constexpr bool DUMP = CD * W * 1024 > STAGE;  // the last code DMAs run past the stage
+    static_assert(KS == 512 || KS == 256, "512- or 256-byte stages");
     static_assert(D >= 3, "at least two stages in flight");
     static_assert(MX == 8 || MX == 16 || MX == 32, "8, 16 or 32 activation rows");
-    static_assert(W * NT * MI * 256 * 4 <= D * STAGE, "partial sums fit in the code ring");
-    static_assert(16 * NT * (NS * kWideKS / 128) * 4 <= kWideTable, "the scale table holds the tiles' rows");
+    static_assert(KS == 512 || MX >= 16, "256-byte stages stage 16 or 32 activation rows");
+    static_assert(W * NT * MI * 256 * 4 <= OTAB, "partial sums fit below the scale table");
+    static_assert(16 * NT * (NS * KS / 128) * 4 <= kWideTable, "the scale table holds the tiles' rows");
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t lds0 = (uint32_t)(uintptr_t)lds;
     const int S = K >> 7;
-    const int nst = (K + kWideKS - 1) / kWideKS;
+    const int nst = (K + KS - 1) / KS;
     const int half = N >> 1;
     const int units = SW ? half : N;
     const int u0 = (int)((int64_t)blockIdx.x * units / gridDim.x);
     const int R = (int)((int64_t)(blockIdx.x + 1) * units / gridDim.x) - u0;  // rows, or pairs
 
-    for (int e = threadIdx.x; e < D * 64; e += 64 * W)
-        *reinterpret_cast<u32x4*>(lds + OX + (e >> 6) * XSLOT + M * 1024 + (e & 63) * 16) = u32x4{0, 0, 0, 0};
+    for (int e = threadIdx.x; e < D * (XROW / 16); e += 64 * W)
+        *reinterpret_cast<u32x4*>(lds + OX + (e >> (KS == 512 ? 6 : 5)) * XSLOT + M * XROW +
+                                  (e & (XROW / 16 - 1)) * 16) = u32x4{0, 0, 0, 0};
     __syncthreads();
 
     i32x4 dq[2], sq[2];
@@ -805,42 +836,48 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     }
     const i32x4 dx = make_desc(x, (uint32_t)(M * K * 2));
 
-    // Code DMA q of a stage: instruction i = wave + 8 q fills slots 2i, 2i + 1
-    // (lanes 0..31, 32..63); lane l fetches chunk (l & 31) ^ (slot & 15) of
-    // its slot's row, local row lr of descriptor part (SW: slot lane rows
-    // 0..7 gate, 8..15 up).
-    uint32_t cvoff[NT];
-    int cch[NT];
+    // Code DMA q of a stage: instruction i = wave + 8 q fills slots RPD i ..
+    // RPD i + RPD - 1 (CPR lanes each); lane l fetches chunk (l % CPR) ^
+    // (slot & 15) of its slot's row, local row lr of descriptor part (SW:
+    // slot lane rows 0..7 gate, 8..15 up).  An instruction past the stage
+    // (its slots past 16 NT) fills the dump area with zeros.
+    uint32_t cvoff[CD];
+    int cch[CD];
 #pragma unroll
-    for (int q = 0; q < NT; ++q) {
-        const int slot = 2 * (wave + W * q) + (lane >> 5);
+    for (int q = 0; q < CD; ++q) {
+        const int slot = RPD * (wave + W * q) + (lane >> (KS == 512 ? 5 : 4));
         const int t = slot >> 4, n = slot & 15;
         const int lr = SW ? 8 * t + (n & 7) : slot;
-        cch[q] = (lane & 31) ^ n;
-        cvoff[q] = lr < R ? (uint32_t)(lr * K + 16 * cch[q]) : kBufferOob;
+        cch[q] = (lane & (CPR - 1)) ^ n;
+        cvoff[q] = (!DUMP || slot < 16 * NT) && lr < R ? (uint32_t)(lr * K + 16 * cch[q]) : kBufferOob;
     }
     auto issue_codes = [&](int s) __attribute__((always_inline)) {
         const uint32_t base = lds0 + (uint32_t)((s % D) * STAGE);
 #pragma unroll
-        for (int q = 0; q < NT; ++q) {
+        for (int q = 0; q < CD; ++q) {
             const int ins = wave + W * q;
-            const int part = SW ? ((2 * ins) & 15) >> 3 : 0;  // both slots of an instruction are gate or up
-            const bool ok = s < nst && kWideKS * s + 16 * cch[q] < K && cvoff[q] != kBufferOob;
-            dma16_nt(__builtin_amdgcn_readfirstlane(base + (uint32_t)(ins * 1024)),
-                     ok ? cvoff[q] + (uint32_t)(kWideKS * s) : kBufferOob, dq[part], 0);
+            const int part = SW ? ((RPD * ins) & 15) >> 3 : 0;  // an instruction's slots are all gate or all up
+            const bool ok = s < nst && KS * s + 16 * cch[q] < K && cvoff[q] != kBufferOob;
+            uint32_t dst = base + (uint32_t)(ins * 1024);
+            if constexpr (DUMP)
+                if ((ins + 1) * 1024 > STAGE) dst = lds0 + (uint32_t)wide_odump<NT, MX, D, KS>();
+            dma16_nt(__builtin_amdgcn_readfirstlane(dst), ok ? cvoff[q] + (uint32_t)(KS * s) : kBufferOob,
+                     dq[part], 0);
         }
     };
-    // Activation DMA of a stage: wave w fills row w (and w + 8 when MX =
-    // 16; chunk l ^ 2m of row m at position l); rows past M land zeros in
-    // the zero row.
+    // Activation DMA h of a stage: rows r0 = XRPD (wave + 8 h) .. r0 + XRPD -
+    // 1, 64 / XRPD lanes each; chunk p of row m holds the row's chunk p ^ (2 m
+    // mod XROW / 16).  Rows past M land zeros (a DMA wholly past M at the
+    // zero row M).
     auto issue_x = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
         for (int h = 0; h < XD; ++h) {
-            const int xm = wave + 8 * h;
-            const int xch = lane ^ (2 * xm);
-            const int k = kWideKS * s + 8 * xch;
+            const int r0 = XRPD * (wave + 8 * h);
+            const int xm = XRPD == 1 ? r0 : r0 + (lane >> 5);
+            const int xch = KS == 512 ? lane ^ (2 * xm) : (lane & 31) ^ ((2 * xm) & 31);
+            const int k = KS * s + 8 * xch;
             const bool ok = xm < M && k < K;
-            const uint32_t dst = lds0 + (uint32_t)(OX + (s % D) * XSLOT + (xm < M ? xm : M) * 1024);
+            const uint32_t dst = lds0 + (uint32_t)(OX + (s % D) * XSLOT + (r0 < M ? r0 : M) * XROW);
             dma16(__builtin_amdgcn_readfirstlane(dst), ok ? (uint32_t)((xm * K + k) * 2) : kBufferOob, dx, 0);
         }
     };
@@ -876,13 +913,17 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     }
 
     const int row = lane & 15, g = lane >> 4;
+    // a lane's activation fragment: chunk 8 w + 2 g (and the next) of a
+    // 1 KiB row at KS = 512, chunk 4 w + g of a 512-byte row at KS = 256
     uint32_t xoff[MI];
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
         const int xr = 16 * mi + row < M ? 16 * mi + row : M;
-        xoff[mi] = (uint32_t)(OX + xr * 1024 + 16 * ((8 * wave + 2 * g) ^ (2 * (xr & (MX - 1)))));
+        const int ch = KS == 512 ? 8 * wave + 2 * g : 4 * wave + g;
+        xoff[mi] = (uint32_t)(OX + xr * XROW + 16 * (ch ^ (KS == 512 ? 2 * (xr & (MX - 1)) : (2 * xr) & 31)));
     }
-    const uint32_t coff = (uint32_t)(row * kWideKS + 16 * ((4 * wave + g) ^ row));
+    const uint32_t coff = KS == 512 ? (uint32_t)(row * KS + 16 * ((4 * wave + g) ^ row))
+                                    : (uint32_t)(row * KS + 16 * ((2 * wave + (g >> 1)) ^ row) + 8 * (g & 1));
     f32x4 acc[NT][MI];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
@@ -891,37 +932,56 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     const float* tab = reinterpret_cast<const float*>(lds + OTAB);
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-        wait_vm<(D - 2) * (NT + XD)>();
+        wait_vm<(D - 2) * (CD + XD)>();
         gemm_fp8::wait_lgkm<0>();  // stage j - 1's LDS reads are in registers
         barrier();
         issue_codes(j + D - 1);
         issue_x(j + D - 1);
-        if (j < nst && kWideKS * j + 64 * wave < K) {
-            u32x4 x0[MI], x1[MI];
-#pragma unroll
-            for (int mi = 0; mi < MI; ++mi) {
-                x0[mi] = *reinterpret_cast<const u32x4*>(lds + xoff[mi] + (j % D) * XSLOT);
-                x1[mi] = *reinterpret_cast<const u32x4*>(lds + xoff[mi] + (j % D) * XSLOT + 16);
-            }
-            const int blk = 4 * j + (wave >> 1);
-#pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const u32x4 cw =
-                    *reinterpret_cast<const u32x4*>(lds + (j % D) * STAGE + t * 16 * kWideKS + coff);
-                const float sc = tab[sidx(16 * t + row) + blk];
-                uint32_t wv[8];
-                dequant4(cw.x, sc, wv[0], wv[1]);
-                dequant4(cw.y, sc, wv[2], wv[3]);
-                dequant4(cw.z, sc, wv[4], wv[5]);
-                dequant4(cw.w, sc, wv[6], wv[7]);
+        if (j < nst && KS * j + KW * wave < K) {
+            const int blk = KS == 512 ? 4 * j + (wave >> 1) : 2 * j + (wave >> 2);
+            if constexpr (KS == 512) {
+                u32x4 x0[MI], x1[MI];
 #pragma unroll
                 for (int mi = 0; mi < MI; ++mi) {
-                    acc[t][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x0[mi]),
-                                                                         as_bf16x8(wv[0], wv[1], wv[2], wv[3]),
-                                                                         acc[t][mi], 0, 0, 0);
-                    acc[t][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1[mi]),
-                                                                         as_bf16x8(wv[4], wv[5], wv[6], wv[7]),
-                                                                         acc[t][mi], 0, 0, 0);
+                    x0[mi] = *reinterpret_cast<const u32x4*>(lds + xoff[mi] + (j % D) * XSLOT);
+                    x1[mi] = *reinterpret_cast<const u32x4*>(lds + xoff[mi] + (j % D) * XSLOT + 16);
+                }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const u32x4 cw = *reinterpret_cast<const u32x4*>(lds + (j % D) * STAGE + t * 16 * KS + coff);
+                    const float sc = tab[sidx(16 * t + row) + blk];
+                    uint32_t wv[8];
+                    dequant4(cw.x, sc, wv[0], wv[1]);
+                    dequant4(cw.y, sc, wv[2], wv[3]);
+                    dequant4(cw.z, sc, wv[4], wv[5]);
+                    dequant4(cw.w, sc, wv[6], wv[7]);
+#pragma unroll
+                    for (int mi = 0; mi < MI; ++mi) {
+                        acc[t][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x0[mi]),
+                                                                             as_bf16x8(wv[0], wv[1], wv[2], wv[3]),
+                                                                             acc[t][mi], 0, 0, 0);
+                        acc[t][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x1[mi]),
+                                                                             as_bf16x8(wv[4], wv[5], wv[6], wv[7]),
+                                                                             acc[t][mi], 0, 0, 0);
+                    }
+                }
+            } else {
+                u32x4 x0[MI];
+#pragma unroll
+                for (int mi = 0; mi < MI; ++mi)
+                    x0[mi] = *reinterpret_cast<const u32x4*>(lds + xoff[mi] + (j % D) * XSLOT);
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const uint2 cw = *reinterpret_cast<const uint2*>(lds + (j % D) * STAGE + t * 16 * KS + coff);
+                    const float sc = tab[sidx(16 * t + row) + blk];
+                    uint32_t wv[4];
+                    dequant4(cw.x, sc, wv[0], wv[1]);
+                    dequant4(cw.y, sc, wv[2], wv[3]);
+#pragma unroll
+                    for (int mi = 0; mi < MI; ++mi)
+                        acc[t][mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, x0[mi]),
+                                                                             as_bf16x8(wv[0], wv[1], wv[2], wv[3]),
+                                                                             acc[t][mi], 0, 0, 0);
                 }
             }
         }
@@ -959,11 +1019,11 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     }
 }
 
-template <int NS, bool SW, int NT, int MX, int D = kRowD>
+template <int NS, bool SW, int NT, int MX, int D = kRowD, int KS = kWideKS>
 hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                            int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
-    auto kern = small_m_row_wide_kernel<NS, SW, NT, MX, D>;
-    constexpr int lds = wide_lds<NT, MX, D>();
+    auto kern = small_m_row_wide_kernel<NS, SW, NT, MX, D, KS>;
+    constexpr int lds = wide_lds<NT, MX, D, KS>();
     static_assert(lds <= kMaxLds, "row-staged LDS");
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -996,9 +1056,15 @@ hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float*
 // against 13.2 / 14.1, 5120 x 5120 11.0 / 11.9 against 12.0 / 13.1, 2048 x
 // 5120 8.1 / 9.4 against 10.9 / 11.9, 3072 x 8704 12.1 / 14.3 against 16.2 /
 // 17.2, 6144 x 9216 16.5 / 18.2 against 18.5 / 20.2, 6144 x 4096 10.3 / 10.9
-// against 10.8 / 11.7.  The choice depends on the weight geometry and on the
-// row count's range (1..8, 9..16, 17..32) only, the same for the plain and
-// the SwiGLU form.
+// against 10.8 / 11.7.  With 256-byte stages (half the ring and activation
+// slots) it also takes 5 tiles at 9..16 rows and 3..5 at 17..32, at K =
+// 4224..5120 (M = 9 / 16 / 17 / 32, against the row-range kernel): gate/up
+// 19.5 / 19.4 / 21.5 / 21.9 us against 20.2 / 21.4 / 22.8 / 26.6, 8240 x 5120
+// 13.9 / 15.2 us at M = 17 / 32 against 16.6 / 20.1, 12288 x 5120 15.4 /
+// 17.2 against 18.6 / 22.6.  At K = 4096 the row-range kernel stays (17408 x
+// 4096 16.2 against 21.1 us at M = 9 in that form).  The choice depends on
+// the weight geometry and on the row count's range (1..8, 9..16, 17..32)
+// only, the same for the plain and the SwiGLU form.
 int row_wide_tiles(int M, int N, int K, bool swiglu, int& groups) {
     const int cus = compute_units();
     const int units = swiglu ? N / 2 : N;
@@ -1008,8 +1074,13 @@ int row_wide_tiles(int M, int N, int K, bool swiglu, int& groups) {
     groups = std::min(cus, units);
     const int per = (units + groups - 1) / groups;
     const int t = swiglu ? (per + 7) / 8 : (per + 15) / 16;
-    if (M > 16) return t >= 1 && t <= 2 ? t : 0;
-    if (M > kRowMaxM) return t >= 1 && t <= (K > kWideMaxK ? 2 : 4) ? t : 0;
+    if (M > kRowMaxM) {
+        // 512-byte stages hold 4 tiles at 9..16 rows, 2 at 17..32; more (the
+        // 256-byte stages) only at K = 4224..5120
+        if (K > kWideMaxK) return t >= 1 && t <= 2 ? t : 0;
+        if (t <= (M > 16 ? 2 : 4)) return t >= 1 ? t : 0;
+        return K > 4096 && t <= 5 ? t : 0;
+    }
     if (K > kWideMaxK) return t >= 1 && t <= 2 ? t : 0;
     if (K <= 4096 && stream_nb(K) != 0 && rows_per_cu > 40) return 0;
     return t >= 1 && t <= 5 ? t : 0;
@@ -1127,6 +1198,13 @@ namespace {
 // with two tiles a fourth stage was 2-5% slower, a fifth 5-8%; with 32
 // staged activation rows a one-tile ring stays at 3 stages, 122 KiB).
 template <bool SW, int NT, int MX>
+hipError_t dispatch_row_wide_half(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
+                                  int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
+    if (K <= 4096) return launch_row_wide<16, SW, NT, MX, kRowD, 256>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    return launch_row_wide<20, SW, NT, MX, kRowD, 256>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+}
+
+template <bool SW, int NT, int MX>
 hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
     constexpr int D = NT == 1 && MX < 32 ? 4 : kRowD;
@@ -1142,9 +1220,13 @@ hipError_t dispatch_row_wide(int nt, const uint16_t* x, const uint8_t* codes, co
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
     if (M > 16) {
         if (nt == 1) return dispatch_row_wide<SW, 1, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
-        return dispatch_row_wide<SW, 2, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        if (nt == 2) return dispatch_row_wide<SW, 2, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        if (nt == 3) return dispatch_row_wide_half<SW, 3, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        if (nt == 4) return dispatch_row_wide_half<SW, 4, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        return dispatch_row_wide_half<SW, 5, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     }
     if (M > kRowMaxM) {
+        if (nt == 5) return dispatch_row_wide_half<SW, 5, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
         if (nt == 1) return dispatch_row_wide<SW, 1, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
         if (nt == 2) return dispatch_row_wide<SW, 2, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);
         if (nt == 3) return dispatch_row_wide<SW, 3, 16>(x, codes, scales, y, ldy, M, N, K, groups, stream);

@@ -798,8 +798,8 @@ def test_small_m_row_wide(fp8lin, gpu, oracle, m, n, k):
                                    (11, 1100, 8704), (14, 6000, 640)])
 def test_small_m_row_wide_16_rows(fp8lin, gpu, oracle, m, n, k):
     """The wide row-staged form with 16 staged activation rows (fp8_linear at
-    9..16 rows): 64 rows per workgroup (4 tiles, the maximum; 32 SwiGLU
-    pairs), 48 rows at K = 4096, a last stage of 128 values (K = 4224), 32
+    9..16 rows): 64 rows per workgroup (4 tiles, the most with 512-byte
+    stages; 32 SwiGLU pairs), 48 rows at K = 4096, a last stage of 128 values (K = 4224), 32
     rows at K = 9216 (18 stages, the longest), one tile at K = 8704 and a
     short K.  Every output against the FP64 oracle; the first 9 rows those of
     a 9-row call (the summation depends on K only); the fused SwiGLU
@@ -848,6 +848,38 @@ def test_small_m_row_wide_32_rows(fp8lin, gpu, oracle, m, n, k):
     xz = xg.clone()
     xz[16:] = 0
     assert torch.equal(fp8lin.fp8_linear(xz, c, s, True)[:16], y[:16])
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 17408, 5120), (9, 20000, 4224), (32, 17408, 5120), (17, 12288, 5120),
+                                   (24, 16000, 4608), (32, 8240, 5120)])
+def test_small_m_row_wide_half_stages(fp8lin, gpu, oracle, m, n, k):
+    """The wide row-staged form with 256-byte stages (fp8_linear at 9..16
+    rows with 5 tiles per workgroup, at 17..32 rows with 3..5, K =
+    4224..5120): 80 rows per workgroup at 16 and at 32 staged rows (gate/up),
+    a last stage of 128 values (K = 4224), 48 and 64 rows per workgroup, and
+    33 rows (in_proj_all: the third tile holds one row).  Every output
+    against the FP64 oracle; the first 9 (17) rows those of a 9-row (17-row)
+    call; at 17..32 rows, rows 16.. changing none of the first 16 outputs;
+    the fused SwiGLU bit-equal to fused_swiglu(fp8_linear) and within 1 ulp
+    of the oracle SwiGLU of the same sums."""
+    rng = np.random.default_rng(m * 7901 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"row-wide half stages {m}x{n}x{k}")
+    first = 17 if m > 17 else 9 if 9 < m <= 16 else 0
+    if first:
+        assert torch.equal(fp8lin.fp8_linear(xg[:first].contiguous(), c, s, True), y[:first])
+    if m > 16:
+        xz = xg.clone()
+        xz[16:] = 0
+        assert torch.equal(fp8lin.fp8_linear(xz, c, s, True)[:16], y[:16])
     fused = fp8lin.linear_swiglu(xg, c, s, split=False)
     assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
     assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
