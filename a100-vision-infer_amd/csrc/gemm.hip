@@ -148,11 +148,14 @@ hipError_t launch_skinny(const uint16_t* x, const void* w, const float* scales, 
 // padding.  17..32 rows in the wide row-staged form with 32 staged
 // activation rows (up to 32 weight rows per CU), else in the row-range form
 // with two activation tiles (K <= 5120) or the K-split 16-row tiles with two
-// activation tiles.  Its geometry limits are those of the decode routing
-// (block scales [N, K/128], 16-byte aligned x and codes).
+// activation tiles.  33..64 rows where the row-staged form holds them (64
+// staged rows in 256-byte stages, up to 32 weight rows per CU), else the
+// GEMM.  Its geometry limits are those of the decode routing (block scales
+// [N, K/128], 16-byte aligned x and codes).
 bool mid_rows(const uint16_t* x, const void* w, int S, int64_t M, int64_t N, int64_t K) {
     const int64_t lim = (int64_t)1 << 31;
-    return M > 8 && M <= 32 && N > 1024 && K % 128 == 0 && S == K / 128 &&
+    if (M > 32 && !(M <= 64 && N < lim && K < lim && small_m_wide_rows((int)M, (int)N, (int)K))) return false;
+    return M > 8 && N > 1024 && K % 128 == 0 && S == K / 128 &&
            reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 && 16 * K < lim &&
            N * S * 4 < lim && M * K * 2 < lim;
 }

@@ -53,6 +53,8 @@ bool small_m_candidates_supported(int M, int N, int K);
 // Whether fp8lin_linear runs the small-M kernel at two rows and K <= 5120
 // (where it measured faster than the two-row ring GEMV for this weight).
 bool small_m_two_rows(int N, int K);
+// Whether the row-staged small-M form runs M rows against an N x K weight.
+bool small_m_wide_rows(int M, int N, int K);
 hipError_t launch_small_m_candidates(const uint16_t* x, const uint8_t* codes, const float* scales, int M, int N,
                                      int K, uint32_t* part, int64_t& groups, hipStream_t stream);
 // out[2m] = value, out[2m + 1] = column + offset of the best of the `chunks`

@@ -764,17 +764,18 @@ constexpr int wide_lds() {
     return wide_odump<NT, MX, D, KS>() + (wide_code_dmas<NT, KS>() * kWideWaves * 1024 > wide_stage<NT, KS>() ? 1024 : 0);
 }
 static_assert(wide_lds<5, 8>() <= kMaxLds && wide_lds<4, 16>() <= kMaxLds && wide_lds<2, 32>() <= kMaxLds &&
-                  wide_lds<5, 32, kRowD, 256>() <= kMaxLds,
+                  wide_lds<5, 32, kRowD, 256>() <= kMaxLds && wide_lds<2, 64, kRowD, 256>() <= kMaxLds,
               "wide row-staged LDS");
 
 // Requirements (checked by the host): 1 <= M <= MX (8; 16 with NT <= 4; 32
-// with NT <= 2; with KS = 256, 16 or 32 with NT <= 5), K % 128 == 0,
+// with NT <= 2; with KS = 256, 16 or 32 with NT <= 5, 64 with NT <= 2), K % 128 == 0,
 // K <= KS NS <= 5120 (9216 with NT <= 2), at most 16 NT rows (8 NT pairs) per
 // workgroup, N * K < 2^31.  MX = 16 stages 16 activation rows (two DMAs per
 // wave and stage at KS = 512: rows w and w + 8); the MFMA tile is the same.
-// MX = 32 stages 32 and runs two activation tiles, rows 0..15 and 16..31:
-// each converted code word feeds the MFMAs of both, each with its own
-// accumulator, so a row's sums do not depend on the other tile.
+// MX = 32 stages 32 and runs two activation tiles, rows 0..15 and 16..31
+// (MX = 64, at KS = 256 only: four): each converted code word feeds the
+// MFMAs of every activation tile, each with its own accumulator, so a row's
+// sums do not depend on the other tiles.
 //
 // KS is the stage's K bytes per row.  KS = 512: wave w owns K [512 s + 64 w,
 // +64) of stage s, a lane 16 codes, two MFMAs per tile.  KS = 256 (half the
@@ -800,12 +801,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void small_m_row_wide_kernel(const
     constexpr int CD = wide_code_dmas<NT, KS>(); // code DMAs per wave
     constexpr int CPR = KS / 16;                 // 16-byte chunks of a row's stage
     constexpr int KW = KS / 8;                   // K of a wave per stage
-    constexpr int MI = MX == 32 ? 2 : 1;         // activation tiles
+    constexpr int MI = MX >= 16 ? MX / 16 : 1;   // activation tiles
     constexpr bool DUMP = CD * W * 1024 > STAGE;  // the last code DMAs run past the stage
     static_assert(KS == 512 || KS == 256, "512- or 256-byte stages");
     static_assert(D >= 3, "at least two stages in flight");
-    static_assert(MX == 8 || MX == 16 || MX == 32, "8, 16 or 32 activation rows");
-    static_assert(KS == 512 || MX >= 16, "256-byte stages stage 16 or 32 activation rows");
+    static_assert(MX == 8 || MX == 16 || MX == 32 || MX == 64, "8, 16, 32 or 64 activation rows");
+    static_assert(KS == 512 ? MX <= 32 : MX >= 16, "512-byte stages stage 8..32 rows, 256-byte 16..64");
     static_assert(W * NT * MI * 256 * 4 <= OTAB, "partial sums fit below the scale table");
     static_assert(16 * NT * (NS * KS / 128) * 4 <= kWideTable, "the scale table holds the tiles' rows");
     extern __shared__ __align__(16) uint8_t lds[];
@@ -1068,12 +1069,13 @@ hipError_t launch_row_wide(const uint16_t* x, const uint8_t* codes, const float*
 int row_wide_tiles(int M, int N, int K, bool swiglu, int& groups) {
     const int cus = compute_units();
     const int units = swiglu ? N / 2 : N;
-    if (M < 1 || M > 32 || K % 128 != 0 || K > 9216 || units < 1 || (int64_t)N * K >= ((int64_t)1 << 31))
+    if (M < 1 || M > 64 || K % 128 != 0 || K > 9216 || units < 1 || (int64_t)N * K >= ((int64_t)1 << 31))
         return 0;
     const int rows_per_cu = (N + cus - 1) / cus;
     groups = std::min(cus, units);
     const int per = (units + groups - 1) / groups;
     const int t = swiglu ? (per + 7) / 8 : (per + 15) / 16;
+    if (M > 32) return t >= 1 && t <= 2 ? t : 0;  // 64 staged rows in 256-byte stages
     if (M > kRowMaxM) {
         // 512-byte stages hold 4 tiles at 9..16 rows, 2 at 17..32; more (the
         // 256-byte stages) only at K = 4224..5120
@@ -1174,6 +1176,11 @@ hipError_t dispatch_stream(int nb, const uint16_t* x, const uint8_t* codes, cons
 // 8192 x 5120 9.5 against 10.0, 8240 x 5120 10.4 against 10.6).  Fewer rows
 // per CU (5120 x 5120 8.0 against 7.8, 2048 x 5120 6.5 against 5.1) and the
 // 68 of gate/up (18.1 against 17.8) keep the GEMV.
+bool small_m_wide_rows(int M, int N, int K) {
+    int groups = 0;
+    return row_wide_tiles(M, N, K, false, groups) != 0;
+}
+
 bool small_m_two_rows(int N, int K) {
     if (small_m_candidates_supported(2, N, K)) return true;
     const int cus = compute_units();
@@ -1201,6 +1208,9 @@ template <bool SW, int NT, int MX>
 hipError_t dispatch_row_wide_half(const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                                   int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
     if (K <= 4096) return launch_row_wide<16, SW, NT, MX, kRowD, 256>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    if constexpr (NT <= 2)
+        if (K > kWideMaxK)
+            return launch_row_wide<36, SW, NT, MX, kRowD, 256>(x, codes, scales, y, ldy, M, N, K, groups, stream);
     return launch_row_wide<20, SW, NT, MX, kRowD, 256>(x, codes, scales, y, ldy, M, N, K, groups, stream);
 }
 
@@ -1218,6 +1228,10 @@ hipError_t dispatch_row_wide(const uint16_t* x, const uint8_t* codes, const floa
 template <bool SW>
 hipError_t dispatch_row_wide(int nt, const uint16_t* x, const uint8_t* codes, const float* scales, uint16_t* y,
                              int64_t ldy, int M, int N, int K, int groups, hipStream_t stream) {
+    if (M > 32) {
+        if (nt == 1) return dispatch_row_wide_half<SW, 1, 64>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+        return dispatch_row_wide_half<SW, 2, 64>(x, codes, scales, y, ldy, M, N, K, groups, stream);
+    }
     if (M > 16) {
         if (nt == 1) return dispatch_row_wide<SW, 1, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
         if (nt == 2) return dispatch_row_wide<SW, 2, 32>(x, codes, scales, y, ldy, M, N, K, groups, stream);
@@ -1260,6 +1274,7 @@ hipError_t launch_small_m(const uint16_t* x, const uint8_t* codes, const float* 
         if (swiglu) return dispatch_row_wide<true>(nt, x, codes, scales, y, ldy, M, N, K, wide_groups, stream);
         return dispatch_row_wide<false>(nt, x, codes, scales, y, ldy, M, N, K, wide_groups, stream);
     }
+    if (M > 32) return hipErrorNotSupported;  // only the row-staged form stages 33..64 rows
     if (stream_form(M, N, K, nb, per_rows)) {
         if (swiglu)
             return dispatch_stream<true, false>(nb, x, codes, scales, y, ldy, M, N, K, (N / 2 + cus - 1) / cus,

@@ -93,8 +93,9 @@ int fp8lin_decode(const uint8_t* codes, const float* scales, int64_t scale_cols,
  * tests/optimized_test.cpp:57-62); M > 8 runs the MFMA GEMM that dequantizes
  * FP8 tiles to BF16 (128-row tiles for M <= 128, 256-row tiles above), except
  * that 9..16 rows under the same conditions as the 3..8-row case run the
- * small-M matrix-core kernel too (its 16-row MFMA tile holds them all), and
- * 17..32 rows (two such tiles).
+ * small-M matrix-core kernel too (its 16-row MFMA tile holds them all),
+ * 17..32 rows (two such tiles), and 33..64 rows on weights of at most 32
+ * rows per compute unit (four such tiles; no split-K workspace needed).
  * Requires M, N, K > 0 and scale_cols in {1, ceil(K/128)}.
  */
 int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales,

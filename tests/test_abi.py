@@ -332,7 +332,7 @@ def splitk_plan_bytes(m, n, k, cus=256):
     return split * s * bm * 256 * 4 if s > 1 else 0
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 7168, 5120), (512, 5120, 8704), (64, 5120, 8704), (1024, 17408, 5120),
+@pytest.mark.parametrize("m,n,k", [(512, 7168, 5120), (512, 5120, 8704), (64, 17408, 5120), (1024, 17408, 5120),
                                    (4096, 17408, 5120), (512, 17408, 5120), (512, 75968, 5120)])
 def test_linear_workspace_bytes(fp8lin, m, n, k):
     """fp8lin_linear_ws's partials follow the engine branch's split plan (no
@@ -342,10 +342,11 @@ def test_linear_workspace_bytes(fp8lin, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 7168, 5120), (8, 5120, 8704), (16, 5120, 8704), (32, 7168, 5120),
-                                   (512, 48, 5120), (0, 16, 16), (512, 7168, 0)])
+                                   (64, 5120, 8704), (48, 7168, 5120), (512, 48, 5120), (0, 16, 16), (512, 7168, 0)])
 def test_linear_workspace_bytes_none(fp8lin, m, n, k):
     """No partials where fp8_linear runs no GEMM tile (the decode GEMV, the
-    small-M kernel for 9..32 rows, the skinny kernel) or on empty shapes."""
+    small-M kernel for 9..32 rows and for 33..64 on weights of up to 32 rows
+    per CU, the skinny kernel) or on empty shapes."""
     assert fp8lin.lib().fp8lin_linear_workspace_bytes(m, n, k) == 0
 
 

@@ -323,11 +323,12 @@ def _bits(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("m,n,k", [(512, 7168, 5120), (512, 5120, 8704), (64, 5120, 8704)])
+@pytest.mark.parametrize("m,n,k", [(512, 7168, 5120), (512, 5120, 8704), (64, 17408, 5120)])
 def test_shim_fp8_linear_split_k(avi, fp8lin, gpu, oracle, m, n, k):
     """avi::fp8_linear on the prefill projections whose GEMM tiles leave CUs
-    idle (the QKV-gate and down projections at a 512-row chunk, down at a
-    64-row chunk tail) splits K through its own workspace, as the engine
+    idle (the QKV-gate and down projections at a 512-row chunk, the gate/up
+    rows at a 64-row chunk tail; down at 64 rows runs the small-M kernel and
+    needs none) splits K through its own workspace, as the engine
     branch does (src/engine.cpp:222-224): at the parity bar against the FP64
     oracle on the last 600 columns, equal to the Python mirror's call bit for
     bit, and within the split-order bar of the unsplit call everywhere."""

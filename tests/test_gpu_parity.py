@@ -885,6 +885,38 @@ def test_small_m_row_wide_half_stages(fp8lin, gpu, oracle, m, n, k):
     assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
 
 
+@pytest.mark.parametrize("m,n,k", [(64, 5120, 8704), (48, 7168, 5120), (33, 2048, 5120), (64, 6144, 4096),
+                                   (40, 3100, 9216), (57, 4100, 4224), (64, 8190, 640)])
+def test_small_m_row_wide_64_rows(fp8lin, gpu, oracle, m, n, k):
+    """fp8_linear at 33..64 rows on weights of up to 32 rows per CU: the
+    row-staged form with 64 staged activation rows in 256-byte stages (four
+    activation tiles) instead of the GEMM: two tiles at K = 8704 (34 stages)
+    and at K = 5120 and 4096, one tile at K = 5120 and at K = 9216 (the
+    longest), a last stage of 128 values (K = 4224) and a short K.  Every
+    output against the FP64 oracle; the first 33 rows those of a 33-row
+    call, and rows 16.. changing none of the first 16 outputs; the fused
+    SwiGLU bit-equal to fused_swiglu(fp8_linear) and within 1 ulp of the
+    oracle SwiGLU of the same sums; no split-K workspace asked for."""
+    rng = np.random.default_rng(m * 7883 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"row-wide 64 {m}x{n}x{k}")
+    if m > 33:
+        assert torch.equal(fp8lin.fp8_linear(xg[:33].contiguous(), c, s, True), y[:33])
+    xz = xg.clone()
+    xz[16:] = 0
+    assert torch.equal(fp8lin.fp8_linear(xz, c, s, True)[:16], y[:16])
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert torch.equal(fp8lin.linear_swiglu(xg, c, s), fused)
+    assert ulp_distance(bits(fused), oracle.swiglu(bits(y))).max() <= 1
+    assert fp8lin.lib().fp8lin_linear_workspace_bytes(m, n, k) == 0
+
+
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
 @pytest.mark.parametrize("m,n,k", [(9, 2056, 384), (16, 2056, 384), (12, 8208, 5120), (16, 8208, 4096),
                                    (13, 1040, 8704), (16, 8240, 8704), (17, 8208, 5120), (32, 8208, 4096),
