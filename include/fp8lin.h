@@ -112,7 +112,7 @@ int fp8lin_linear_ld(const uint16_t* x, const uint8_t* codes, const float* scale
 /* fp8lin_linear with a workspace for the prefill GEMM's K-split partials:
  * when M > 8 and the GEMM's 256x256 (128-row for M <= 128) tiles number
  * fewer than half the CUs (e.g. the 7168-row QKV-gate and 5120-row down
- * projections at M = 512, or the 5120-row down projection at M = 33..128),
+ * projections at M = 512, or the 5120-row down projection at M = 65..128),
  * or leave a last round on at most half of them, those tiles are cut into
  * K ranges and a second launch adds their FP32 sums in order and rounds
  * once.  Within the parity bar of fp8lin_linear (only the FP32 summation
