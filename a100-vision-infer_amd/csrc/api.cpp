@@ -685,6 +685,23 @@ int fp8lin_engine_linear_groups(const fp8lin_linear_options* options, const fp8l
         require(ldy >= total, FP8LIN_ERR_SHAPE, "Engine linear groups: ldy < sum of group N");
         for (int g = 0; g < ngroups; ++g) validate_engine(*options, groups[g], x, rows, y, ldy);
         ensure_device();
+        // An FP8 weight then a BF16 weight at one row, both on the ring GEMV
+        // (the GDN in_proj_all group): one launch, the same bits.
+        if (ngroups == 2 && rows == 1) {
+            const fp8lin_weight& a = groups[0];
+            const fp8lin_weight& b = groups[1];
+            if (engine_path(*options, a, rows) == FP8LIN_PATH_FP8_GEMV &&
+                engine_path(*options, b, rows) == FP8LIN_PATH_BF16 && !a.bias && !b.bias && a.K % 16 == 0 &&
+                aligned16(x) && aligned16(a.data) && aligned16(b.data)) {
+                const hipError_t e = fp8lin::launch_gemv_pair(
+                    x, static_cast<const uint8_t*>(a.data), a.scales, (int)a.scale_cols, y, (int)a.N,
+                    static_cast<const uint16_t*>(b.data), y + a.N, (int)b.N, ldy, (int)a.K, as_stream(stream));
+                if (e != hipErrorNotSupported) {
+                    check_hip(e, "gemv pair launch");
+                    return;
+                }
+            }
+        }
         int64_t offset = 0;
         for (int g = 0; g < ngroups; ++g) {
             engine_impl(*options, groups[g], x, rows, y + offset, ldy, workspace, workspace_bytes,

@@ -168,6 +168,28 @@ hipError_t launch_gemv(const uint16_t* x, const void* w, bool fp8, const float* 
     return dispatch<false, false>(x, w, nullptr, 1, y, ldy, M, N, K, wide, stream);
 }
 
+// The FP8 weight (kFewRows < na < kSharedXRows rows: the ring kernel's
+// two-row, two-wave form) and the BF16 weight (nb <= kFewRows rows: one row
+// per wave) of one activation row, K <= 5120, 128-bit operands, in one launch
+// (gemv_ring_pair_kernel); hipErrorNotSupported outside that.
+hipError_t launch_gemv_pair(const uint16_t* x, const uint8_t* codes, const float* scales, int S, uint16_t* ya,
+                            int na, const uint16_t* wb, uint16_t* yb, int nb, int64_t ldy, int K,
+                            hipStream_t stream) {
+    using namespace gemv;
+    if (!(na > kFewRows && na < kSharedXRows && nb >= 1 && nb <= kFewRows && K >= 16 && K <= 5120 &&
+          K % 16 == 0))
+        return hipErrorNotSupported;
+    const int blocks_a = ((na + 1) / 2 + 1) / 2;
+    const int blocks = blocks_a + (nb + 1) / 2;
+    if (K <= 4096)
+        hipLaunchKernelGGL((gemv_ring_pair_kernel<4, kNT>), dim3((unsigned)blocks), dim3(128), 0, stream, x, codes,
+                           scales, S, ya, na, wb, yb, nb, ldy, K, blocks_a);
+    else
+        hipLaunchKernelGGL((gemv_ring_pair_kernel<5, kNT>), dim3((unsigned)blocks), dim3(128), 0, stream, x, codes,
+                           scales, S, ya, na, wb, yb, nb, ldy, K, blocks_a);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemv_swiglu(const uint16_t* x, const uint8_t* codes, const float* scales, int S,
                               uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
                               hipStream_t stream) {

@@ -485,6 +485,39 @@ __global__ __launch_bounds__(64 * WPG) void gemv_ring_kernel(
     if (lane == 0) store_group<R, MR, SWIGLU>(y, ldy, M, rows, row_ok, acc);
 }
 
+// Two weights at one activation row in one launch: workgroups [0, blocks_a)
+// run the FP8 weight's ring groups (two rows per wave, two waves), the rest
+// the BF16 weight's rows (one per wave) -- the GDN in_proj_all group's 8192
+// FP8 and 48 BF16 rows, whose second launch would pay its own ramp.  Each
+// part's rows are summed exactly as in its own launch (a wave owns its rows,
+// activations are not shared through LDS in either), so the outputs are
+// those of the two launches bit for bit.
+template <int MAXSTEPS, int AUX>
+__global__ __launch_bounds__(128) void gemv_ring_pair_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ wa, const float* __restrict__ sa, int sa_cols,
+    uint16_t* __restrict__ ya, int na, const uint16_t* __restrict__ wb, uint16_t* __restrict__ yb, int nb,
+    int64_t ldy, int K, int blocks_a) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    if ((int)blockIdx.x < blocks_a) {
+        const int64_t g = (int64_t)blockIdx.x * 2 + wave;
+        const Buffers b = make_buffers(x, wa, sa, sa_cols, 1, na, K, true);
+        int64_t rows[2];
+        bool row_ok[2];
+        float acc[2][1];
+        ring_group<1, 2, MAXSTEPS, true, false, AUX, 2, false>(b, sa_cols, 1, na, K, g, lane, rows, row_ok, acc);
+        if (lane == 0) store_group<2, 1, false>(ya, ldy, 1, rows, row_ok, acc);
+    } else {
+        const int64_t g = (int64_t)(blockIdx.x - blocks_a) * 2 + wave;
+        const Buffers b = make_buffers(x, wb, nullptr, 1, 1, nb, K, false);
+        int64_t rows[1];
+        bool row_ok[1];
+        float acc[1][1];
+        ring_group<1, 1, MAXSTEPS, false, false, AUX, 2, false>(b, 1, 1, nb, K, g, lane, rows, row_ok, acc);
+        if (lane == 0) store_group<1, 1, false>(yb, ldy, 1, rows, row_ok, acc);
+    }
+}
+
 // The ring kernel with the output head's candidate epilogue: no logits are
 // written.  Each workgroup rounds its rows' totals to BF16 (the logits
 // fp8lin_linear would store) and writes, per activation row m, the best

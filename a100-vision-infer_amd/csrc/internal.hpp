@@ -8,6 +8,9 @@ namespace fp8lin {
 
 // Decode GEMV, 1 <= M <= 8 (gemv.hip).  `w` is E4M3FN codes when fp8, else
 // BF16.  `wide` selects 128-bit loads (caller checked alignment and K % 16).
+hipError_t launch_gemv_pair(const uint16_t* x, const uint8_t* codes, const float* scales, int S, uint16_t* ya,
+                            int na, const uint16_t* wb, uint16_t* yb, int nb, int64_t ldy, int K,
+                            hipStream_t stream);
 hipError_t launch_gemv(const uint16_t* x, const void* w, bool fp8, const float* scales, int S,
                        uint16_t* y, int64_t ldy, int M, int N, int K, bool wide,
                        hipStream_t stream);

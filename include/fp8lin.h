@@ -271,7 +271,10 @@ int fp8lin_engine_linear(const fp8lin_linear_options* options, const fp8lin_weig
                          fp8lin_stream_t stream);
 /* Mixed projection groups (src/engine.cpp:198-199, fuse_weights :147-177):
  * each group's output is written to consecutive column slices of y, in
- * order, exactly like at::cat(parts, -1). */
+ * order, exactly like at::cat(parts, -1).  Two groups at one row that both
+ * take the decode GEMV (an FP8 weight of 1025..16383 rows, then a BF16 weight
+ * of at most 1024, K <= 5120, no bias: the GDN in_proj_all group) run in one
+ * launch, with the bits of the two groups' own calls. */
 int fp8lin_engine_linear_groups(const fp8lin_linear_options* options,
                                 const fp8lin_weight* groups, int ngroups,
                                 const uint16_t* x, int64_t rows, uint16_t* y, int64_t ldy,

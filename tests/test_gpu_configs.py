@@ -175,6 +175,34 @@ def test_gdn_in_proj_all(fp8lin, gpu, oracle, m):
     assert_parity(y[sample], ref, f"in_proj_all M={m}")
     if m == 4:
         assert eng.cache_stats()["fp8_tensor_calls"] == 1
+    if m == 1:
+        # one launch for both groups (the FP8 ring GEMV's rows, then the BF16
+        # rows): the bits of the two groups' own calls
+        sep = np.concatenate([bits(eng.linear(x, f"l.in_proj_all.group{i}")) for i in (0, 1)], axis=1)
+        assert np.array_equal(y, sep)
+
+
+@pytest.mark.parametrize("na,nb,k", [(2049, 7, 4096), (1025, 1, 2304), (16383, 1024, 5120), (3000, 48, 128)])
+def test_fp8_bf16_pair_one_row(fp8lin, gpu, oracle, na, nb, k):
+    """An FP8 weight and a BF16 weight in one group call at one activation
+    row run in one launch (odd row counts, the row limits of both parts,
+    K = 4096's four steps and a one-step K): every output against the oracle
+    and bit-equal to each weight's own call."""
+    F = fp8lin
+    eng = F.LinearEngine()
+    codes, scales, c_np, s_np = weights(F, gpu, na, k, tag=40)
+    eng.add("l.a.weight", codes, scales)
+    wb = (F.gen_activations(nb, k, seed=2, tag=41, device=gpu).float() * 0.02).to(torch.bfloat16).contiguous()
+    eng.add("l.b.weight", wb)
+    eng.fuse_weights("l.ab", ["l.a", "l.b"])
+    assert eng.mixed_projections["l.ab"] == ["l.a", "l.b"]
+    x = F.gen_activations(1, k, seed=0, tag=42, device=gpu)
+    y = bits(eng.linear(x, "l.ab"))
+    xb = bits(x)
+    ref = np.concatenate([oracle.linear(xb, c_np, s_np), oracle.linear_bf16w(xb, bits(wb))], axis=1)
+    assert_parity(y, ref, f"pair {na}+{nb} K={k}")
+    sep = np.concatenate([bits(eng.linear(x, "l.a")), bits(eng.linear(x, "l.b"))], axis=1)
+    assert np.array_equal(y, sep)
 
 
 def test_split_k_into_unaligned_column_slice(fp8lin, gpu, oracle):
