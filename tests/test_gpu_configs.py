@@ -175,11 +175,46 @@ def test_gdn_in_proj_all(fp8lin, gpu, oracle, m):
     assert_parity(y[sample], ref, f"in_proj_all M={m}")
     if m == 4:
         assert eng.cache_stats()["fp8_tensor_calls"] == 1
-    if m == 1:
-        # one launch for both groups (the FP8 ring GEMV's rows, then the BF16
-        # rows): the bits of the two groups' own calls
-        sep = np.concatenate([bits(eng.linear(x, f"l.in_proj_all.group{i}")) for i in (0, 1)], axis=1)
-        assert np.array_equal(y, sep)
+    # M = 1: one launch for both groups (the FP8 ring GEMV's rows, then the
+    # BF16 rows); more rows: one launch per group.  Either way the bits of the
+    # groups' own calls.
+    sep = np.concatenate([bits(eng.linear(x, f"l.in_proj_all.group{i}")) for i in (0, 1)], axis=1)
+    assert np.array_equal(y, sep)
+
+
+@pytest.mark.parametrize("m", [4, 300])
+def test_mixed_group_under_capture(fp8lin, gpu, m):
+    """A mixed FP8 + BF16 group at several rows captured in a HIP graph:
+    every replay (with eager calls of other sizes on the capture stream and
+    on the default stream in between) equals the eager call."""
+    F, k = fp8lin, 5120
+    eng = F.LinearEngine()
+    codes, scales, _, _ = weights(F, gpu, 8192, k, tag=50)
+    eng.add("l.q.weight", codes, scales)
+    w = (F.gen_activations(48, k, seed=1, tag=51, device=gpu).float() * 0.02).to(torch.bfloat16).contiguous()
+    eng.add("l.b.weight", w)
+    eng.fuse_weights("l.g", ["l.q", "l.b"])
+    x = F.gen_activations(m, k, seed=0, tag=52, device=gpu)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        eng.linear(x, "l.g")
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            out = eng.linear(x, "l.g")
+    for i in range(3):
+        x.copy_(F.gen_activations(m, k, seed=0, tag=60 + i, device=gpu))
+        other = F.gen_activations(m + 3, k, seed=0, tag=70 + i, device=gpu)
+        with torch.cuda.stream(stream):
+            eng.linear(other, "l.g")
+        eng.linear(other, "l.g")
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = eng.linear(x, "l.g")
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
 
 
 @pytest.mark.parametrize("na,nb,k", [(2049, 7, 4096), (1025, 1, 2304), (16383, 1024, 5120), (3000, 48, 128)])
