@@ -1,4 +1,4 @@
-// Small-M (2..16 activation rows) block-FP8 linear on the matrix cores.
+// Small-M (2..64 activation rows) block-FP8 linear on the matrix cores.
 //
 // Contract of fp8_tensor_small (src/fp8_tensor.cu:18-71): K % 128 == 0, block
 // scales [N, K/128], each weight is decoded to BF16 with the reference
@@ -42,8 +42,11 @@
 //
 // Most decode shapes run small_m_row_wide_kernel, the row-staged form: one
 // workgroup per compute unit streams its rows (up to 80 at M <= 8, 64 at
-// 9..16 rows; 32 when K > 5120) 512 bytes of each row per stage, with the
-// activations staged beside the codes (see that kernel).
+// 9..16 rows, 32 at 17..64; 32 when K > 5120) 512 bytes of each row per
+// stage, with the activations staged beside the codes (8, 16 or 32 rows per
+// stage; 256 bytes per stage where 512 would not fit the LDS: 80 rows at
+// 9..32 rows and K = 4224..5120, and 64 staged rows at 33..64; see that
+// kernel).
 //
 // Every kernel here DMAs the weight codes, which one launch reads once, with
 // the non-temporal cache policy (dma16_nt): 10-15% more bytes per second
