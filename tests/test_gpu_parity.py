@@ -917,6 +917,36 @@ def test_small_m_row_wide_64_rows(fp8lin, gpu, oracle, m, n, k):
     assert fp8lin.lib().fp8lin_linear_workspace_bytes(m, n, k) == 0
 
 
+def _mid_rows_sweep_cases(count=14, seed=2027):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < count:
+        m = int(rng.integers(9, 65))
+        n = 2 * int(rng.integers(520, 4200))
+        k = 128 * int(rng.integers(1, 41))
+        cases.append((m, n, k))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k", _mid_rows_sweep_cases())
+def test_mid_rows_random_sweep(fp8lin, gpu, oracle, m, n, k):
+    """Seeded random shapes over fp8_linear's 9..64-row routing (the
+    row-staged form with 16, 32 or 64 staged rows in 512- or 256-byte
+    stages, the row-range and K-split forms, or the GEMM where none holds
+    the rows): every output against the FP64 oracle, and the fused SwiGLU
+    bit-equal to fused_swiglu(fp8_linear) on the same weight."""
+    rng = np.random.default_rng(m * 131 + n * 7 + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True, split=False)
+    assert_parity(bits(y), ref, f"sweep {m}x{n}x{k}")
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+
+
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
 @pytest.mark.parametrize("m,n,k", [(9, 2056, 384), (16, 2056, 384), (12, 8208, 5120), (16, 8208, 4096),
                                    (13, 1040, 8704), (16, 8240, 8704), (17, 8208, 5120), (32, 8208, 4096),
