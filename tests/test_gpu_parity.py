@@ -947,6 +947,38 @@ def test_mid_rows_random_sweep(fp8lin, gpu, oracle, m, n, k):
     assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
 
 
+def _small_rows_sweep_cases(count=14, seed=2029):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < count:
+        m = int(rng.integers(2, 9))
+        n = 2 * int(rng.integers(520, 10000))
+        k = 128 * int(rng.integers(1, 73))
+        cases.append((m, n, k))
+    return cases
+
+
+@pytest.mark.parametrize("m,n,k", _small_rows_sweep_cases())
+def test_small_rows_random_sweep(fp8lin, gpu, oracle, m, n, k):
+    """Seeded random shapes over fp8_linear's 2..8-row routing (the ring or
+    general GEMV, the row-staged form with 1..5 tiles, the row-range form):
+    every output against the FP64 oracle, the fused SwiGLU bit-equal to
+    fused_swiglu(fp8_linear), and fp8_tensor_small (src/fp8_tensor.cu:53-71)
+    on the same inputs at the parity bar too."""
+    rng = np.random.default_rng(m * 137 + n * 3 + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True)
+    assert_parity(bits(y), ref, f"small sweep {m}x{n}x{k}")
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    t = fp8lin.fp8_tensor_small(xg, c, s, 1)
+    assert_parity(bits(t), ref, f"tensor_small sweep {m}x{n}x{k}")
+
+
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
 @pytest.mark.parametrize("m,n,k", [(9, 2056, 384), (16, 2056, 384), (12, 8208, 5120), (16, 8208, 4096),
                                    (13, 1040, 8704), (16, 8240, 8704), (17, 8208, 5120), (32, 8208, 4096),
