@@ -95,7 +95,9 @@ int fp8lin_decode(const uint8_t* codes, const float* scales, int64_t scale_cols,
  * that 9..16 rows under the same conditions as the 3..8-row case run the
  * small-M matrix-core kernel too (its 16-row MFMA tile holds them all),
  * 17..32 rows (two such tiles), and 33..64 rows on weights of at most 32
- * rows per compute unit (four such tiles; no split-K workspace needed).
+ * rows per compute unit (four such tiles; no split-K workspace needed);
+ * 65..128 rows on such weights run as two row halves of those kernels (each
+ * half the bits of a call of its own rows) instead of whole GEMM tiles.
  * Requires M, N, K > 0 and scale_cols in {1, ceil(K/128)}.
  */
 int fp8lin_linear(const uint16_t* x, const uint8_t* codes, const float* scales,

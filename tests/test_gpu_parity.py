@@ -233,7 +233,7 @@ def test_gemm_fp8(fp8lin, gpu, oracle, m, n, k):
     assert_parity(bits(y), oracle.linear(x, codes, scales), f"gemm {m}x{n}x{k}")
 
 
-@pytest.mark.parametrize("n,k,swiglu", [(520, 512, False), (2056, 1024, False), (1040, 768, True),
+@pytest.mark.parametrize("n,k,swiglu", [(520, 512, False), (8200, 1024, False), (8200, 768, True),
                                         (17408, 5120, True)])
 def test_gemm_tile_heights_agree(fp8lin, gpu, oracle, n, k, swiglu):
     """The FP8 GEMM runs 128-row tiles for M <= 128 and 256-row tiles above.
@@ -241,7 +241,9 @@ def test_gemm_tile_heights_agree(fp8lin, gpu, oracle, n, k, swiglu):
     accumulator position), so an M = 128 call equals rows 0..127 of an
     M = 129 call on the same rows bit for bit; the M = 128 call also holds
     the oracle bar (plain: a column sample, SwiGLU: all outputs of a row
-    sample)."""
+    sample).  The weights have more than 32 rows per CU or at most 1024
+    rows, so M = 128 runs the GEMM (narrow weights of more than 1024 rows
+    run 65..128 rows as two small-M halves without a workspace)."""
     rng = np.random.default_rng(n + k)
     codes = rand_codes(rng, n, k)
     scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
@@ -977,6 +979,30 @@ def test_small_rows_random_sweep(fp8lin, gpu, oracle, m, n, k):
     assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
     t = fp8lin.fp8_tensor_small(xg, c, s, 1)
     assert_parity(bits(t), ref, f"tensor_small sweep {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(65, 5120, 8704), (96, 7168, 5120), (128, 5120, 5120), (101, 2048, 1024)])
+def test_linear_65_128_rows_no_workspace(fp8lin, gpu, oracle, m, n, k):
+    """fp8_linear without a workspace at 65..128 rows on weights of up to 32
+    rows per CU runs the small-M kernels on the two row halves instead of
+    whole GEMM tiles: every output against the FP64 oracle, each half
+    bit-equal to a call of its own rows, the fused SwiGLU bit-equal to
+    fused_swiglu(fp8_linear); with a workspace the split-K GEMM runs, at
+    the bar."""
+    rng = np.random.default_rng(m * 101 + n + k)
+    codes = rand_codes(rng, n, k)
+    scales = (rng.random((n, k // 128)) * .01 + .001).astype(np.float32)
+    x = rand_bf16(rng, (m, k))
+    ref = oracle.linear(x, codes, scales)
+    c, s, xg = up(codes, gpu), up(scales, gpu), up(x, gpu)
+    y = fp8lin.fp8_linear(xg, c, s, True, split=False)
+    assert_parity(bits(y), ref, f"65..128 rows {m}x{n}x{k}")
+    h = m - m // 2
+    assert torch.equal(fp8lin.fp8_linear(xg[:h].contiguous(), c, s, True, split=False), y[:h])
+    assert torch.equal(fp8lin.fp8_linear(xg[h:].contiguous(), c, s, True, split=False), y[h:])
+    fused = fp8lin.linear_swiglu(xg, c, s, split=False)
+    assert torch.equal(fused, fp8lin.fused_swiglu(y)), "fused != fused_swiglu(fp8_linear)"
+    assert_parity(bits(fp8lin.fp8_linear(xg, c, s, True)), ref, f"65..128 rows split {m}x{n}x{k}")
 
 
 # ------------------------------------ fp8_linear at 9..32 rows on the matrix cores
