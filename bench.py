@@ -435,10 +435,11 @@ def secondary(torch, fp8lin, dev, rot, log, sections, prefill_m=(128, 512, 1024,
         del xa, wb
     # The drop-in operator (fp8_linear through fp8lin_linear_ws, as the ATen
     # shim calls it) on the prefill projections whose tiles leave CUs idle,
-    # against the same call without a workspace (every tile whole); graph
-    # replays over the rotation, as the chain section times the engine branch.
+    # against the same call without a workspace (M = 64 and 128: the small-M
+    # kernels; M = 512: every tile whole); graph replays over the rotation, as
+    # the chain section times the engine branch.
     for name, n, k in (SHAPES[1:] if "prefill" in sections else ()):
-        for m in (64, 512):
+        for m in (64, 128, 512):
             x = fp8lin.gen_activations(m, k, seed=0, tag=2, device=dev)
             y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
             need = L.fp8lin_linear_workspace_bytes(m, n, k)
